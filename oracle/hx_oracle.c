@@ -1,0 +1,667 @@
+/*
+ * hx_oracle.c -- TEST INFRASTRUCTURE ONLY.
+ *
+ * CPU restatement of helexa neuron's Qwen3-Next sparse-MoE block, used as the
+ * checker for the HIP library (libhxmoe.so). Only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg may load this library; the product path never
+ * does.
+ *
+ * What it restates (reference paths are relative to the helexa repository):
+ *   - route_scatter            crates/neuron/src/harness/arch/qwen3_5/moe.rs:124-162
+ *       router Linear (moe.rs:134), f32 softmax (moe.rs:135), descending argsort
+ *       top-k (moe.rs:140-142), renormalisation (moe.rs:143-146), per-expert
+ *       ascending token lists (moe.rs:152-160)
+ *   - dispatch permutation     crates/neuron/src/harness/tp/tp_qwen3_5.rs:1189
+ *       (topk_ids.flatten_all().sort_last_dim(true), ties by flat index)
+ *   - Module::forward          moe.rs:164-199 (experts ascending, then shared)
+ *   - Qwen3_5MLP::forward      crates/neuron/src/harness/arch/qwen3_5/mlp.rs:54-60
+ *   - MaybeQuantLinear         crates/neuron/src/harness/tp/tp_linear.rs:98-140
+ *       (quantised weights: GGUF Q8_0 / Q4_K / Q6_K blocks, public ggml format)
+ *   - quantize_blocks          crates/neuron/src/harness/tp/isq.rs:57-113
+ *       (block layout and divisibility; the per-block search is our own)
+ *   - Qwen3_5RmsNorm::forward  crates/neuron/src/harness/arch/qwen3_5/rmsnorm.rs:67-80
+ *   - decoder residual         crates/neuron/src/harness/arch/qwen3_5/decoder.rs:129-132
+ *
+ * Numeric contract shared (by restatement, not by code) with the HIP library:
+ *   - router logit = lane-strided dot product: the H inputs are cut into groups
+ *     of 8 (the last one may be shorter); group g belongs to lane g % 64; each lane runs an fmaf chain over its
+ *     groups in increasing order; the 64 lane partials are then combined by an
+ *     xor butterfly (offsets 32,16,8,4,2,1). The result is rounded to the
+ *     activation dtype (candle's Linear returns the input dtype, moe.rs:134).
+ *   - softmax uses hxo_expf below (Cody-Waite reduction + degree-7 Taylor,
+ *     evaluated with fmaf), a lane-strided sum with the same butterfly, and an
+ *     IEEE division.
+ *   - top-k: k largest probabilities, ties to the lower expert id.
+ *   - renormalisation: sequential sum in rank order, IEEE division.
+ * Everything here is compiled with -ffp-contract=off so that no multiply-add is
+ * fused unless fmaf is written explicitly.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define HXO_F32 0
+#define HXO_F16 1
+#define HXO_Q8_0 8
+#define HXO_Q4_K 12
+#define HXO_Q6_K 14
+#define HXO_BF16 30
+
+/* ------------------------------------------------------------------------- */
+/* scalar formats                                                            */
+/* ------------------------------------------------------------------------- */
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+uint16_t hxo_f32_to_bf16(float f) {
+    uint32_t u = f2u(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+float hxo_bf16_to_f32(uint16_t h) { return u2f((uint32_t)h << 16); }
+
+uint16_t hxo_f32_to_f16(float f) {
+    uint32_t x = f2u(f);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    uint32_t ax = x & 0x7fffffffu;
+    if (ax > 0x7f800000u) return sign | 0x7e00u;           /* NaN */
+    if (ax >= 0x38800000u) {                                /* f16 normal range */
+        uint32_t m = ax + 0xfffu + ((ax >> 13) & 1u);       /* RNE to 10 bits */
+        m -= (112u << 23);
+        if (m >= 0x0f800000u) return sign | 0x7c00u;        /* overflow -> inf */
+        return (uint16_t)(sign | (m >> 13));
+    }
+    /* f16 subnormal or zero: value * 2^24 rounded to an integer, RNE */
+    float v = u2f(ax) * 16777216.0f;
+    volatile float r = v + 8388608.0f;
+    float q = r - 8388608.0f;
+    return (uint16_t)(sign | (uint16_t)q);
+}
+
+float hxo_f16_to_f32(uint16_t h) {
+    uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
+    if (e == 0) {
+        float v = (float)m * 5.9604644775390625e-8f;        /* m * 2^-24 */
+        return sign ? -v : v;
+    }
+    if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));
+    return u2f(sign | ((e + 112u) << 23) | (m << 13));
+}
+
+/* exp(x) for the router softmax. Cody-Waite split of ln2 (the Cephes
+ * constants 0.693145751953125 + 1.42860682030941723212e-6), then the degree-7
+ * Taylor polynomial of e^r on |r| <= ln2/2 in Horner form with fmaf, then an
+ * exact scaling by 2^n. Inputs below -87 return 0 (the result would be within
+ * a factor 2 of FLT_MIN); inputs above 88.5 return +inf. */
+float hxo_expf(float x) {
+    if (x != x) return x;
+    if (x < -87.0f) return 0.0f;
+    if (x > 88.5f) return INFINITY;
+    float n = rintf(x * 1.44269504088896341f);
+    float r = fmaf(n, -0.693145751953125f, x);
+    r = fmaf(n, -1.42860682030941723212e-6f, r);
+    float p = 1.98412698412698413e-4f;              /* 1/7! */
+    p = fmaf(p, r, 1.38888888888888889e-3f);        /* 1/6! */
+    p = fmaf(p, r, 8.33333333333333333e-3f);        /* 1/5! */
+    p = fmaf(p, r, 4.16666666666666667e-2f);        /* 1/4! */
+    p = fmaf(p, r, 1.66666666666666667e-1f);        /* 1/3! */
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    int ni = (int)n;
+    if (ni > 127) return p * u2f((uint32_t)(127 + 127) << 23) * 2.0f;
+    return p * u2f((uint32_t)(ni + 127) << 23);
+}
+
+/* ------------------------------------------------------------------------- */
+/* GGUF blocks (public ggml format)                                          */
+/* ------------------------------------------------------------------------- */
+int64_t hxo_block_elems(int dtype) {
+    switch (dtype) {
+    case HXO_F32: case HXO_F16: case HXO_BF16: return 1;
+    case HXO_Q8_0: return 32;
+    case HXO_Q4_K: case HXO_Q6_K: return 256;
+    default: return 0;
+    }
+}
+
+int64_t hxo_block_bytes(int dtype) {
+    switch (dtype) {
+    case HXO_F32: return 4;
+    case HXO_F16: case HXO_BF16: return 2;
+    case HXO_Q8_0: return 34;
+    case HXO_Q4_K: return 144;
+    case HXO_Q6_K: return 210;
+    default: return 0;
+    }
+}
+
+/* bytes of one row of n elements; -1 if n does not tile into whole blocks */
+int64_t hxo_row_bytes(int dtype, int64_t n) {
+    int64_t be = hxo_block_elems(dtype);
+    if (be == 0 || n % be) return -1;
+    return n / be * hxo_block_bytes(dtype);
+}
+
+static inline float ld_f16(const uint8_t* p) { uint16_t h; memcpy(&h, p, 2); return hxo_f16_to_f32(h); }
+
+static void dq_q8_0(const uint8_t* b, float* y) {
+    float d = ld_f16(b);
+    const int8_t* qs = (const int8_t*)(b + 2);
+    for (int j = 0; j < 32; j++) y[j] = d * (float)qs[j];
+}
+
+/* Q4_K 6-bit scale/min of sub-block j from the 12 packed bytes */
+static void q4k_scale_min(int j, const uint8_t* s, int* sc, int* m) {
+    if (j < 4) {
+        *sc = s[j] & 63;
+        *m = s[j + 4] & 63;
+    } else {
+        *sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+        *m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+static void dq_q4_k(const uint8_t* b, float* y) {
+    float d = ld_f16(b), dmin = ld_f16(b + 2);
+    const uint8_t* sc = b + 4;
+    const uint8_t* qs = b + 16;
+    for (int c = 0; c < 4; c++) {
+        int s0, m0, s1, m1;
+        q4k_scale_min(2 * c, sc, &s0, &m0);
+        q4k_scale_min(2 * c + 1, sc, &s1, &m1);
+        float d0 = d * (float)s0, mm0 = dmin * (float)m0;
+        float d1 = d * (float)s1, mm1 = dmin * (float)m1;
+        for (int l = 0; l < 32; l++) {
+            uint8_t q = qs[32 * c + l];
+            y[64 * c + l] = d0 * (float)(q & 0xF) - mm0;
+            y[64 * c + 32 + l] = d1 * (float)(q >> 4) - mm1;
+        }
+    }
+}
+
+static void dq_q6_k(const uint8_t* b, float* y) {
+    const uint8_t* ql = b;
+    const uint8_t* qh = b + 128;
+    const int8_t* sc = (const int8_t*)(b + 192);
+    float d = ld_f16(b + 208);
+    for (int n = 0; n < 2; n++) {
+        for (int l = 0; l < 32; l++) {
+            int is = l / 16;
+            int q1 = (int)((ql[64 * n + l] & 0xF) | (((qh[32 * n + l] >> 0) & 3) << 4)) - 32;
+            int q2 = (int)((ql[64 * n + l + 32] & 0xF) | (((qh[32 * n + l] >> 2) & 3) << 4)) - 32;
+            int q3 = (int)((ql[64 * n + l] >> 4) | (((qh[32 * n + l] >> 4) & 3) << 4)) - 32;
+            int q4 = (int)((ql[64 * n + l + 32] >> 4) | (((qh[32 * n + l] >> 6) & 3) << 4)) - 32;
+            y[128 * n + l] = d * (float)sc[8 * n + is] * (float)q1;
+            y[128 * n + l + 32] = d * (float)sc[8 * n + is + 2] * (float)q2;
+            y[128 * n + l + 64] = d * (float)sc[8 * n + is + 4] * (float)q3;
+            y[128 * n + l + 96] = d * (float)sc[8 * n + is + 6] * (float)q4;
+        }
+    }
+}
+
+/* dequantise n elements (a whole number of blocks) to f32 */
+int hxo_dequant(int dtype, const void* src, int64_t n, float* dst) {
+    const uint8_t* s = (const uint8_t*)src;
+    int64_t be = hxo_block_elems(dtype), bb = hxo_block_bytes(dtype);
+    if (be == 0 || n % be) return 1;
+    for (int64_t b = 0; b < n / be; b++) {
+        const uint8_t* blk = s + b * bb;
+        float* y = dst + b * be;
+        switch (dtype) {
+        case HXO_F32: memcpy(y, blk, 4); break;
+        case HXO_F16: *y = ld_f16(blk); break;
+        case HXO_BF16: { uint16_t h; memcpy(&h, blk, 2); *y = hxo_bf16_to_f32(h); } break;
+        case HXO_Q8_0: dq_q8_0(blk, y); break;
+        case HXO_Q4_K: dq_q4_k(blk, y); break;
+        case HXO_Q6_K: dq_q6_k(blk, y); break;
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* quantisers (our own per-block search; block layout per isq.rs:57-113)      */
+/* ------------------------------------------------------------------------- */
+static inline int nearest(float v) { return (int)rintf(v); }
+
+static void qz_q8_0(const float* x, uint8_t* b) {
+    float amax = 0.0f;
+    for (int j = 0; j < 32; j++) { float a = fabsf(x[j]); if (a > amax) amax = a; }
+    float d = amax / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint16_t dh = hxo_f32_to_f16(d);
+    memcpy(b, &dh, 2);
+    for (int j = 0; j < 32; j++) {
+        int q = nearest(x[j] * id);
+        if (q > 127) q = 127;
+        if (q < -127) q = -127;
+        b[2 + j] = (uint8_t)(int8_t)q;
+    }
+}
+
+static void qz_q4_k(const float* x, uint8_t* b) {
+    float scale[8], mins[8];
+    float max_scale = 0.0f, max_min = 0.0f;
+    for (int j = 0; j < 8; j++) {
+        float mn = 0.0f, mx = x[32 * j];
+        for (int l = 0; l < 32; l++) {
+            float v = x[32 * j + l];
+            if (v < mn) mn = v;
+            if (v > mx) mx = v;
+        }
+        scale[j] = (mx - mn) / 15.0f;
+        mins[j] = -mn;
+        if (scale[j] > max_scale) max_scale = scale[j];
+        if (mins[j] > max_min) max_min = mins[j];
+    }
+    float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+    float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+    uint8_t ls[8], lm[8];
+    for (int j = 0; j < 8; j++) {
+        int a = nearest(inv_scale * scale[j]), m = nearest(inv_min * mins[j]);
+        ls[j] = (uint8_t)(a > 63 ? 63 : a);
+        lm[j] = (uint8_t)(m > 63 ? 63 : m);
+    }
+    uint16_t dh = hxo_f32_to_f16(max_scale / 63.0f), mh = hxo_f32_to_f16(max_min / 63.0f);
+    memcpy(b, &dh, 2);
+    memcpy(b + 2, &mh, 2);
+    uint8_t* s = b + 4;
+    for (int j = 0; j < 4; j++) {
+        s[j] = (uint8_t)((ls[j] & 63) | ((ls[j + 4] >> 4) << 6));
+        s[j + 4] = (uint8_t)((lm[j] & 63) | ((lm[j + 4] >> 4) << 6));
+        s[j + 8] = (uint8_t)((ls[j + 4] & 0xF) | ((lm[j + 4] & 0xF) << 4));
+    }
+    float d = hxo_f16_to_f32(dh), dmin = hxo_f16_to_f32(mh);
+    uint8_t q[256];
+    for (int j = 0; j < 8; j++) {
+        float dd = d * (float)ls[j], dm = dmin * (float)lm[j];
+        for (int l = 0; l < 32; l++) {
+            int v = 0;
+            if (dd != 0.0f) {
+                v = nearest((x[32 * j + l] + dm) / dd);
+                if (v < 0) v = 0;
+                if (v > 15) v = 15;
+            }
+            q[32 * j + l] = (uint8_t)v;
+        }
+    }
+    uint8_t* qs = b + 16;
+    for (int c = 0; c < 4; c++)
+        for (int l = 0; l < 32; l++)
+            qs[32 * c + l] = (uint8_t)(q[64 * c + l] | (q[64 * c + 32 + l] << 4));
+}
+
+static void qz_q6_k(const float* x, uint8_t* b) {
+    float scale[16];
+    float max_scale = 0.0f, max_abs_scale = 0.0f;
+    for (int i = 0; i < 16; i++) {
+        float vmax = 0.0f, amax = 0.0f;
+        for (int l = 0; l < 16; l++) {
+            float v = x[16 * i + l], a = fabsf(v);
+            if (a > amax) { amax = a; vmax = v; }
+        }
+        scale[i] = vmax != 0.0f ? vmax / -32.0f : 0.0f;
+        float as = fabsf(scale[i]);
+        if (as > max_abs_scale) { max_abs_scale = as; max_scale = scale[i]; }
+    }
+    float iscale = max_scale != 0.0f ? -128.0f / max_scale : 0.0f;
+    int8_t sc[16];
+    for (int i = 0; i < 16; i++) {
+        int v = nearest(iscale * scale[i]);
+        if (v > 127) v = 127;
+        if (v < -128) v = -128;
+        sc[i] = (int8_t)v;
+    }
+    uint16_t dh = hxo_f32_to_f16(iscale != 0.0f ? 1.0f / iscale : 0.0f);
+    float d = hxo_f16_to_f32(dh);
+    uint8_t L[256];
+    for (int i = 0; i < 16; i++) {
+        float di = d * (float)sc[i];
+        for (int l = 0; l < 16; l++) {
+            int v = 0;
+            if (di != 0.0f) {
+                v = nearest(x[16 * i + l] / di);
+                if (v < -32) v = -32;
+                if (v > 31) v = 31;
+            }
+            L[16 * i + l] = (uint8_t)(v + 32);
+        }
+    }
+    uint8_t* ql = b;
+    uint8_t* qh = b + 128;
+    for (int n = 0; n < 2; n++) {
+        for (int l = 0; l < 32; l++) {
+            uint8_t q1 = L[128 * n + l], q2 = L[128 * n + 32 + l];
+            uint8_t q3 = L[128 * n + 64 + l], q4 = L[128 * n + 96 + l];
+            ql[64 * n + l] = (uint8_t)((q1 & 0xF) | ((q3 & 0xF) << 4));
+            ql[64 * n + 32 + l] = (uint8_t)((q2 & 0xF) | ((q4 & 0xF) << 4));
+            qh[32 * n + l] = (uint8_t)((q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6));
+        }
+    }
+    memcpy(b + 192, sc, 16);
+    memcpy(b + 208, &dh, 2);
+}
+
+/* quantise a [rows, cols] f32 matrix into GGUF rows; cols must tile into blocks
+ * (the same constraint as isq.rs:62-68). Returns 0 on success. */
+int hxo_quantize(int dtype, const float* src, int64_t rows, int64_t cols, void* dst, int nthreads) {
+    int64_t be = hxo_block_elems(dtype), bb = hxo_block_bytes(dtype);
+    if (be == 0 || cols <= 0 || cols % be) return 1;
+    int64_t nb = rows * (cols / be);
+    uint8_t* d = (uint8_t*)dst;
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+    for (int64_t b = 0; b < nb; b++) {
+        const float* x = src + b * be;
+        uint8_t* o = d + b * bb;
+        switch (dtype) {
+        case HXO_F32: memcpy(o, x, 4); break;
+        case HXO_F16: { uint16_t h = hxo_f32_to_f16(*x); memcpy(o, &h, 2); } break;
+        case HXO_BF16: { uint16_t h = hxo_f32_to_bf16(*x); memcpy(o, &h, 2); } break;
+        case HXO_Q8_0: qz_q8_0(x, o); break;
+        case HXO_Q4_K: qz_q4_k(x, o); break;
+        case HXO_Q6_K: qz_q6_k(x, o); break;
+        }
+    }
+    (void)nthreads;
+    return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* router                                                                     */
+/* ------------------------------------------------------------------------- */
+static inline float ld_act(int dtype, const void* p, int64_t i) {
+    if (dtype == HXO_BF16) return hxo_bf16_to_f32(((const uint16_t*)p)[i]);
+    return ((const float*)p)[i];
+}
+
+/* 64 lane partials combined by the xor butterfly 32,16,8,4,2,1 */
+static float butterfly64(float* p) {
+    for (int off = 32; off >= 1; off >>= 1) {
+        float q[64];
+        for (int l = 0; l < 64; l++) q[l] = p[l] + p[l ^ off];
+        memcpy(p, q, sizeof q);
+    }
+    return p[0];
+}
+
+/* canonical router dot product of x (act dtype) and one router row (router dtype) */
+static float router_dot(int act_dtype, const void* x, int router_dtype, const void* w, int64_t H) {
+    float acc[64];
+    for (int l = 0; l < 64; l++) acc[l] = 0.0f;
+    for (int64_t g = 0; 8 * g < H; g++) {
+        int l = (int)(g % 64);
+        for (int i = 0; i < 8 && 8 * g + i < H; i++) {
+            int64_t h = 8 * g + i;
+            acc[l] = fmaf(ld_act(act_dtype, x, h), ld_act(router_dtype, w, h), acc[l]);
+        }
+    }
+    return butterfly64(acc);
+}
+
+typedef struct hxo_moe {
+    int32_t hidden, num_experts, top_k, inter, shared_inter, norm_topk_prob, act_dtype;
+    int32_t router_dtype; const void* router;        /* [E, H] */
+    int32_t gate_dtype; const void* gate;            /* [E, I, H] GGUF rows */
+    int32_t up_dtype; const void* up;                /* [E, I, H] */
+    int32_t down_dtype; const void* down;            /* [E, H, I] */
+    int32_t sgate_dtype; const void* sgate;          /* [Is, H] */
+    int32_t sup_dtype; const void* sup;              /* [Is, H] */
+    int32_t sdown_dtype; const void* sdown;          /* [H, Is] */
+    int32_t seg_dtype; const void* seg;              /* shared_expert_gate [1, H] */
+} hxo_moe;
+
+/* logits [T, E] exactly as the router kernel produces them (rounded to the
+ * activation dtype, then + bias if given) */
+int hxo_router_logits(const hxo_moe* m, const void* x, int64_t T, const float* bias, float* logits) {
+    int64_t H = m->hidden, E = m->num_experts;
+    int64_t wrow = H * (m->router_dtype == HXO_BF16 ? 2 : 4);
+    int64_t xrow = H * (m->act_dtype == HXO_BF16 ? 2 : 4);
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t t = 0; t < T; t++) {
+        const void* xt = (const uint8_t*)x + t * xrow;
+        for (int64_t e = 0; e < E; e++) {
+            float v = router_dot(m->act_dtype, xt, m->router_dtype, (const uint8_t*)m->router + e * wrow, H);
+            if (m->act_dtype == HXO_BF16) v = hxo_bf16_to_f32(hxo_f32_to_bf16(v));
+            if (bias) v = v + bias[e];
+            logits[t * E + e] = v;
+        }
+    }
+    return 0;
+}
+
+/* softmax over E with the lane-strided sum + butterfly */
+static void softmax_row(const float* l, int64_t E, float* p) {
+    float mx = l[0];
+    for (int64_t e = 1; e < E; e++) if (l[e] > mx) mx = l[e];
+    float acc[64];
+    for (int i = 0; i < 64; i++) acc[i] = 0.0f;
+    for (int64_t e = 0; e < E; e++) {
+        p[e] = hxo_expf(l[e] - mx);
+        acc[e % 64] = acc[e % 64] + p[e];
+    }
+    float s = butterfly64(acc);
+    for (int64_t e = 0; e < E; e++) p[e] = p[e] / s;
+}
+
+/* k largest with ties to the lower index; selection by repeated scan */
+static void topk_row(const float* p, int64_t E, int k, int32_t* idx, unsigned char* taken) {
+    memset(taken, 0, (size_t)E);
+    for (int j = 0; j < k; j++) {
+        int64_t best = -1;
+        for (int64_t e = 0; e < E; e++) {
+            if (taken[e]) continue;
+            if (best < 0 || p[e] > p[best]) best = e;
+        }
+        taken[best] = 1;
+        idx[j] = (int32_t)best;
+    }
+}
+
+/* route_scatter (moe.rs:124-162) up to the device->host copy: probs, top-k ids and
+ * weights. Any of the outputs may be NULL. */
+int hxo_route(const hxo_moe* m, const void* x, int64_t T, const float* bias,
+              float* logits_out, float* probs_out, int32_t* topk_idx, float* topk_w) {
+    int64_t E = m->num_experts;
+    int k = m->top_k;
+    if (k <= 0 || k > E || k > 1024 || E > 65536) return 1;
+    float* logits = (float*)malloc(sizeof(float) * T * E);
+    float* probs = (float*)malloc(sizeof(float) * T * E);
+    if (!logits || !probs) { free(logits); free(probs); return 2; }
+    int rc = hxo_router_logits(m, x, T, bias, logits);
+    if (rc) { free(logits); free(probs); return rc; }
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+    for (int64_t t = 0; t < T; t++) {
+        int32_t ids[1024];
+        unsigned char taken[65536];
+        softmax_row(logits + t * E, E, probs + t * E);
+        topk_row(probs + t * E, E, k, ids, taken);
+        float s = 0.0f;
+        for (int j = 0; j < k; j++) s = s + probs[t * E + ids[j]];
+        for (int j = 0; j < k; j++) {
+            float w = probs[t * E + ids[j]];
+            if (m->norm_topk_prob) w = w / s;
+            if (topk_idx) topk_idx[t * k + j] = ids[j];
+            if (topk_w) topk_w[t * k + j] = w;
+        }
+    }
+    if (logits_out) memcpy(logits_out, logits, sizeof(float) * T * E);
+    if (probs_out) memcpy(probs_out, probs, sizeof(float) * T * E);
+    free(logits);
+    free(probs);
+    return 0;
+}
+
+/* dispatch permutation: flat index f = t*k + j stably sorted by expert id
+ * (tp_qwen3_5.rs:1189; equals moe.rs:152-160's ascending-token lists).
+ * perm[pos] = f, offsets[E+1] exclusive scan of the histogram, inv[f] = pos. */
+int hxo_dispatch(const int32_t* topk_idx, int64_t T, int k, int64_t E,
+                 int32_t* perm, int32_t* offsets, int32_t* inv) {
+    int64_t F = T * k;
+    int32_t* cnt = (int32_t*)calloc((size_t)E + 1, sizeof(int32_t));
+    if (!cnt) return 2;
+    for (int64_t f = 0; f < F; f++) {
+        int32_t e = topk_idx[f];
+        if (e < 0 || e >= E) { free(cnt); return 1; }
+        cnt[e]++;
+    }
+    int32_t run = 0;
+    for (int64_t e = 0; e < E; e++) { int32_t c = cnt[e]; offsets[e] = run; cnt[e] = run; run += c; }
+    offsets[E] = run;
+    for (int64_t f = 0; f < F; f++) {
+        int32_t pos = cnt[topk_idx[f]]++;
+        perm[pos] = (int32_t)f;
+        if (inv) inv[f] = pos;
+    }
+    free(cnt);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* forward                                                                    */
+/* ------------------------------------------------------------------------- */
+/* dot product with a fixed order: 8 interleaved double accumulators summed
+ * pairwise at the end (deterministic, vectorisable without reassociation) */
+static double dotd(const float* a, const float* b, int64_t K) {
+    double s[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int64_t i = 0;
+    for (; i + 8 <= K; i += 8)
+        for (int j = 0; j < 8; j++) s[j] += (double)a[i + j] * (double)b[i + j];
+    for (; i < K; i++) s[0] += (double)a[i] * (double)b[i];
+    return ((s[0] + s[4]) + (s[1] + s[5])) + ((s[2] + s[6]) + (s[3] + s[7]));
+}
+
+static inline float silu_f(float g) { return g / (1.0f + expf(-g)); }
+
+/* One SwiGLU expert (mlp.rs:54-60) over the n tokens rows[0..n) of xf:
+ * acc[rows[p]] += scale[p] * down(silu(gate x) * up x).
+ * gate/up are [I, H] GGUF rows, down is [H, I]. hbuf holds n*I floats. */
+static void expert_rows(int gdt, const void* g, int udt, const void* u, int ddt, const void* d,
+                        int64_t H, int64_t I, const float* xf, const int32_t* rows, const double* scale,
+                        int64_t n, double* acc, float* hbuf, int nthreads) {
+    int64_t grb = hxo_row_bytes(gdt, H), urb = hxo_row_bytes(udt, H), drb = hxo_row_bytes(ddt, I);
+#ifdef _OPENMP
+#pragma omp parallel num_threads(nthreads)
+#endif
+    {
+        float* wg = (float*)malloc(sizeof(float) * H);
+        float* wu = (float*)malloc(sizeof(float) * H);
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (int64_t i = 0; i < I; i++) {
+            hxo_dequant(gdt, (const uint8_t*)g + i * grb, H, wg);
+            hxo_dequant(udt, (const uint8_t*)u + i * urb, H, wu);
+            for (int64_t p = 0; p < n; p++) {
+                const float* xt = xf + (int64_t)rows[p] * H;
+                float gv = (float)dotd(wg, xt, H), uv = (float)dotd(wu, xt, H);
+                hbuf[p * I + i] = silu_f(gv) * uv;
+            }
+        }
+        float* wd = wg;
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (int64_t r = 0; r < H; r++) {
+            hxo_dequant(ddt, (const uint8_t*)d + r * drb, I, wd);
+            for (int64_t p = 0; p < n; p++)
+                acc[(int64_t)rows[p] * H + r] += scale[p] * dotd(wd, hbuf + p * I, I);
+        }
+        free(wg);
+        free(wu);
+    }
+}
+
+/* Module::forward (moe.rs:164-199): the scatter loop over experts in ascending
+ * id, each expert's tokens ascending (moe.rs:178-189), then the sigmoid-gated
+ * shared expert (moe.rs:191-195). y is f32 [T, H], not rounded to the
+ * activation dtype; products accumulate in double. */
+int hxo_moe_forward(const hxo_moe* m, const void* x, int64_t T, const float* bias, float* y, int nthreads) {
+    int64_t H = m->hidden, E = m->num_experts, I = m->inter, Is = m->shared_inter;
+    int k = m->top_k;
+    if (hxo_row_bytes(m->gate_dtype, H) < 0 || hxo_row_bytes(m->up_dtype, H) < 0 ||
+        hxo_row_bytes(m->down_dtype, I) < 0)
+        return 1;
+    if (Is > 0 && (hxo_row_bytes(m->sgate_dtype, H) < 0 || hxo_row_bytes(m->sup_dtype, H) < 0 ||
+                   hxo_row_bytes(m->sdown_dtype, Is) < 0 || !m->seg))
+        return 1;
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#else
+    nthreads = 1;
+#endif
+    int64_t F = T * k, KM = I > Is ? I : Is;
+    int32_t* idx = (int32_t*)malloc(sizeof(int32_t) * F);
+    float* w = (float*)malloc(sizeof(float) * F);
+    int32_t* perm = (int32_t*)malloc(sizeof(int32_t) * F);
+    int32_t* offs = (int32_t*)malloc(sizeof(int32_t) * (E + 1));
+    int32_t* rows = (int32_t*)malloc(sizeof(int32_t) * (T > F ? T : F));
+    double* sc = (double*)malloc(sizeof(double) * (T > F ? T : F));
+    float* xf = (float*)malloc(sizeof(float) * T * H);
+    float* hbuf = (float*)malloc(sizeof(float) * (T > F ? T : F) * KM);
+    double* acc = (double*)calloc((size_t)(T * H), sizeof(double));
+    int rc = 0;
+    if (!idx || !w || !perm || !offs || !rows || !sc || !xf || !hbuf || !acc) { rc = 2; goto done; }
+    rc = hxo_route(m, x, T, bias, NULL, NULL, idx, w);
+    if (rc) goto done;
+    rc = hxo_dispatch(idx, T, k, E, perm, offs, NULL);
+    if (rc) goto done;
+    for (int64_t i = 0; i < T * H; i++) xf[i] = ld_act(m->act_dtype, x, i);
+    {
+        int64_t gb = hxo_row_bytes(m->gate_dtype, H) * I, ub = hxo_row_bytes(m->up_dtype, H) * I;
+        int64_t db = hxo_row_bytes(m->down_dtype, I) * H;
+        for (int64_t e = 0; e < E; e++) {
+            int64_t n = offs[e + 1] - offs[e];
+            if (n == 0) continue;
+            for (int64_t p = 0; p < n; p++) {
+                int32_t f = perm[offs[e] + p];
+                rows[p] = f / k;
+                sc[p] = (double)w[f];
+            }
+            expert_rows(m->gate_dtype, (const uint8_t*)m->gate + e * gb, m->up_dtype,
+                        (const uint8_t*)m->up + e * ub, m->down_dtype, (const uint8_t*)m->down + e * db,
+                        H, I, xf, rows, sc, n, acc, hbuf, nthreads);
+        }
+    }
+    if (Is > 0) {
+        float* wr = (float*)malloc(sizeof(float) * H);
+        hxo_dequant(m->seg_dtype, m->seg, H, wr);
+        for (int64_t t = 0; t < T; t++) {
+            rows[t] = (int32_t)t;
+            sc[t] = 1.0 / (1.0 + exp(-dotd(wr, xf + t * H, H)));
+        }
+        free(wr);
+        expert_rows(m->sgate_dtype, m->sgate, m->sup_dtype, m->sup, m->sdown_dtype, m->sdown,
+                    H, Is, xf, rows, sc, T, acc, hbuf, nthreads);
+    }
+    for (int64_t i = 0; i < T * H; i++) y[i] = (float)acc[i];
+done:
+    free(idx); free(w); free(perm); free(offs); free(rows); free(sc); free(xf); free(hbuf); free(acc);
+    return rc;
+}
+
+/* Qwen3_5RmsNorm::forward (rmsnorm.rs:67-80): x * rsqrt(mean(x^2) + eps) * (1 + w),
+ * computed in f32; output f32 (caller rounds). */
+int hxo_rmsnorm(int act_dtype, const void* x, int64_t T, int64_t H, const float* w, float eps, float* y) {
+    for (int64_t t = 0; t < T; t++) {
+        double ss = 0.0;
+        for (int64_t i = 0; i < H; i++) { double v = ld_act(act_dtype, x, t * H + i); ss += v * v; }
+        float inv = (float)(1.0 / sqrt(ss / (double)H + (double)eps));
+        for (int64_t i = 0; i < H; i++) y[t * H + i] = ld_act(act_dtype, x, t * H + i) * inv * (1.0f + w[i]);
+    }
+    return 0;
+}

@@ -1,0 +1,69 @@
+"""Shared helpers for the tests: seeded synthetic blocks and the oracle view of them.
+
+Weights are drawn from N(0, 0.02) and activations from N(0, 1) with numpy's PCG64
+(`np.random.default_rng(seed)`), which gives the same stream on every platform.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import oracle as O
+
+KEYS = ("router", "gate", "up", "down", "sgate", "sup", "sdown", "seg")
+
+
+def shapes(H, E, I, Is):
+    s = {"router": (E, H), "gate": (E, I, H), "up": (E, I, H), "down": (E, H, I)}
+    if Is > 0:
+        s.update({"sgate": (Is, H), "sup": (Is, H), "sdown": (H, Is), "seg": (1, H)})
+    return s
+
+
+def make_f32_block(seed, H, E, I, Is, std=0.02):
+    rng = np.random.default_rng(seed)
+    return {k: (rng.standard_normal(shp, dtype=np.float32) * np.float32(std)) for k, shp in shapes(H, E, I, Is).items()}
+
+
+def make_x(seed, T, H):
+    rng = np.random.default_rng(seed + 7919)
+    return rng.standard_normal((T, H), dtype=np.float32)
+
+
+def bf16_bits(a: np.ndarray) -> np.ndarray:
+    """round-to-nearest-even f32 -> bf16 bits (vectorised; NaN-free inputs)"""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = u + 0x7FFF + ((u >> 16) & 1)
+    return (u >> 16).astype(np.uint16)
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return O.bf16_bits_to_f32(b)
+
+
+def store(w: dict, formats: dict) -> dict:
+    """Convert f32 weights to their storage formats. formats maps key -> dtype."""
+    out = {}
+    for k, a in w.items():
+        dt = formats.get(k, O.F32)
+        if dt == O.F32:
+            out[k] = (dt, np.ascontiguousarray(a, dtype=np.float32))
+        elif dt == O.BF16:
+            out[k] = (dt, bf16_bits(a))
+        else:
+            out[k] = (dt, O.quantize(dt, a))
+    return out
+
+
+def oracle_block(cfg, stored, act_dtype):
+    H, E, k, I, Is, norm = cfg
+    return O.OracleMoe(H, E, k, I, Is, norm, act_dtype, stored)
+
+
+C1 = dict(H=256, E=16, k=4, I=128, Is=128, norm=True, T=32)
+
+
+def rel_err(got, ref):
+    """normwise max|got-ref| / max|ref| (the parity gate)"""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
