@@ -1,0 +1,112 @@
+// Internal declarations of libhxmoe: kernel argument blocks, launchers and the
+// handle. Not part of the C ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+#include <vector>
+
+#include "hx_formats.h"
+
+// Largest expert count the routing kernels hold in registers / LDS.
+#define HX_MAX_EXPERTS 1024
+// Largest k (top-k) supported: one lane per selected expert.
+#define HX_MAX_TOPK 64
+// Token count up to which the decode path (fused routing tail, GEMV experts,
+// in-register combine) is used.
+#define HX_DECODE_MAX_T 8
+// Rows of a grouped-GEMM M tile.
+#define HX_TILE_M 64
+
+namespace hx {
+
+struct DispatchArgs {
+  int32_t* topk_idx;   // [T*k] (input)
+  int T, k, E, F;
+  bool has_shared;
+  int tile_m;
+  int32_t* perm;       // [F]
+  int32_t* inv;        // [F] or null
+  int32_t* offsets;    // [E+1]
+  int32_t* slots;      // [(min(F,E)+1) * 3]: expert, start position, count
+  int32_t* tiles;      // [max_tiles * 4]: slot, expert, start position, rows
+  int32_t* counts;     // [2]: number of slots, number of tiles
+};
+
+struct RouterArgs {
+  const void* x;       // [T, H] act dtype
+  int T, H;
+  const void* R;       // [E1, H] router rows (+ shared-expert gate row)
+  int E1, E, k;
+  bool norm, has_shared;
+  const float* bias;   // [E] or null
+  float* logits;       // [T, E1]
+  float* topk_w;       // [T*k]
+  float* sgw;          // [T] sigmoid of the shared-expert gate
+  unsigned* counter;   // zero between launches
+  DispatchArgs d;
+};
+
+// One projection stack: E matrices of [rows][K] in the internal layout.
+struct WMat {
+  int fmt = -1;        // HX_F32 / HX_BF16 / HX_Q8_0 (planar) / HX_Q4_K / HX_Q6_K (planar)
+  int rows = 0, K = 0, count = 0;
+  int64_t mat_bytes = 0;
+  uint8_t* base = nullptr;
+  __host__ __device__ const uint8_t* mat(int e) const { return base + (int64_t)e * mat_bytes; }
+};
+
+struct ExpertArgs {
+  // routed stacks
+  WMat gate, up, down;
+  // shared expert (count 1) - fmt -1 if absent
+  WMat sgate, sup, sdown;
+  int E, k, H, I, Is, T, F;
+  const void* x;
+  bool xbf;
+  const int32_t* perm;
+  const float* topk_w;
+  const float* sgw;
+  const int32_t* slots;
+  const int32_t* tiles;
+  const int32_t* counts;
+  float* hbuf;         // [(F+T), hstride] SwiGLU activations, f32
+  int hstride;
+  uint16_t* hbf;       // [(F+T), hstride] bf16 copy for the grouped GEMMs
+  void* obuf;          // [(F+T), H] weighted expert outputs (prefill): bf16 for bf16
+                       // activations, f32 for f32 ones
+  const int32_t* inv;
+  const int32_t* topk_idx;
+  void* y;             // [T, H] act dtype
+  int max_slots, max_tiles;
+};
+
+void launch_router(const RouterArgs& a, bool xbf, bool rbf, bool tail, hipStream_t s);
+void launch_route_tokens(const RouterArgs& a, hipStream_t s);
+void launch_dispatch(const DispatchArgs& d, hipStream_t s);
+
+// decode (T <= HX_DECODE_MAX_T)
+hipError_t launch_gate_up_gemv(const ExpertArgs& a, hipStream_t s);
+hipError_t launch_down_gemv_combine(const ExpertArgs& a, hipStream_t s);
+// prefill
+hipError_t launch_gate_up_prefill(const ExpertArgs& a, hipStream_t s);
+hipError_t launch_down_prefill(const ExpertArgs& a, hipStream_t s);
+hipError_t launch_combine(const ExpertArgs& a, hipStream_t s);
+
+// weights
+hipError_t launch_quantize(int fmt, const float* src, int64_t rows, int64_t cols, void* dst, hipStream_t s);
+hipError_t launch_dequantize(int fmt, const void* src, int64_t rows, int64_t cols, float* dst, hipStream_t s);
+// GGUF rows of `count` contiguous [rows][K] matrices -> internal layout, matrix m
+// written at dst + m * dst_stride bytes
+hipError_t launch_repack(int fmt, const void* src, int64_t count, int64_t rows, int64_t K, void* dst,
+                         int64_t dst_stride, hipStream_t s);
+
+hipError_t launch_rmsnorm(const void* x, bool xbf, int64_t T, int64_t H, const float* w, float eps, void* y,
+                          hipStream_t s);
+hipError_t launch_residual_add(void* x, const void* y, bool bf, int64_t n, hipStream_t s);
+
+int64_t gguf_block_elems(int fmt);
+int64_t gguf_block_bytes(int fmt);
+
+}  // namespace hx

@@ -1,0 +1,614 @@
+// C ABI of libhxmoe (include/hx_moe.h): the block handle, weight upload and the
+// forward orchestration.
+//
+// Reference: Qwen3_5MoeBlock::{load, forward} (crates/neuron/src/harness/arch/qwen3_5/moe.rs:55-199),
+// TpQwen3_5MoeBlock::{load, forward_fused, forward}
+// (crates/neuron/src/harness/tp/tp_qwen3_5.rs:1060-1275).
+//
+// Decode (T <= HX_DECODE_MAX_T) runs three kernels: the router (whose last
+// block also does softmax / top-k / dispatch), gate/up + SwiGLU, and down +
+// combine. Prefill runs router, per-token routing, dispatch, gate/up, down
+// (weighted rows) and combine.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/hx_moe.h"
+#include "hx_internal.h"
+
+using namespace hx;
+
+static thread_local char g_err[512];
+
+static int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof g_err, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+#define HX_HIP(call)                                                                               \
+  do {                                                                                             \
+    hipError_t e_ = (call);                                                                        \
+    if (e_ != hipSuccess) return fail(HX_ERR_DEVICE, "%s failed: %s (%s:%d)", #call, hipGetErrorString(e_), \
+                                      __FILE__, __LINE__);                                         \
+  } while (0)
+
+extern "C" const char* hx_last_error(void) { return g_err; }
+
+extern "C" int64_t hx_row_bytes(int dtype, int64_t n) {
+  int64_t be = gguf_block_elems(dtype);
+  if (be == 0 || n <= 0 || n % be) return -1;
+  return n / be * gguf_block_bytes(dtype);
+}
+
+// ----------------------------------------------------------------------------
+// timing slots
+// ----------------------------------------------------------------------------
+enum { SLOT_ROUTER = 0, SLOT_ROUTE_TOKENS, SLOT_DISPATCH, SLOT_GATE_UP, SLOT_DOWN, SLOT_COMBINE, N_SLOTS };
+static const char* kSlotNames[N_SLOTS] = {"router", "route_tokens", "dispatch", "gate_up", "down", "combine"};
+
+struct Timing {
+  bool on = false;
+  int max_calls = 0, calls = 0;
+  std::vector<hipEvent_t> ev;  // [max_calls][N_SLOTS][2]
+  std::vector<int> used;       // [max_calls][N_SLOTS]
+};
+
+struct hx_moe {
+  hx_moe_config cfg{};
+  int device = 0;
+  int E1 = 0;
+  int rdt = HX_F32;   // dtype of the combined router rows
+  void* router = nullptr;
+  WMat gate, up, down, sgate, sup, sdown;
+  unsigned* counter = nullptr;
+  void* own_ws = nullptr;
+  size_t own_ws_bytes = 0;
+  Timing tm;
+};
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+struct WsLayout {
+  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, hbuf, hbf, obuf, xn, ym, total;
+  int hstride, max_slots, max_tiles;
+};
+
+static WsLayout ws_layout(const hx_moe* m, int64_t T) {
+  WsLayout L{};
+  const int64_t E = m->cfg.num_experts, k = m->cfg.num_experts_per_tok, H = m->cfg.hidden_size;
+  const int64_t F = T * k;
+  const int64_t I = m->cfg.moe_intermediate_size, Is = m->cfg.shared_expert_intermediate_size;
+  const bool decode = T <= HX_DECODE_MAX_T;
+  L.hstride = (int)(((I > Is ? I : Is) + 7) / 8 * 8);
+  L.max_slots = (int)((F < E ? F : E) + 1);
+  L.max_tiles = (int)((F + HX_TILE_M - 1) / HX_TILE_M + (F < E ? F : E) + (T + HX_TILE_M - 1) / HX_TILE_M + 1);
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    size_t at = o;
+    o += align256(bytes);
+    return at;
+  };
+  L.logits = take(sizeof(float) * T * m->E1);
+  L.topk_idx = take(sizeof(int32_t) * F);
+  L.topk_w = take(sizeof(float) * F);
+  L.sgw = take(sizeof(float) * T);
+  L.perm = take(sizeof(int32_t) * F);
+  L.inv = take(sizeof(int32_t) * F);
+  L.offsets = take(sizeof(int32_t) * (E + 1));
+  L.slots = take(sizeof(int32_t) * 3 * L.max_slots);
+  L.tiles = take(sizeof(int32_t) * 4 * L.max_tiles);
+  L.counts = take(sizeof(int32_t) * 4);
+  L.hbuf = take(sizeof(float) * (F + T) * L.hstride);
+  L.hbf = decode ? 0 : take(sizeof(uint16_t) * (F + T) * L.hstride);
+  const size_t act = m->cfg.act_dtype == HX_BF16 ? 2 : 4;
+  L.obuf = decode ? 0 : take(act * (F + T) * H);
+  L.xn = take(act * T * H);
+  L.ym = take(act * T * H);
+  L.total = o;
+  return L;
+}
+
+// ----------------------------------------------------------------------------
+// creation
+// ----------------------------------------------------------------------------
+static int chunk_elems(int fmt) {
+  switch (fmt) {
+    case HX_F32: case HX_BF16: return 8;
+    case HX_Q8_0: case HX_Q4_K: case HX_Q6_K: return 32;
+    default: return 0;
+  }
+}
+
+static int check_proj(const char* name, int fmt, int64_t K) {
+  if (fmt != HX_F32 && fmt != HX_BF16 && fmt != HX_Q8_0 && fmt != HX_Q4_K && fmt != HX_Q6_K)
+    return fail(HX_ERR_UNSUPPORTED, "%s: unsupported storage dtype %d", name, fmt);
+  if (hx_row_bytes(fmt, K) < 0)
+    return fail(HX_ERR_INVALID_ARGUMENT, "%s: input dim %lld does not tile into dtype %d blocks", name,
+                (long long)K, fmt);
+  int ch = chunk_elems(fmt);
+  if (K % ch || K / ch > 512)
+    return fail(HX_ERR_UNSUPPORTED, "%s: input dim %lld must be a multiple of %d and at most %d", name,
+                (long long)K, ch, 512 * ch);
+  return HX_OK;
+}
+
+// upload one projection stack ([count][rows][K] GGUF rows) into the internal
+// layout; every expert matrix starts on a 256-byte boundary
+static int upload_proj(WMat& w, const char* name, int fmt, const void* src, int loc, int count, int rows, int K) {
+  w.fmt = fmt;
+  w.rows = rows;
+  w.K = K;
+  w.count = count;
+  const int64_t packed = (int64_t)rows * hx_row_bytes(fmt, K);
+  w.mat_bytes = (int64_t)align256((size_t)packed);
+  const size_t bytes = (size_t)w.mat_bytes * count, src_bytes = (size_t)packed * count;
+  if (!src) return fail(HX_ERR_INVALID_ARGUMENT, "%s: null weight pointer", name);
+  if (hipMalloc(&w.base, bytes) != hipSuccess)
+    return fail(HX_ERR_OUT_OF_MEMORY, "%s: cannot allocate %zu bytes", name, bytes);
+  const void* dsrc = src;
+  void* tmp = nullptr;
+  if (loc == HX_HOST) {
+    if (hipMalloc(&tmp, src_bytes) != hipSuccess)
+      return fail(HX_ERR_OUT_OF_MEMORY, "%s: cannot allocate %zu staging bytes", name, src_bytes);
+    hipError_t e = hipMemcpy(tmp, src, src_bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(tmp);
+      return fail(HX_ERR_DEVICE, "%s: upload failed: %s", name, hipGetErrorString(e));
+    }
+    dsrc = tmp;
+  }
+  hipError_t e = launch_repack(fmt, dsrc, count, rows, K, w.base, w.mat_bytes, 0);
+  if (e == hipSuccess) e = hipDeviceSynchronize();
+  if (tmp) (void)hipFree(tmp);
+  if (e != hipSuccess) return fail(HX_ERR_DEVICE, "%s: repack failed: %s", name, hipGetErrorString(e));
+  return HX_OK;
+}
+
+static void free_mat(WMat& w) {
+  if (w.base) (void)hipFree(w.base);
+  w.base = nullptr;
+}
+
+extern "C" int hx_moe_destroy(hx_moe* m) {
+  if (!m) return HX_OK;
+  (void)hipSetDevice(m->device);
+  (void)hipDeviceSynchronize();
+  free_mat(m->gate); free_mat(m->up); free_mat(m->down);
+  free_mat(m->sgate); free_mat(m->sup); free_mat(m->sdown);
+  if (m->router) (void)hipFree(m->router);
+  if (m->counter) (void)hipFree(m->counter);
+  if (m->own_ws) (void)hipFree(m->own_ws);
+  for (hipEvent_t e : m->tm.ev) (void)hipEventDestroy(e);
+  delete m;
+  return HX_OK;
+}
+
+static int build_router(hx_moe* m, const hx_moe_weights* w) {
+  const int E = m->cfg.num_experts, H = m->cfg.hidden_size;
+  const bool sh = m->cfg.shared_expert_intermediate_size > 0;
+  const int rd = w->router_dtype, sd = sh ? w->shared_expert_gate_dtype : rd;
+  if ((rd != HX_F32 && rd != HX_BF16) || (sd != HX_F32 && sd != HX_BF16))
+    return fail(HX_ERR_UNSUPPORTED, "router / shared_expert_gate must be F32 or BF16");
+  if (!w->router || (sh && !w->shared_expert_gate))
+    return fail(HX_ERR_INVALID_ARGUMENT, "null router or shared_expert_gate pointer");
+  m->rdt = rd == sd ? rd : HX_F32;
+  const size_t es = m->rdt == HX_BF16 ? 2 : 4;
+  m->E1 = E + (sh ? 1 : 0);
+  std::vector<uint8_t> host((size_t)m->E1 * H * es);
+  auto fetch = [&](const void* src, int dt, int rows, uint8_t* dst) -> int {
+    const size_t sbytes = (size_t)rows * H * (dt == HX_BF16 ? 2 : 4);
+    std::vector<uint8_t> tmp(sbytes);
+    if (w->location == HX_HOST) memcpy(tmp.data(), src, sbytes);
+    else HX_HIP(hipMemcpy(tmp.data(), src, sbytes, hipMemcpyDeviceToHost));
+    if (dt == m->rdt) {
+      memcpy(dst, tmp.data(), sbytes);
+    } else {  // bf16 -> f32, exact
+      const uint16_t* s = (const uint16_t*)tmp.data();
+      float* d = (float*)dst;
+      for (size_t i = 0; i < (size_t)rows * H; i++) {
+        uint32_t u = (uint32_t)s[i] << 16;
+        memcpy(&d[i], &u, 4);
+      }
+    }
+    return HX_OK;
+  };
+  int rc = fetch(w->router, rd, E, host.data());
+  if (rc) return rc;
+  if (sh && (rc = fetch(w->shared_expert_gate, sd, 1, host.data() + (size_t)E * H * es))) return rc;
+  if (hipMalloc(&m->router, host.size()) != hipSuccess) return fail(HX_ERR_OUT_OF_MEMORY, "router allocation");
+  HX_HIP(hipMemcpy(m->router, host.data(), host.size(), hipMemcpyHostToDevice));
+  return HX_OK;
+}
+
+extern "C" int hx_moe_create(const hx_moe_config* cfg, const hx_moe_weights* w, int device, hx_moe** out) {
+  if (!cfg || !w || !out) return fail(HX_ERR_INVALID_ARGUMENT, "null argument");
+  *out = nullptr;
+  const hx_moe_config c = *cfg;
+  // moe.rs:56-69
+  if (c.num_experts <= 0 || c.num_experts_per_tok <= 0 || c.moe_intermediate_size <= 0)
+    return fail(HX_ERR_INVALID_ARGUMENT,
+                "MoE block needs num_experts (%d), num_experts_per_tok (%d) and moe_intermediate_size (%d) all > 0",
+                c.num_experts, c.num_experts_per_tok, c.moe_intermediate_size);
+  if (c.num_experts_per_tok > c.num_experts)
+    return fail(HX_ERR_INVALID_ARGUMENT, "num_experts_per_tok (%d) exceeds num_experts (%d)",
+                c.num_experts_per_tok, c.num_experts);
+  if (c.hidden_size <= 0 || c.shared_expert_intermediate_size < 0)
+    return fail(HX_ERR_INVALID_ARGUMENT, "bad hidden_size / shared_expert_intermediate_size");
+  if (c.num_experts > HX_MAX_EXPERTS || c.num_experts_per_tok > HX_MAX_TOPK)
+    return fail(HX_ERR_UNSUPPORTED, "at most %d experts and top-%d are supported", HX_MAX_EXPERTS, HX_MAX_TOPK);
+  if (c.act_dtype != HX_F32 && c.act_dtype != HX_BF16)
+    return fail(HX_ERR_UNSUPPORTED, "act_dtype must be HX_F32 or HX_BF16");
+  if (w->location != HX_HOST && w->location != HX_DEVICE)
+    return fail(HX_ERR_INVALID_ARGUMENT, "weights.location must be HX_HOST or HX_DEVICE");
+  const int H = c.hidden_size, I = c.moe_intermediate_size, Is = c.shared_expert_intermediate_size;
+  const bool sh = Is > 0;
+  int rc;
+  if ((rc = check_proj("experts.gate_proj", w->gate_dtype, H)) || (rc = check_proj("experts.up_proj", w->up_dtype, H)) ||
+      (rc = check_proj("experts.down_proj", w->down_dtype, I)))
+    return rc;
+  if (w->gate_dtype != w->up_dtype) return fail(HX_ERR_UNSUPPORTED, "gate_proj and up_proj must share a dtype");
+  if (sh) {
+    if ((rc = check_proj("shared_expert.gate_proj", w->shared_gate_dtype, H)) ||
+        (rc = check_proj("shared_expert.up_proj", w->shared_up_dtype, H)) ||
+        (rc = check_proj("shared_expert.down_proj", w->shared_down_dtype, Is)))
+      return rc;
+    if (w->shared_gate_dtype != w->gate_dtype || w->shared_up_dtype != w->up_dtype ||
+        w->shared_down_dtype != w->down_dtype)
+      return fail(HX_ERR_UNSUPPORTED, "the shared expert must use the routed experts' projection dtypes");
+    if (chunk_elems(w->down_dtype) && (I > Is ? I : Is) / chunk_elems(w->down_dtype) > 512)
+      return fail(HX_ERR_UNSUPPORTED, "intermediate size too large");
+  }
+  if (hipSetDevice(device) != hipSuccess) return fail(HX_ERR_DEVICE, "hipSetDevice(%d) failed", device);
+  hx_moe* m = new hx_moe();
+  m->cfg = c;
+  m->device = device;
+  const int E = c.num_experts;
+  if ((rc = build_router(m, w)) || (rc = upload_proj(m->gate, "experts.gate_proj", w->gate_dtype, w->experts_gate, w->location, E, I, H)) ||
+      (rc = upload_proj(m->up, "experts.up_proj", w->up_dtype, w->experts_up, w->location, E, I, H)) ||
+      (rc = upload_proj(m->down, "experts.down_proj", w->down_dtype, w->experts_down, w->location, E, H, I))) {
+    hx_moe_destroy(m);
+    return rc;
+  }
+  if (sh && ((rc = upload_proj(m->sgate, "shared_expert.gate_proj", w->shared_gate_dtype, w->shared_gate, w->location, 1, Is, H)) ||
+             (rc = upload_proj(m->sup, "shared_expert.up_proj", w->shared_up_dtype, w->shared_up, w->location, 1, Is, H)) ||
+             (rc = upload_proj(m->sdown, "shared_expert.down_proj", w->shared_down_dtype, w->shared_down, w->location, 1, H, Is)))) {
+    hx_moe_destroy(m);
+    return rc;
+  }
+  if (hipMalloc(&m->counter, 256) != hipSuccess) {
+    hx_moe_destroy(m);
+    return fail(HX_ERR_OUT_OF_MEMORY, "counter allocation");
+  }
+  if (hipMemset(m->counter, 0, 256) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
+    hx_moe_destroy(m);
+    return fail(HX_ERR_DEVICE, "counter initialisation");
+  }
+  *out = m;
+  return HX_OK;
+}
+
+extern "C" int hx_moe_workspace_size(const hx_moe* m, int64_t n_tokens, size_t* bytes) {
+  if (!m || !bytes || n_tokens < 0) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
+  *bytes = ws_layout(m, n_tokens).total;
+  return HX_OK;
+}
+
+// ----------------------------------------------------------------------------
+// forward
+// ----------------------------------------------------------------------------
+static int get_ws(hx_moe* m, int64_t T, void*& ws, size_t& ws_bytes, WsLayout& L) {
+  L = ws_layout(m, T);
+  if (ws) {
+    if (ws_bytes < L.total)
+      return fail(HX_ERR_WORKSPACE_TOO_SMALL, "workspace of %zu bytes, %zu needed for %lld tokens", ws_bytes,
+                  L.total, (long long)T);
+    return HX_OK;
+  }
+  if (m->own_ws_bytes < L.total) {
+    if (m->own_ws) {
+      HX_HIP(hipDeviceSynchronize());
+      (void)hipFree(m->own_ws);
+      m->own_ws = nullptr;
+      m->own_ws_bytes = 0;
+    }
+    if (hipMalloc(&m->own_ws, L.total) != hipSuccess)
+      return fail(HX_ERR_OUT_OF_MEMORY, "workspace allocation of %zu bytes", L.total);
+    m->own_ws_bytes = L.total;
+  }
+  ws = m->own_ws;
+  ws_bytes = m->own_ws_bytes;
+  return HX_OK;
+}
+
+struct Plan {
+  RouterArgs ra;
+  ExpertArgs ea;
+};
+
+static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws, const WsLayout& L,
+                      const float* bias, Plan& p) {
+  const hx_moe_config& c = m->cfg;
+  const int k = c.num_experts_per_tok, E = c.num_experts;
+  const int F = (int)(T * k);
+  RouterArgs& r = p.ra;
+  r = RouterArgs{};
+  r.x = x;
+  r.T = (int)T;
+  r.H = c.hidden_size;
+  r.R = m->router;
+  r.E1 = m->E1;
+  r.E = E;
+  r.k = k;
+  r.norm = c.norm_topk_prob != 0;
+  r.has_shared = c.shared_expert_intermediate_size > 0;
+  r.bias = bias;
+  r.logits = (float*)(ws + L.logits);
+  r.topk_w = (float*)(ws + L.topk_w);
+  r.sgw = (float*)(ws + L.sgw);
+  r.counter = m->counter;
+  DispatchArgs& d = r.d;
+  d.topk_idx = (int32_t*)(ws + L.topk_idx);
+  d.T = (int)T;
+  d.k = k;
+  d.E = E;
+  d.F = F;
+  d.has_shared = r.has_shared;
+  d.tile_m = HX_TILE_M;
+  d.perm = (int32_t*)(ws + L.perm);
+  d.inv = (int32_t*)(ws + L.inv);
+  d.offsets = (int32_t*)(ws + L.offsets);
+  d.slots = (int32_t*)(ws + L.slots);
+  d.tiles = (int32_t*)(ws + L.tiles);
+  d.counts = (int32_t*)(ws + L.counts);
+  ExpertArgs& a = p.ea;
+  a = ExpertArgs{};
+  a.gate = m->gate; a.up = m->up; a.down = m->down;
+  a.sgate = m->sgate; a.sup = m->sup; a.sdown = m->sdown;
+  a.E = E; a.k = k; a.H = c.hidden_size; a.I = c.moe_intermediate_size; a.Is = c.shared_expert_intermediate_size;
+  a.T = (int)T; a.F = F;
+  a.x = x;
+  a.xbf = c.act_dtype == HX_BF16;
+  a.perm = d.perm;
+  a.topk_w = r.topk_w;
+  a.sgw = r.sgw;
+  a.slots = d.slots;
+  a.tiles = d.tiles;
+  a.counts = d.counts;
+  a.hbuf = (float*)(ws + L.hbuf);
+  a.hstride = L.hstride;
+  a.hbf = L.hbf ? (uint16_t*)(ws + L.hbf) : nullptr;
+  a.obuf = L.obuf ? (void*)(ws + L.obuf) : nullptr;
+  a.inv = d.inv;
+  a.topk_idx = d.topk_idx;
+  a.y = y;
+  a.max_slots = L.max_slots;
+  a.max_tiles = L.max_tiles;
+}
+
+// event helpers for the optional per-kernel timing
+static void tm_mark(hx_moe* m, int slot, int which, hipStream_t s) {
+  Timing& t = m->tm;
+  if (!t.on || t.calls >= t.max_calls) return;
+  (void)hipEventRecord(t.ev[((size_t)t.calls * N_SLOTS + slot) * 2 + which], s);
+  if (which == 1) t.used[(size_t)t.calls * N_SLOTS + slot] = 1;
+}
+
+static int run_routing(hx_moe* m, Plan& p, bool decode, hipStream_t s) {
+  const bool xbf = m->cfg.act_dtype == HX_BF16, rbf = m->rdt == HX_BF16;
+  tm_mark(m, SLOT_ROUTER, 0, s);
+  launch_router(p.ra, xbf, rbf, decode, s);
+  tm_mark(m, SLOT_ROUTER, 1, s);
+  HX_HIP(hipGetLastError());
+  if (!decode) {
+    tm_mark(m, SLOT_ROUTE_TOKENS, 0, s);
+    launch_route_tokens(p.ra, s);
+    tm_mark(m, SLOT_ROUTE_TOKENS, 1, s);
+    HX_HIP(hipGetLastError());
+    tm_mark(m, SLOT_DISPATCH, 0, s);
+    launch_dispatch(p.ra.d, s);
+    tm_mark(m, SLOT_DISPATCH, 1, s);
+    HX_HIP(hipGetLastError());
+  }
+  return HX_OK;
+}
+
+static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, size_t ws_bytes,
+                        const float* bias, hipStream_t s) {
+  WsLayout L;
+  int rc = get_ws(m, T, ws, ws_bytes, L);
+  if (rc) return rc;
+  Plan p;
+  make_plan(m, x, T, y, (uint8_t*)ws, L, bias, p);
+  const bool decode = T <= HX_DECODE_MAX_T;
+  if ((rc = run_routing(m, p, decode, s))) return rc;
+  if (decode) {
+    tm_mark(m, SLOT_GATE_UP, 0, s);
+    HX_HIP(launch_gate_up_gemv(p.ea, s));
+    tm_mark(m, SLOT_GATE_UP, 1, s);
+    tm_mark(m, SLOT_DOWN, 0, s);
+    HX_HIP(launch_down_gemv_combine(p.ea, s));
+    tm_mark(m, SLOT_DOWN, 1, s);
+  } else {
+    tm_mark(m, SLOT_GATE_UP, 0, s);
+    HX_HIP(launch_gate_up_prefill(p.ea, s));
+    tm_mark(m, SLOT_GATE_UP, 1, s);
+    tm_mark(m, SLOT_DOWN, 0, s);
+    HX_HIP(launch_down_prefill(p.ea, s));
+    tm_mark(m, SLOT_DOWN, 1, s);
+    tm_mark(m, SLOT_COMBINE, 0, s);
+    HX_HIP(launch_combine(p.ea, s));
+    tm_mark(m, SLOT_COMBINE, 1, s);
+  }
+  if (m->tm.on && m->tm.calls < m->tm.max_calls) m->tm.calls++;
+  return HX_OK;
+}
+
+extern "C" int hx_moe_forward(hx_moe* m, const void* x, int64_t n_tokens, void* y, void* workspace,
+                              size_t workspace_bytes, const float* router_bias, void* stream) {
+  if (!m || n_tokens < 0 || (n_tokens > 0 && (!x || !y))) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
+  if (n_tokens == 0) return HX_OK;
+  if (n_tokens > (int64_t)1 << 24) return fail(HX_ERR_UNSUPPORTED, "too many tokens in one call");
+  HX_HIP(hipSetDevice(m->device));
+  return forward_impl(m, x, n_tokens, y, workspace, workspace_bytes, router_bias, (hipStream_t)stream);
+}
+
+extern "C" int hx_moe_forward_host(hx_moe* m, const void* x_host, int64_t n_tokens, void* y_host,
+                                   const float* router_bias_host) {
+  if (!m || n_tokens < 0 || (n_tokens > 0 && (!x_host || !y_host)))
+    return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
+  if (n_tokens == 0) return HX_OK;
+  HX_HIP(hipSetDevice(m->device));
+  const size_t bytes = (size_t)n_tokens * m->cfg.hidden_size * (m->cfg.act_dtype == HX_BF16 ? 2 : 4);
+  void *dx = nullptr, *dy = nullptr;
+  float* db = nullptr;
+  int rc = HX_OK;
+  if (hipMalloc(&dx, bytes) != hipSuccess || hipMalloc(&dy, bytes) != hipSuccess ||
+      (router_bias_host && hipMalloc((void**)&db, sizeof(float) * m->cfg.num_experts) != hipSuccess)) {
+    rc = fail(HX_ERR_OUT_OF_MEMORY, "staging allocation");
+  } else if (hipMemcpy(dx, x_host, bytes, hipMemcpyHostToDevice) != hipSuccess ||
+             (db && hipMemcpy(db, router_bias_host, sizeof(float) * m->cfg.num_experts, hipMemcpyHostToDevice) !=
+                        hipSuccess)) {
+    rc = fail(HX_ERR_DEVICE, "copy to device failed");
+  } else if ((rc = forward_impl(m, dx, n_tokens, dy, nullptr, 0, db, 0)) == HX_OK) {
+    if (hipMemcpy(y_host, dy, bytes, hipMemcpyDeviceToHost) != hipSuccess) rc = fail(HX_ERR_DEVICE, "copy to host failed");
+  }
+  if (dx) (void)hipFree(dx);
+  if (dy) (void)hipFree(dy);
+  if (db) (void)hipFree(db);
+  return rc;
+}
+
+extern "C" int hx_moe_route(hx_moe* m, const void* x, int64_t n_tokens, const float* router_bias, int32_t* topk_idx,
+                            float* topk_w, int32_t* perm, int32_t* offsets, int32_t* inv, void* workspace,
+                            size_t workspace_bytes, void* stream) {
+  if (!m || n_tokens < 0 || (n_tokens > 0 && !x)) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
+  if (n_tokens == 0) return HX_OK;
+  HX_HIP(hipSetDevice(m->device));
+  hipStream_t s = (hipStream_t)stream;
+  WsLayout L;
+  int rc = get_ws(m, n_tokens, workspace, workspace_bytes, L);
+  if (rc) return rc;
+  Plan p;
+  make_plan(m, x, n_tokens, nullptr, (uint8_t*)workspace, L, router_bias, p);
+  if ((rc = run_routing(m, p, n_tokens <= HX_DECODE_MAX_T, s))) return rc;
+  const int64_t F = n_tokens * m->cfg.num_experts_per_tok;
+  if (topk_idx) HX_HIP(hipMemcpyAsync(topk_idx, p.ra.d.topk_idx, 4 * F, hipMemcpyDeviceToDevice, s));
+  if (topk_w) HX_HIP(hipMemcpyAsync(topk_w, p.ra.topk_w, 4 * F, hipMemcpyDeviceToDevice, s));
+  if (perm) HX_HIP(hipMemcpyAsync(perm, p.ra.d.perm, 4 * F, hipMemcpyDeviceToDevice, s));
+  if (inv) HX_HIP(hipMemcpyAsync(inv, p.ra.d.inv, 4 * F, hipMemcpyDeviceToDevice, s));
+  if (offsets)
+    HX_HIP(hipMemcpyAsync(offsets, p.ra.d.offsets, 4 * (m->cfg.num_experts + 1), hipMemcpyDeviceToDevice, s));
+  return HX_OK;
+}
+
+extern "C" int hx_moe_router_logits(hx_moe* m, const void* x, int64_t n_tokens, const float* router_bias,
+                                    float* logits, void* stream) {
+  if (!m || n_tokens < 0 || (n_tokens > 0 && (!x || !logits))) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
+  if (n_tokens == 0) return HX_OK;
+  HX_HIP(hipSetDevice(m->device));
+  hipStream_t s = (hipStream_t)stream;
+  void* ws = nullptr;
+  size_t wsb = 0;
+  WsLayout L;
+  int rc = get_ws(m, n_tokens, ws, wsb, L);
+  if (rc) return rc;
+  Plan p;
+  make_plan(m, x, n_tokens, nullptr, (uint8_t*)ws, L, router_bias, p);
+  launch_router(p.ra, m->cfg.act_dtype == HX_BF16, m->rdt == HX_BF16, false, s);
+  HX_HIP(hipGetLastError());
+  const int E = m->cfg.num_experts, E1 = m->E1;
+  HX_HIP(hipMemcpy2DAsync(logits, sizeof(float) * E, p.ra.logits, sizeof(float) * E1, sizeof(float) * E, n_tokens,
+                          hipMemcpyDeviceToDevice, s));
+  return HX_OK;
+}
+
+extern "C" int hx_moe_decoder_mlp(hx_moe* m, void* x, int64_t n_tokens, const float* norm_w, float eps,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  if (!m || n_tokens < 0 || (n_tokens > 0 && (!x || !norm_w))) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
+  if (n_tokens == 0) return HX_OK;
+  HX_HIP(hipSetDevice(m->device));
+  hipStream_t s = (hipStream_t)stream;
+  WsLayout L;
+  int rc = get_ws(m, n_tokens, workspace, workspace_bytes, L);
+  if (rc) return rc;
+  uint8_t* ws = (uint8_t*)workspace;
+  const bool bf = m->cfg.act_dtype == HX_BF16;
+  const int64_t H = m->cfg.hidden_size;
+  HX_HIP(launch_rmsnorm(x, bf, n_tokens, H, norm_w, eps, ws + L.xn, s));
+  if ((rc = forward_impl(m, ws + L.xn, n_tokens, ws + L.ym, workspace, workspace_bytes, nullptr, s))) return rc;
+  HX_HIP(launch_residual_add(x, ws + L.ym, bf, n_tokens * H, s));
+  return HX_OK;
+}
+
+extern "C" int hx_quantize(int dtype, const float* src, int64_t rows, int64_t cols, void* dst, void* stream) {
+  if (!src || !dst || rows < 0) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
+  if (dtype != HX_Q8_0 && dtype != HX_Q4_K && dtype != HX_Q6_K && dtype != HX_BF16 && dtype != HX_F16)
+    return fail(HX_ERR_UNSUPPORTED, "hx_quantize: dtype %d", dtype);
+  if (hx_row_bytes(dtype, cols) < 0)
+    return fail(HX_ERR_INVALID_ARGUMENT, "hx_quantize: %lld columns do not tile into dtype %d blocks", (long long)cols, dtype);
+  if (rows == 0) return HX_OK;
+  HX_HIP(launch_quantize(dtype, src, rows, cols, dst, (hipStream_t)stream));
+  return HX_OK;
+}
+
+extern "C" int hx_dequantize(int dtype, const void* src, int64_t rows, int64_t cols, float* dst, void* stream) {
+  if (!src || !dst || rows < 0) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
+  if (hx_row_bytes(dtype, cols) < 0)
+    return fail(HX_ERR_INVALID_ARGUMENT, "hx_dequantize: %lld columns do not tile into dtype %d blocks", (long long)cols, dtype);
+  if (rows == 0) return HX_OK;
+  HX_HIP(launch_dequantize(dtype, src, rows, cols, dst, (hipStream_t)stream));
+  return HX_OK;
+}
+
+// ----------------------------------------------------------------------------
+// timing
+// ----------------------------------------------------------------------------
+extern "C" int hx_moe_timing_begin(hx_moe* m, int max_calls) {
+  if (!m || max_calls <= 0) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
+  HX_HIP(hipSetDevice(m->device));
+  Timing& t = m->tm;
+  const size_t need = (size_t)max_calls * N_SLOTS * 2;
+  while (t.ev.size() < need) {
+    hipEvent_t e;
+    HX_HIP(hipEventCreate(&e));
+    t.ev.push_back(e);
+  }
+  t.used.assign((size_t)max_calls * N_SLOTS, 0);
+  t.max_calls = max_calls;
+  t.calls = 0;
+  t.on = true;
+  return HX_OK;
+}
+
+extern "C" int hx_moe_timing_end(hx_moe* m, double* ms, int64_t* launches, int* n_slots) {
+  if (!m || !ms || !launches || !n_slots) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
+  Timing& t = m->tm;
+  const int cap = *n_slots;
+  *n_slots = N_SLOTS;
+  if (cap < N_SLOTS) return fail(HX_ERR_INVALID_ARGUMENT, "need room for %d slots", N_SLOTS);
+  HX_HIP(hipSetDevice(m->device));
+  for (int i = 0; i < N_SLOTS; i++) {
+    ms[i] = 0.0;
+    launches[i] = 0;
+  }
+  for (int c = 0; c < t.calls; c++)
+    for (int i = 0; i < N_SLOTS; i++) {
+      if (!t.used[(size_t)c * N_SLOTS + i]) continue;
+      hipEvent_t a = t.ev[((size_t)c * N_SLOTS + i) * 2], b = t.ev[((size_t)c * N_SLOTS + i) * 2 + 1];
+      HX_HIP(hipEventSynchronize(b));
+      float v = 0.f;
+      HX_HIP(hipEventElapsedTime(&v, a, b));
+      ms[i] += v;
+      launches[i]++;
+    }
+  t.on = false;
+  t.calls = 0;
+  return HX_OK;
+}
+
+extern "C" const char* hx_moe_timing_name(int slot) {
+  return slot >= 0 && slot < N_SLOTS ? kSlotNames[slot] : "";
+}

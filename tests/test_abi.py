@@ -1,0 +1,56 @@
+"""CPU checks of the boundary: libhxmoe.so loads, exports every entry point
+include/hx_moe.h declares, and the host-only helpers answer without a GPU."""
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_functions():
+    text = open(os.path.join(ROOT, "include", "hx_moe.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?(?:int|int64_t|char|void)\s*\**\s*(hx_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_python_export_list():
+    from helexa_amd.moe import EXPORTS
+    assert declared_functions() == sorted(EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    import ctypes
+    from helexa_amd.moe import LIB_PATH
+    if not os.path.exists(LIB_PATH):
+        pytest.skip("libhxmoe.so not built")
+    L = ctypes.CDLL(LIB_PATH)
+    missing = [n for n in declared_functions() if not hasattr(L, n)]
+    assert not missing, missing
+
+
+def test_host_helpers():
+    import helexa_amd as hx
+    assert hx.row_bytes(hx.Q8_0, 2048) == 2176
+    assert hx.row_bytes(hx.Q4_K, 2048) == 1152
+    assert hx.row_bytes(hx.Q6_K, 512) == 420
+    assert hx.row_bytes(hx.Q6_K, 100) == -1
+    assert hx.moe.last_error() == ""
+
+
+def test_text_config_from_config_json_and_layer_uses_moe():
+    """mod.rs:1160-1230 / 1358-1378: the 80B-A3B flat config parses to E=512, k=10,
+    I=512, shared 512, norm on, every layer MoE; the step / exclusion rules."""
+    from helexa_amd.moe import TextConfig
+    cfg = TextConfig.from_config_json('{"model_type": "qwen3_next", "hidden_size": 2048, "num_experts": 512, '
+                                      '"num_experts_per_tok": 10, "moe_intermediate_size": 512, '
+                                      '"shared_expert_intermediate_size": 512, "norm_topk_prob": true, '
+                                      '"decoder_sparse_step": 1, "mlp_only_layers": [], "num_hidden_layers": 48}')
+    assert (cfg.num_experts, cfg.num_experts_per_tok, cfg.moe_intermediate_size,
+            cfg.shared_expert_intermediate_size, cfg.norm_topk_prob) == (512, 10, 512, 512, True)
+    assert all(cfg.layer_uses_moe(i) for i in range(48))
+    cfg2 = TextConfig(hidden_size=8, num_experts=4, decoder_sparse_step=2, mlp_only_layers=[3])
+    assert [cfg2.layer_uses_moe(i) for i in range(6)] == [False, True, False, False, False, True]
+    assert not TextConfig(hidden_size=8).layer_uses_moe(0)
+    nested = TextConfig.from_config_json('{"model_type": "qwen3_5_moe", "text_config": {"hidden_size": 64, '
+                                         '"num_experts": 8, "num_experts_per_tok": 2}}')
+    assert nested.num_experts == 8 and nested.hidden_size == 64

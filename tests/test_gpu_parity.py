@@ -1,0 +1,265 @@
+"""GPU parity: libhxmoe.so (through its C ABI) against the CPU oracle on the same
+seeded inputs. Routing (logits, top-k ids and weights, dispatch permutation) is
+bit-exact; outputs are within max|y-r|/max|r| <= 1e-2 for bf16 activations and
+<= 1e-4 for f32."""
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+
+from oracle import oracle as O  # noqa: E402
+from tests.common import rel_err  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+TOL_BF16, TOL_F32 = 1e-2, 1e-4
+
+
+def _hx():
+    import helexa_amd as hx
+    from helexa_amd import synth
+    return hx, synth
+
+
+def oracle_for(cfg, wnp, act):
+    return O.OracleMoe(cfg.hidden_size, cfg.num_experts, cfg.num_experts_per_tok, cfg.moe_intermediate_size,
+                       cfg.shared_expert_intermediate_size, cfg.norm_topk_prob, act, wnp)
+
+
+def x_np(x):
+    x = x.detach().cpu().contiguous()
+    return x.view(torch.int16).numpy().view(np.uint16) if x.dtype == torch.bfloat16 else x.numpy()
+
+
+class Case:
+    def __init__(self, cfg, fmt, seed, act):
+        hx, synth = _hx()
+        print(f"[case] H={cfg.hidden_size} E={cfg.num_experts} k={cfg.num_experts_per_tok} "
+              f"I={cfg.moe_intermediate_size} fmt={fmt['gate']}/{fmt['down']} seed={seed}", flush=True)
+        self.cfg, self.act, self.seed = cfg, act, seed
+        self.w = synth.make_weights(cfg, fmt, seed)
+        self.block = hx.Qwen3_5MoeBlock.load(cfg, self.w, act_dtype=act)
+        self.wnp = synth.to_numpy(self.w)
+        self.oracle = oracle_for(cfg, self.wnp, act)
+
+    def x(self, T, seed=0):
+        _, synth = _hx()
+        return synth.make_x(self.cfg, T, self.seed * 1000 + seed, self.act)
+
+
+@pytest.fixture(scope="module")
+def c1():
+    _, synth = _hx()
+    return Case(synth.C1, synth.FMT_F32, 2024, O.F32)
+
+
+@pytest.fixture(scope="module")
+def router_case():
+    """A3B router shape (hidden 2048, 512 experts, top-10) with thin bf16 experts"""
+    hx, synth = _hx()
+    cfg = hx.TextConfig(hidden_size=2048, num_experts=512, num_experts_per_tok=10, moe_intermediate_size=64,
+                        shared_expert_intermediate_size=64, norm_topk_prob=True)
+    return Case(cfg, synth.FMT_BF16, 31, O.BF16)
+
+
+@pytest.fixture(scope="module")
+def c2():
+    _, synth = _hx()
+    return Case(synth.A3B, synth.FMT_Q8_0, 7, O.BF16)
+
+
+# ------------------------------------------------------------------ weights
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_K, O.Q6_K, O.BF16])
+def test_device_quantiser_matches_oracle_bytes(dt):
+    hx, _ = _hx()
+    g = torch.Generator(device="cuda").manual_seed(5)
+    w = torch.randn((96, 2048), generator=g, device="cuda") * 0.02
+    w[3, :256] = 0.0                                  # all-zero blocks
+    w[4, :32] = 1e-3                                  # constant block
+    q = hx.quantize(dt, w).cpu().numpy()
+    ref = O.quantize(dt, w.cpu().numpy())
+    assert np.array_equal(q.reshape(-1), ref.reshape(-1))
+
+
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_K, O.Q6_K])
+def test_device_dequantiser_matches_oracle(dt):
+    hx, _ = _hx()
+    g = torch.Generator(device="cuda").manual_seed(6)
+    w = torch.randn((64, 512), generator=g, device="cuda") * 0.02
+    q = hx.quantize(dt, w)
+    got = hx.dequantize(dt, q, 512).cpu().numpy()
+    ref = O.dequantize(dt, q.cpu().numpy(), 512)
+    assert np.array_equal(got, ref)
+
+
+# ------------------------------------------------------------------ routing
+@pytest.mark.parametrize("T", [1, 3, 8, 9, 300])
+def test_router_logits_bit_exact(router_case, T):
+    c = router_case
+    x = c.x(T, seed=T)
+    got = c.block.router_logits(x).cpu().numpy()
+    ref = c.oracle.logits(x_np(x))
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [1, 2, 8, 9, 64, 1000])
+def test_routing_and_dispatch_bit_exact(router_case, T):
+    c = router_case
+    x = c.x(T, seed=100 + T)
+    r = c.block.route(x)
+    _, _, ix, wt = c.oracle.route(x_np(x))
+    assert np.array_equal(r["topk_idx"].cpu().numpy(), ix)
+    assert np.array_equal(r["topk_w"].cpu().numpy().view(np.uint32), wt.view(np.uint32))
+    perm, offs, inv = O.dispatch(ix, c.cfg.num_experts)
+    assert np.array_equal(r["perm"].cpu().numpy(), perm)
+    assert np.array_equal(r["offsets"].cpu().numpy(), offs)
+    assert np.array_equal(r["inv"].cpu().numpy(), inv)
+
+
+def test_routing_ties_break_to_lower_id():
+    """Duplicate router rows give exactly tied logits; the lower id must win."""
+    hx, synth = _hx()
+    cfg = hx.TextConfig(hidden_size=256, num_experts=64, num_experts_per_tok=6, moe_intermediate_size=32,
+                        shared_expert_intermediate_size=0, norm_topk_prob=True)
+    w = synth.make_weights(cfg, synth.FMT_BF16, 9)
+    r = w["router"][1]
+    r[32:] = r[:32]                                   # expert 32+i ties expert i
+    blk = hx.Qwen3_5MoeBlock.load(cfg, w, act_dtype=hx.BF16)
+    x = synth.make_x(cfg, 200, 9)
+    got = blk.route(x)["topk_idx"].cpu().numpy()
+    o = oracle_for(cfg, synth.to_numpy(w), O.BF16)
+    ref = o.route(x_np(x))[2]
+    assert np.array_equal(got, ref)
+    # a twin 32+i is only ever picked together with i, and ranks right after it
+    for row in got:
+        for j, e in enumerate(row):
+            if e >= 32:
+                assert e - 32 in row[:j], row
+
+
+def test_router_bias_hook(router_case):
+    c = router_case
+    _, synth = _hx()
+    bias = synth.zipf_bias(c.cfg.num_experts, 1.1, 1.0, 3)
+    x = c.x(40, seed=77)
+    r = c.block.route(x, router_bias=bias)
+    _, _, ix, wt = c.oracle.route(x_np(x), bias=bias.cpu().numpy())
+    assert np.array_equal(r["topk_idx"].cpu().numpy(), ix)
+    assert np.array_equal(r["topk_w"].cpu().numpy(), wt)
+
+
+# ------------------------------------------------------------------ forward
+@pytest.mark.parametrize("T", [1, 4, 8, 32])
+def test_forward_c1_f32(c1, T):
+    x = c1.x(T, seed=T)
+    got = c1.block.forward(x).cpu().numpy()
+    ref = c1.oracle.forward(x_np(x))
+    assert rel_err(got, ref) <= TOL_F32
+
+
+def test_forward_c1_matches_transformers_golden(c1):
+    """the C1 block at the golden fixture's seed, end to end on the GPU"""
+    import os
+    hx, synth = _hx()
+    g = np.load(os.path.join(os.path.dirname(__file__), "golden", "c1_transformers.npz"))
+    from tests.common import make_f32_block, make_x
+    cfg = synth.C1
+    w = make_f32_block(int(g["seed"]), cfg.hidden_size, cfg.num_experts, cfg.moe_intermediate_size,
+                       cfg.shared_expert_intermediate_size)
+    dev = {k: (hx.F32, torch.from_numpy(v).cuda()) for k, v in w.items()}
+    blk = hx.Qwen3_5MoeBlock.load(cfg, dev, act_dtype=hx.F32)
+    x = torch.from_numpy(make_x(int(g["seed"]), 32, cfg.hidden_size)).cuda()
+    r = blk.route(x)
+    assert np.array_equal(r["topk_idx"].cpu().numpy(), g["topk_idx"])
+    assert rel_err(blk.forward(x).cpu().numpy(), g["y"]) <= TOL_F32
+    xs3 = x.reshape(1, 32, cfg.hidden_size)                     # (b, l, hidden) in, same shape out
+    assert blk.forward(xs3).shape == xs3.shape
+
+
+@pytest.mark.parametrize("T", [1, 4, 8])
+def test_forward_c2_decode_q8_0(c2, T):
+    x = c2.x(T, seed=T)
+    got = c2.block.forward(x).float().cpu().numpy()
+    ref = c2.oracle.forward(x_np(x))
+    assert rel_err(got, ref) <= TOL_BF16
+
+
+def test_forward_q4_k_m_prefill_sampled_tokens():
+    hx, synth = _hx()
+    c = Case(synth.A3B, synth.FMT_Q4_K_M, 11, O.BF16)
+    T = 2048
+    x = c.x(T, seed=5)
+    y = c.block.forward(x)
+    r = c.block.route(x)
+    _, _, ix, _ = c.oracle.route(x_np(x))
+    assert np.array_equal(r["topk_idx"].cpu().numpy(), ix)
+    sample = np.linspace(0, T - 1, 12).astype(int)
+    ref = c.oracle.forward(x_np(x)[sample])
+    assert rel_err(y.float().cpu().numpy()[sample], ref) <= TOL_BF16
+    # the decode path on the same block
+    xd = c.x(3, seed=6)
+    assert rel_err(c.block.forward(xd).float().cpu().numpy(), c.oracle.forward(x_np(xd))) <= TOL_BF16
+
+
+def test_forward_host_entry_matches_device(c1):
+    import ctypes as C
+    hx, _ = _hx()
+    x = c1.x(5, seed=3)
+    dev = c1.block.forward(x).cpu().numpy()
+    xh = x.cpu().numpy()
+    yh = np.empty_like(xh)
+    hx.moe.check(hx.lib().hx_moe_forward_host(c1.block.handle, xh.ctypes.data_as(C.c_void_p), 5,
+                                              yh.ctypes.data_as(C.c_void_p), None), "forward_host")
+    assert np.array_equal(dev, yh)
+
+
+def test_decoder_mlp_residual(c1):
+    hx, _ = _hx()
+    x = c1.x(6, seed=4)
+    w = torch.linspace(-0.5, 0.5, c1.cfg.hidden_size, device="cuda")
+    ref_n = O.rmsnorm(x_np(x), w.cpu().numpy(), 1e-6, O.F32)
+    ref = x_np(x) + c1.oracle.forward(ref_n)
+    got = c1.block.decoder_mlp_(x.clone(), w, 1e-6).cpu().numpy()
+    assert rel_err(got, ref) <= TOL_F32
+
+
+# ------------------------------------------------------------------ edges / errors
+def test_zero_tokens_is_noop(c1):
+    x = torch.empty((0, c1.cfg.hidden_size), device="cuda")
+    assert c1.block.forward(x).shape == (0, c1.cfg.hidden_size)
+
+
+def test_workspace_too_small_is_an_error(c1):
+    hx, _ = _hx()
+    ws = torch.empty(16, dtype=torch.uint8, device="cuda")
+    with pytest.raises(hx.HxError) as e:
+        c1.block.forward(c1.x(4), workspace=ws)
+    assert e.value.code == 4
+
+
+def test_caller_workspace_and_stream(c1):
+    x = c1.x(20, seed=8)
+    ref = c1.block.forward(x)
+    ws = torch.empty(c1.block.workspace_size(20), dtype=torch.uint8, device="cuda")
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        y = c1.block.forward(x, workspace=ws, stream=s)
+    s.synchronize()
+    assert torch.equal(y, ref)
+
+
+def test_invalid_configs_are_rejected():
+    hx, synth = _hx()
+    w = synth.make_weights(synth.C1, synth.FMT_F32, 1)
+    bad = hx.TextConfig(hidden_size=256, num_experts=16, num_experts_per_tok=17, moe_intermediate_size=128,
+                        shared_expert_intermediate_size=128, norm_topk_prob=True)
+    with pytest.raises(hx.HxError) as e:
+        hx.Qwen3_5MoeBlock.load(bad, w, act_dtype=hx.F32)
+    assert e.value.code == 1 and "exceeds num_experts" in str(e.value)
+    qcfg = hx.TextConfig(hidden_size=256, num_experts=16, num_experts_per_tok=4, moe_intermediate_size=128,
+                         shared_expert_intermediate_size=128, norm_topk_prob=True)
+    wq = dict(w)
+    wq["down"] = (hx.Q6_K, torch.zeros((16, 256, 10), dtype=torch.uint8, device="cuda"))  # I=128 not /256
+    with pytest.raises(hx.HxError) as e:
+        hx.Qwen3_5MoeBlock.load(qcfg, wq, act_dtype=hx.F32)
+    assert e.value.code == 1
