@@ -1,0 +1,284 @@
+"""Benchmark: Qwen3-Next-80B-A3B sparse-MoE layer on one MI355X.
+
+Headline (the JSON `value`): C2 -- one MoE-layer decode step (T=1, hidden 2048,
+512 experts, top-10 renormalised, intermediate 512, shared expert 512 with its
+sigmoid gate; experts and shared expert GGUF Q8_0 from seeded N(0,0.02), router
+and shared gate bf16, activations bf16 N(0,1)), in microseconds per layer.
+
+Method
+  * L distinct layers (default 16, each its own 1.7 GB Q8_0 expert stack) are
+    generated on the device and rotated, with a different token per step, so
+    the ~37 MB a step touches is never still resident in the 256 MB Infinity
+    Cache when that layer comes round again.
+  * The steps are captured into one HIP graph (the library launches three
+    kernels per decode step on the capturing stream) and the graph is replayed;
+    the timed region is bracketed by torch.cuda.synchronize() on both sides.
+  * Kernel durations for the roofline come from HIP events the library records
+    around each of its kernels (hx_moe_timing_*), captured into a second graph
+    of the same steps and read after each replay.
+  * Algorithmic bytes per step are computed from the actual routing (unique
+    experts touched) and the GGUF sizes of what must be read once.
+  * cpu_baseline: the CPU restatement of the reference's candle path (oracle/)
+    on the host cores, on a bounded sample of the same workload.
+  * `prefill` (secondary): C3, 2048 tokens of the same layer in Q4_K_M (gate/up
+    Q4_K, down Q6_K), tokens/s with its MFMA and HBM fractions.
+
+    python bench.py [--steps K] [--warmup W] [--layers L] [--no-cpu] [--no-prefill]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
+MFMA_BF16_PEAK_TFS = 2516.6     # dense bf16: 256 CU x 4096 flop/clk x 2.4 GHz
+METRIC = "MoE-layer decode µs + % HBM peak; prefill tok/s + % MFMA peak (Q4_K_M)"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gguf_bytes(fmt, rows, cols):
+    from helexa_amd import row_bytes
+    return rows * row_bytes(fmt, cols)
+
+
+def step_bytes(cfg, fmts, unique_experts, T):
+    """algorithmic HBM bytes of one forward (every touched weight byte once, the
+    tokens in and out once) and per kernel (each kernel's weights plus the
+    activations it must read or write)"""
+    H, E, I, Is = cfg.hidden_size, cfg.num_experts, cfg.moe_intermediate_size, cfg.shared_expert_intermediate_size
+    act = T * H * 2
+    router_w = (E + 1) * H * 2                  # router rows + shared-expert gate row, bf16
+    gate_up_w = (unique_experts * (gguf_bytes(fmts["gate"], I, H) + gguf_bytes(fmts["up"], I, H))
+                 + gguf_bytes(fmts["sgate"], Is, H) + gguf_bytes(fmts["sup"], Is, H))
+    down_w = unique_experts * gguf_bytes(fmts["down"], H, I) + gguf_bytes(fmts["sdown"], H, Is)
+    total = router_w + gate_up_w + down_w + 2 * act
+    return total, {"router": router_w + act, "gate_up": gate_up_w + act, "down": down_w + act}
+
+
+def build_layers(cfg, fmts, n_layers, seed, keep_host_copy_of_first=False):
+    import torch
+    import helexa_amd as hx
+    from helexa_amd import synth
+    blocks, host0 = [], None
+    for i in range(n_layers):
+        w = synth.make_weights(cfg, fmts, seed + i)
+        blocks.append(hx.Qwen3_5MoeBlock.load(cfg, w, act_dtype=hx.BF16))
+        if i == 0 and keep_host_copy_of_first:
+            host0 = synth.to_numpy(w)
+        del w
+        torch.cuda.synchronize()
+    return blocks, host0
+
+
+def capture(blocks, xs, ys, wss, n_steps, timing=False):
+    """one HIP graph holding n_steps decode steps, step s on layer s % L"""
+    import torch
+    L = len(blocks)
+    if timing:
+        for b in blocks:
+            b.timing_begin((n_steps + L - 1) // L)
+    g = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            for i in range(n_steps):
+                blocks[i % L].forward(xs[i % len(xs)], workspace=wss[i % L], stream=s, out=ys[i % len(ys)])
+    torch.cuda.current_stream().wait_stream(s)
+    return g
+
+
+def bench_decode(args):
+    import numpy as np
+    import torch
+    import helexa_amd as hx
+    from helexa_amd import synth
+
+    cfg, fmts = synth.A3B, synth.FMT_Q8_0
+    log(f"[bench] building {args.layers} Q8_0 layers")
+    t0 = time.time()
+    blocks, host0 = build_layers(cfg, fmts, args.layers, 1000, keep_host_copy_of_first=not args.no_cpu)
+    log(f"[bench] layers ready in {time.time() - t0:.1f}s")
+    n_x = 64
+    xs = [synth.make_x(cfg, 1, 50 + i) for i in range(n_x)]
+    ys = [torch.empty_like(xs[0]) for _ in range(n_x)]
+    wss = [torch.empty(b.workspace_size(1), dtype=torch.uint8, device="cuda") for b in blocks]
+
+    # routing of the measured steps -> unique experts per step
+    uniq = []
+    for i in range(n_x):
+        idx = blocks[i % len(blocks)].route(xs[i])["topk_idx"]
+        uniq.append(int(torch.unique(idx).numel()))
+    U = float(np.mean(uniq))
+    total_bytes, kbytes = step_bytes(cfg, fmts, U, 1)
+
+    G = 256                                     # steps per graph
+    g = capture(blocks, xs, ys, wss, G)
+    for _ in range(max(1, args.warmup // G)):
+        g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, args.steps // G)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    steps = reps * G
+    us_per_layer = dt / steps * 1e6
+
+    # per-kernel durations: the same steps launched eagerly with the library's HIP
+    # events around each kernel, queued behind a ~30 ms sleep kernel so that the
+    # GPU runs them back to back (no host launch gaps inside an event pair)
+    kern = {}
+    n_t = min(G, 256)
+    for _ in range(max(1, min(reps, 4))):
+        for b in blocks:
+            b.timing_begin((n_t + len(blocks) - 1) // len(blocks))
+        torch.cuda._sleep(int(2.4e9 * 0.03))
+        for i in range(n_t):
+            blocks[i % len(blocks)].forward(xs[i % len(xs)], workspace=wss[i % len(blocks)], out=ys[i % len(ys)])
+        torch.cuda.synchronize()
+        for b in blocks:
+            for name, (ms, n) in b.timing_end().items():
+                if n:
+                    a = kern.setdefault(name, [0.0, 0])
+                    a[0] += ms
+                    a[1] += n
+    kern_us = {k: v[0] / v[1] * 1e3 for k, v in kern.items()}
+    dominant = max(("gate_up", "down"), key=lambda k: kbytes[k])
+    d_us = kern_us.get(dominant, float("nan"))
+    achieved = kbytes[dominant] / (d_us * 1e-6) / 1e9
+    layer_gbs = total_bytes / (us_per_layer * 1e-6) / 1e9
+
+    # the graph's last write of ys[0] came from layer 0 on xs[0]: it must equal an
+    # eager forward bit for bit
+    graph_ok = bool(torch.equal(blocks[0].forward(xs[0]), ys[0]))
+
+    out = {
+        "metric": METRIC, "value": round(us_per_layer, 3), "unit": "us/layer (C2 decode)",
+        "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(us_per_layer / 1e3, 6),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded N(0,0.02) weights quantised to GGUF Q8_0 on device; bf16 N(0,1) tokens)",
+        "config": {"workload": "C2: Qwen3-Next-80B-A3B MoE layer decode, T=1, Q8_0 experts, bf16 router+acts",
+                   "hidden": cfg.hidden_size, "experts": cfg.num_experts, "top_k": cfg.num_experts_per_tok,
+                   "moe_intermediate": cfg.moe_intermediate_size,
+                   "shared_intermediate": cfg.shared_expert_intermediate_size,
+                   "layers_rotated": args.layers, "unique_experts_per_step": U,
+                   "graph_steps": G, "kernels_per_step": 3, "graph_replay_matches_eager": graph_ok},
+        "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": int(kbytes[dominant]), "avg_launch_us": round(d_us, 3)},
+        "layer": {"algorithmic_bytes": int(total_bytes), "achieved_GBs": round(layer_gbs, 1),
+                  "hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4),
+                  "kernel_us": {k: round(v, 3) for k, v in kern_us.items()}},
+    }
+    return out, blocks, host0, xs
+
+
+def cpu_baseline(cfg, fmts, host0, x0, budget_s):
+    import numpy as np
+    import torch
+    from oracle import oracle as O
+    orc = O.OracleMoe(cfg.hidden_size, cfg.num_experts, cfg.num_experts_per_tok, cfg.moe_intermediate_size,
+                      cfg.shared_expert_intermediate_size, cfg.norm_topk_prob, O.BF16, host0)
+    xn = x0.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+    threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
+    orc.forward(xn, nthreads=threads)                     # warm-up
+    n, t0 = 0, time.perf_counter()
+    while True:
+        orc.forward(xn, nthreads=threads)
+        n += 1
+        if time.perf_counter() - t0 > budget_s or n >= 200:
+            break
+    dt = (time.perf_counter() - t0) / n
+    return {"value": round(dt * 1e6, 1), "unit": "us/layer (C2 decode)", "cores": threads, "kind": "port",
+            "sample": f"{n} single-token decodes of layer 0 (same weights and token as the GPU run), "
+                      f"oracle/hx_oracle.c scatter loop, {threads} OpenMP threads"}
+
+
+def bench_prefill(T=2048, reps=5):
+    import numpy as np
+    import torch
+    import helexa_amd as hx
+    from helexa_amd import synth
+    cfg, fmts = synth.A3B, synth.FMT_Q4_K_M
+    w = synth.make_weights(cfg, fmts, 4242)
+    blk = hx.Qwen3_5MoeBlock.load(cfg, w, act_dtype=hx.BF16)
+    del w
+    x = synth.make_x(cfg, T, 77)
+    ws = torch.empty(blk.workspace_size(T), dtype=torch.uint8, device="cuda")
+    y = torch.empty_like(x)
+    idx = blk.route(x)["topk_idx"]
+    U = int(torch.unique(idx).numel())
+    for _ in range(2):
+        blk.forward(x, workspace=ws, out=y)
+    torch.cuda.synchronize()
+    blk.timing_begin(reps)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        blk.forward(x, workspace=ws, out=y)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    kern = {k: v[0] / v[1] * 1e3 for k, v in blk.timing_end().items() if v[1]}
+    H, I, Is, E, k = cfg.hidden_size, cfg.moe_intermediate_size, cfg.shared_expert_intermediate_size, \
+        cfg.num_experts, cfg.num_experts_per_tok
+    flops = 2 * T * k * 3 * H * I + 2 * T * 3 * H * Is + 2 * T * H * E
+    nbytes = (U * (gguf_bytes(fmts["gate"], I, H) * 2 + gguf_bytes(fmts["down"], H, I))
+              + gguf_bytes(fmts["sgate"], Is, H) * 2 + gguf_bytes(fmts["sdown"], H, Is)
+              + (E + 1) * H * 2 + 2 * T * H * 2)
+    blk.close()
+    return {"workload": f"C3: {T}-token prefill, Q4_K_M (gate/up Q4_K, down Q6_K), bf16", "tokens": T,
+            "us": round(dt * 1e6, 1), "tok_per_s": round(T / dt, 1),
+            "mfma_frac": round(flops / dt / (MFMA_BF16_PEAK_TFS * 1e12), 4),
+            "hbm_frac": round(nbytes / dt / (HBM_PEAK_GBS * 1e9), 4),
+            "algorithmic_flops": flops, "algorithmic_bytes": nbytes, "unique_experts": U,
+            "kernel_us": {k: round(v, 1) for k, v in kern.items()}}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=4096)
+    ap.add_argument("--warmup", type=int, default=512)
+    ap.add_argument("--layers", type=int, default=16)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(expert-parallel sharding is described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X (cuda:0)", file=sys.stderr)
+        sys.exit(2)
+    from helexa_amd import synth
+    out, blocks, host0, xs = bench_decode(args)
+    log(f"[bench] decode {out['value']} us/layer; kernels {out['layer']['kernel_us']}")
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        out["cpu_baseline"] = cpu_baseline(synth.A3B, synth.FMT_Q8_0, host0, xs[0], args.cpu_seconds)
+    else:
+        out["cpu_baseline"] = None
+    for b in blocks:
+        b.close()
+    del blocks
+    torch.cuda.empty_cache()
+    if not args.no_prefill:
+        log("[bench] prefill")
+        out["prefill"] = bench_prefill()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -392,7 +392,11 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
 static void tm_mark(hx_moe* m, int slot, int which, hipStream_t s) {
   Timing& t = m->tm;
   if (!t.on || t.calls >= t.max_calls) return;
-  (void)hipEventRecord(t.ev[((size_t)t.calls * N_SLOTS + slot) * 2 + which], s);
+  hipEvent_t ev = t.ev[((size_t)t.calls * N_SLOTS + slot) * 2 + which];
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  (void)hipStreamIsCapturing(s, &st);
+  // timing events are not recorded into graphs under capture
+  if (st == hipStreamCaptureStatusNone) (void)hipEventRecord(ev, s);
   if (which == 1) t.used[(size_t)t.calls * N_SLOTS + slot] = 1;
 }
 
@@ -583,7 +587,7 @@ extern "C" int hx_moe_timing_begin(hx_moe* m, int max_calls) {
   return HX_OK;
 }
 
-extern "C" int hx_moe_timing_end(hx_moe* m, double* ms, int64_t* launches, int* n_slots) {
+extern "C" int hx_moe_timing_read(hx_moe* m, double* ms, int64_t* launches, int* n_slots) {
   if (!m || !ms || !launches || !n_slots) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
   Timing& t = m->tm;
   const int cap = *n_slots;
@@ -604,9 +608,16 @@ extern "C" int hx_moe_timing_end(hx_moe* m, double* ms, int64_t* launches, int* 
       ms[i] += v;
       launches[i]++;
     }
-  t.on = false;
-  t.calls = 0;
   return HX_OK;
+}
+
+extern "C" int hx_moe_timing_end(hx_moe* m, double* ms, int64_t* launches, int* n_slots) {
+  int rc = hx_moe_timing_read(m, ms, launches, n_slots);
+  if (m) {
+    m->tm.on = false;
+    m->tm.calls = 0;
+  }
+  return rc;
 }
 
 extern "C" const char* hx_moe_timing_name(int slot) {

@@ -35,7 +35,7 @@ STATUS = {0: "HX_OK", 1: "HX_ERR_INVALID_ARGUMENT", 2: "HX_ERR_UNSUPPORTED", 3: 
 # every entry point include/hx_moe.h declares
 EXPORTS = ("hx_moe_create", "hx_moe_destroy", "hx_moe_workspace_size", "hx_moe_forward", "hx_moe_forward_host",
            "hx_moe_route", "hx_moe_router_logits", "hx_moe_decoder_mlp", "hx_quantize", "hx_dequantize",
-           "hx_row_bytes", "hx_moe_timing_begin", "hx_moe_timing_end", "hx_moe_timing_name", "hx_last_error")
+           "hx_row_bytes", "hx_moe_timing_begin", "hx_moe_timing_read", "hx_moe_timing_end", "hx_moe_timing_name", "hx_last_error")
 
 
 class HxError(RuntimeError):
@@ -86,6 +86,7 @@ def lib() -> C.CDLL:
             "hx_dequantize": (i32, [i32, vp, i64, i64, vp, vp]),
             "hx_row_bytes": (i64, [i32, i64]),
             "hx_moe_timing_begin": (i32, [vp, i32]),
+            "hx_moe_timing_read": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.POINTER(C.c_int)]),
             "hx_moe_timing_end": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.POINTER(C.c_int)]),
             "hx_moe_timing_name": (C.c_char_p, [i32]),
             "hx_last_error": (C.c_char_p, []),
@@ -227,15 +228,21 @@ class Qwen3_5MoeBlock:
         check(lib().hx_moe_workspace_size(self._h, n_tokens, C.byref(n)), "hx_moe_workspace_size")
         return n.value
 
-    def forward(self, xs, router_bias=None, workspace=None, stream=None):
-        """Module::forward: xs (b, l, hidden) or (T, hidden) on this GPU -> same shape."""
+    def forward(self, xs, router_bias=None, workspace=None, stream=None, out=None):
+        """Module::forward: xs (b, l, hidden) or (T, hidden) on this GPU -> same shape.
+        `out`, if given, is a contiguous tensor of xs's shape and dtype to write."""
         import torch
         if xs.shape[-1] != self.cfg.hidden_size:
             raise ValueError(f"last dim {xs.shape[-1]} != hidden {self.cfg.hidden_size}")
         if _act_dtype(xs.dtype) != self.act_dtype:
             raise TypeError("activation dtype differs from the block's")
         x = xs.contiguous()
-        y = torch.empty_like(x)
+        if out is None:
+            y = torch.empty_like(x)
+        else:
+            if out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous():
+                raise ValueError("out must be contiguous with the input's shape and dtype")
+            y = out
         T = x.numel() // self.cfg.hidden_size
         ws_ptr, ws_n = (None, 0) if workspace is None else (_ptr(workspace), workspace.numel() * workspace.element_size())
         check(lib().hx_moe_forward(self._h, _ptr(x), T, _ptr(y), ws_ptr, ws_n, _ptr(router_bias), _stream(stream)),
@@ -279,12 +286,19 @@ class Qwen3_5MoeBlock:
     def timing_begin(self, max_calls: int) -> None:
         check(lib().hx_moe_timing_begin(self._h, max_calls), "hx_moe_timing_begin")
 
-    def timing_end(self) -> dict:
+    def _timing(self, fn) -> dict:
         n = C.c_int(16)
         ms = (C.c_double * 16)()
         cnt = (C.c_int64 * 16)()
-        check(lib().hx_moe_timing_end(self._h, ms, cnt, C.byref(n)), "hx_moe_timing_end")
+        check(fn(self._h, ms, cnt, C.byref(n)), fn.__name__)
         return {lib().hx_moe_timing_name(i).decode(): (ms[i], cnt[i]) for i in range(n.value)}
+
+    def timing_read(self) -> dict:
+        """{kernel slot: (summed ms, timed launches)} over the armed forwards"""
+        return self._timing(lib().hx_moe_timing_read)
+
+    def timing_end(self) -> dict:
+        return self._timing(lib().hx_moe_timing_end)
 
 
 def quantize(dtype: int, w, stream=None):

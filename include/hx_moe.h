@@ -144,13 +144,16 @@ int hx_dequantize(int dtype, const void* src, int64_t rows, int64_t cols, float*
 /* Bytes of one GGUF row of n elements, or -1 if n does not tile into blocks. */
 int64_t hx_row_bytes(int dtype, int64_t n);
 
-/* Per-kernel timing with HIP events recorded on the forward's stream around
- * each kernel it launches. hx_moe_timing_begin arms it for up to max_calls
- * forwards; hx_moe_timing_end synchronises and returns, per kernel slot, the
- * summed milliseconds and the launch count (arrays of length *n_slots on input
- * capacity, on output the slots used) plus the slots' names via
- * hx_moe_timing_name. */
+/* Per-kernel timing (a measurement hook with no reference counterpart): HIP
+ * events recorded on the forward's stream around each kernel it launches.
+ * hx_moe_timing_begin arms it for the next max_calls forwards (forwards under
+ * stream capture are not timed).
+ * hx_moe_timing_read synchronises on the recorded events and returns, per
+ * kernel slot, the summed milliseconds and the number of timed launches
+ * (*n_slots: capacity in, slots used out); hx_moe_timing_end does the same and
+ * disarms. hx_moe_timing_name names a slot. */
 int hx_moe_timing_begin(hx_moe* m, int max_calls);
+int hx_moe_timing_read(hx_moe* m, double* ms, int64_t* launches, int* n_slots);
 int hx_moe_timing_end(hx_moe* m, double* ms, int64_t* launches, int* n_slots);
 const char* hx_moe_timing_name(int slot);
 
