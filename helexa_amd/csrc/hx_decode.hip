@@ -1,0 +1,496 @@
+// Decode expert kernels for bf16 activations (T <= HX_DECODE_MAX_T).
+//
+// Reference: Qwen3_5MLP::forward (crates/neuron/src/harness/arch/qwen3_5/mlp.rs:54-60)
+// inside the scatter loop of Module::forward (moe.rs:177-195) and
+// MaybeQuantLinear's GGUF GEMV arm (crates/neuron/src/harness/tp/tp_linear.rs:120-137).
+//
+// Arithmetic: each quantised weight is turned into the f16 value 1024 + u, where
+// u is its unsigned code (Q8_0: q + 128; Q4_K: the nibble; Q6_K: the 6-bit
+// code), by writing u under the f16 pattern 0x6400 -- exact, one v_perm or
+// v_and_or per two weights. Activations are bf16, which converts to f16
+// exactly in f16's normal range, and the pair products go through
+// v_dot2_f32_f16 into f32. The offset is removed with the per-run activation
+// sums: sum((1024 + u) x) - (1024 + bias) sum(x) = sum((u - bias) x).
+// The SwiGLU activations between the two passes are stored as f16.
+#include "hx_internal.h"
+#include "hx_route_small.h"
+#include "hx_router_dev.h"
+
+namespace hx {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+HX_DEV half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
+HX_DEV float dot2(uint32_t w, uint32_t x, float acc) { return __builtin_amdgcn_fdot2(as_h2(w), as_h2(x), acc, false); }
+
+// two bf16 (packed) -> two f16 (packed)
+HX_DEV uint32_t bf16x2_to_f16x2(uint32_t v) {
+  float lo = __uint_as_float(v << 16), hi = __uint_as_float(v & 0xffff0000u);
+  half2_t h = {(_Float16)lo, (_Float16)hi};
+  return __builtin_bit_cast(uint32_t, h);
+}
+
+HX_DEV float f16x2_sum(uint32_t v) {
+  half2_t h = as_h2(v);
+  return (float)h.x + (float)h.y;
+}
+
+// 16 bytes of f16 (8 values) at p -> 4 packed pairs ordered (e0,e2) (e1,e3) (e4,e6) (e5,e7)
+// to match the weight pairing below (bytes i, i+2 of each dword)
+HX_DEV void pairs_from_f16x8(uint4 v, uint32_t* out) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};  // (e0,e1) (e2,e3) (e4,e5) (e6,e7)
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const uint32_t a = w[2 * j], b = w[2 * j + 1];
+    out[2 * j] = __builtin_amdgcn_perm(b, a, 0x05040100u);      // (lo a, lo b) = (e0, e2)
+    out[2 * j + 1] = __builtin_amdgcn_perm(b, a, 0x07060302u);  // (hi a, hi b) = (e1, e3)
+  }
+}
+
+// x: 8 bf16 at p -> 4 f16 pairs in weight-pair order
+HX_DEV void x_pairs_bf16(const uint16_t* p, uint32_t* out) {
+  uint4 v = *(const uint4*)p;
+  uint4 h;
+  h.x = bf16x2_to_f16x2(v.x);
+  h.y = bf16x2_to_f16x2(v.y);
+  h.z = bf16x2_to_f16x2(v.z);
+  h.w = bf16x2_to_f16x2(v.w);
+  pairs_from_f16x8(h, out);
+}
+
+HX_DEV void x_pairs_f16(const uint16_t* p, uint32_t* out) { pairs_from_f16x8(*(const uint4*)p, out); }
+
+// 4 bytes b0..b3 (already offset to unsigned) -> f16 pairs (1024+b0, 1024+b2), (1024+b1, 1024+b3)
+HX_DEV uint32_t bytes02(uint32_t q) { return __builtin_amdgcn_perm(q, 0x64646464u, 0x00060004u); }
+HX_DEV uint32_t bytes13(uint32_t q) { return __builtin_amdgcn_perm(q, 0x64646464u, 0x00070005u); }
+// nibble pairs (low nibbles of bytes 0,2) etc, as 1024 + nibble
+HX_DEV uint32_t nib02(uint32_t q) { return (q & 0x000F000Fu) | 0x64006400u; }
+
+template <int FMT>
+struct DChunk;
+
+// Q8_0 planar: chunk = one 32-weight block: 32 int8 + f16 scale
+template <>
+struct DChunk<HX_Q8_0> {
+  static constexpr int NX = 16;  // f16 pairs of activations per chunk
+  static constexpr int NS = 1;   // activation sums per chunk
+  using Raw = Chunk<HX_Q8_0>::Raw;
+  HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
+    Chunk<HX_Q8_0>::load(mat, R, K, row, c, r);
+  }
+  // activation positions: elements 32c .. 32c+31, pairs per 8
+  template <bool XF16>
+  HX_DEV static void load_x(const uint16_t* xrow, int c, uint32_t* xp, float* xs) {
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      if (XF16) x_pairs_f16(xrow + 32 * c + 8 * v, xp + 4 * v);
+      else x_pairs_bf16(xrow + 32 * c + 8 * v, xp + 4 * v);
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) s += f16x2_sum(xp[i]);
+    xs[0] = s;
+  }
+  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs) {
+    const uint32_t q[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
+    float acc = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const uint32_t u = q[j] ^ 0x80808080u;  // int8 -> q + 128
+      acc = dot2(bytes02(u), xp[2 * j], acc);
+      acc = dot2(bytes13(u), xp[2 * j + 1], acc);
+    }
+    return f16_to_f32((uint16_t)r.d) * (acc - 1152.0f * xs[0]);
+  }
+};
+
+// Q4_K (GGUF): chunk = 16 bytes of nibbles: low run (sub-block 2p) and high run (2p+1)
+template <>
+struct DChunk<HX_Q4_K> {
+  static constexpr int NX = 16, NS = 2;
+  using Raw = Chunk<HX_Q4_K>::Raw;
+  HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
+    Chunk<HX_Q4_K>::load(mat, R, K, row, c, r);
+  }
+  template <bool XF16>
+  HX_DEV static void load_x(const uint16_t* xrow, int c, uint32_t* xp, float* xs) {
+    const int sb = c >> 3, cc = c & 7, p = cc >> 1, h = cc & 1;
+    const uint16_t* lo = xrow + sb * 256 + 64 * p + 16 * h;
+#pragma unroll
+    for (int v = 0; v < 2; v++) {
+      if (XF16) {
+        x_pairs_f16(lo + 8 * v, xp + 4 * v);
+        x_pairs_f16(lo + 32 + 8 * v, xp + 8 + 4 * v);
+      } else {
+        x_pairs_bf16(lo + 8 * v, xp + 4 * v);
+        x_pairs_bf16(lo + 32 + 8 * v, xp + 8 + 4 * v);
+      }
+    }
+    float a = 0.f, b = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      a += f16x2_sum(xp[i]);
+      b += f16x2_sum(xp[8 + i]);
+    }
+    xs[0] = a;
+    xs[1] = b;
+  }
+  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs) {
+    const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    float lo = 0.f, hi = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      lo = dot2(nib02(q[j]), xp[2 * j], lo);
+      lo = dot2(nib02(q[j] >> 8), xp[2 * j + 1], lo);
+      hi = dot2(nib02(q[j] >> 4), xp[8 + 2 * j], hi);
+      hi = dot2(nib02(q[j] >> 12), xp[8 + 2 * j + 1], hi);
+    }
+    const float d = f16_to_f32((uint16_t)(r.hdr.x & 0xffffu)), dmin = f16_to_f32((uint16_t)(r.hdr.x >> 16));
+    int sc0, m0, sc1, m1;
+    const int p = r.cc >> 1;
+    Chunk<HX_Q4_K>::scale_min(r.hdr, 2 * p, sc0, m0);
+    Chunk<HX_Q4_K>::scale_min(r.hdr, 2 * p + 1, sc1, m1);
+    return d * ((float)sc0 * (lo - 1024.0f * xs[0]) + (float)sc1 * (hi - 1024.0f * xs[1])) -
+           dmin * ((float)m0 * xs[0] + (float)m1 * xs[1]);
+  }
+};
+
+// Q6_K planar: chunk = quarters 0..3 of l = 8a .. 8a+7 in half n of a superblock
+template <>
+struct DChunk<HX_Q6_K> {
+  static constexpr int NX = 16, NS = 4;
+  using Raw = Chunk<HX_Q6_K>::Raw;
+  HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
+    Chunk<HX_Q6_K>::load(mat, R, K, row, c, r);
+  }
+  template <bool XF16>
+  HX_DEV static void load_x(const uint16_t* xrow, int c, uint32_t* xp, float* xs) {
+    const int sb = c >> 3, cc = c & 7, n = cc >> 2, a = cc & 3;
+    const uint16_t* base = xrow + sb * 256 + 128 * n + 8 * a;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      if (XF16) x_pairs_f16(base + 32 * s, xp + 4 * s);
+      else x_pairs_bf16(base + 32 * s, xp + 4 * s);
+      float t = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; i++) t += f16x2_sum(xp[4 * s + i]);
+      xs[s] = t;
+    }
+  }
+  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs) {
+    const uint32_t l0[2] = {r.l0.x, r.l0.y}, l1[2] = {r.l1.x, r.l1.y}, hh[2] = {r.h.x, r.h.y};
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int w = 0; w < 2; w++) {
+#pragma unroll
+      for (int par = 0; par < 2; par++) {   // byte pairs (0,2) then (1,3)
+        const int sh = 8 * par;
+        const uint32_t a0 = l0[w] >> sh, a1 = l1[w] >> sh, h = hh[w] >> sh;
+        const uint32_t q0 = nib02(a0) | ((h << 4) & 0x00300030u);
+        const uint32_t q1 = nib02(a1) | ((h << 2) & 0x00300030u);
+        const uint32_t q2 = nib02(a0 >> 4) | (h & 0x00300030u);
+        const uint32_t q3 = nib02(a1 >> 4) | ((h >> 2) & 0x00300030u);
+        acc[0] = dot2(q0, xp[0 + 2 * w + par], acc[0]);
+        acc[1] = dot2(q1, xp[4 + 2 * w + par], acc[1]);
+        acc[2] = dot2(q2, xp[8 + 2 * w + par], acc[2]);
+        acc[3] = dot2(q3, xp[12 + 2 * w + par], acc[3]);
+      }
+    }
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const float sc = (float)(int8_t)((r.sc >> (8 * q)) & 0xffu);
+      s = __builtin_fmaf(sc, acc[q] - 1056.0f * xs[q], s);
+    }
+    return f16_to_f32((uint16_t)r.d) * s;
+  }
+};
+
+// the decode plan, pulled into LDS by the whole workgroup in one pass
+HX_DEV void load_plan(const ExpertArgs& a, int32_t* splan) {
+  const int np = plan_ints(a.max_slots, a.F, a.T);
+  for (int i = threadIdx.x; i < np; i += 256) splan[i] = a.plan[i];
+  __syncthreads();
+}
+
+// Touch one dword in each of (at most) two 128-byte lines per thread of
+// [base, base + nbytes) (<= 64 KiB per workgroup) so those lines come from HBM
+// into the caches -- the memory-side Infinity Cache keeps them for the next
+// kernel. The values are consumed only at the end of the kernel (touch_sink),
+// so the loads are in flight during the workgroup's own work.
+struct Touch {
+  uint32_t a, b;
+};
+HX_DEV Touch touch_lines(const uint8_t* base, int64_t nbytes) {
+  Touch t{0u, 0u};
+  const int64_t o0 = (int64_t)threadIdx.x * 128, o1 = o0 + 256 * 128;
+  if (o0 < nbytes) t.a = *(const uint32_t*)(base + o0);
+  if (o1 < nbytes) t.b = *(const uint32_t*)(base + o1);
+  return t;
+}
+// the condition is never true for a decode call (y is set); it keeps the loads live
+HX_DEV void touch_sink(const ExpertArgs& a, Touch t) {
+  if ((t.a ^ t.b) == 0x9e3779b9u && a.y == nullptr) ((uint32_t*)a.hbf)[0] = t.a;
+}
+
+// NR (gate, up) row pairs of one expert for a list of tokens; h stored as f16
+template <int FMT, int LPR, int NR>
+HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U, int rows, int row0, int count,
+                         const int* tok, const int* hrow) {
+  using D = DChunk<FMT>;
+  constexpr int RG = 64 / LPR;
+  const int c = lane_id() % LPR, K = a.H;
+  typename D::Raw rgt[NR], rup[NR];
+#pragma unroll
+  for (int g = 0; g < NR; g++) {
+    const int row = row0 + g * RG;
+    if (row < rows) {
+      D::load(G, rows, K, row, c, rgt[g]);
+      D::load(U, rows, K, row, c, rup[g]);
+    }
+  }
+  for (int j = 0; j < count; j++) {
+    uint32_t xp[D::NX];
+    float xs[D::NS];
+    D::template load_x<false>((const uint16_t*)a.x + (int64_t)tok[j] * K, c, xp, xs);
+#pragma unroll
+    for (int g = 0; g < NR; g++) {
+      const int row = row0 + g * RG;
+      float pg = row < rows ? D::dot(rgt[g], xp, xs) : 0.f;
+      float pu = row < rows ? D::dot(rup[g], xp, xs) : 0.f;
+      pg = wave_sum<LPR>(pg);
+      pu = wave_sum<LPR>(pu);
+      if (c == 0 && row < rows) {
+        const float h = siluf_(pg) * pu;
+        ((_Float16*)a.hbf)[(int64_t)hrow[j] * a.hstride + row] = (_Float16)h;
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// K1: router logits (blocks [0, nrb)) and the shared expert's gate/up + SwiGLU
+// (blocks [nrb, ...)), which needs only the tokens. The shared blocks also pull
+// the shared down projection into the caches for K3.
+// ----------------------------------------------------------------------------
+template <int FMT, int LPR, int NR, bool RBF, int TT>
+__global__ __launch_bounds__(256) void k_router_dec(RouterArgs r, ExpertArgs a, int nrb) {
+  const int wave = threadIdx.x >> 6;
+  if ((int)blockIdx.x < nrb) {
+    router_rows<true, RBF, TT, 1>(r, blockIdx.x * 4 + wave, 0);
+    return;
+  }
+  constexpr int RG = 64 / LPR;
+  const int sb = blockIdx.x - nrb, nsb = gridDim.x - nrb;
+  const int64_t per = (a.sdown.mat_bytes + nsb - 1) / nsb;
+  const int64_t lo = (int64_t)sb * per, n = lo + per < a.sdown.mat_bytes ? per : a.sdown.mat_bytes - lo;
+  const Touch pf = n > 0 ? touch_lines(a.sdown.base + lo, n) : Touch{0u, 0u};
+  int tok[HX_DECODE_MAX_T], hrow[HX_DECODE_MAX_T];
+  for (int j = 0; j < a.T; j++) {
+    tok[j] = j;
+    hrow[j] = a.F + j;
+  }
+  const int row0 = (sb * 4 + wave) * (RG * NR) + lane_id() / LPR;
+  if (row0 - lane_id() / LPR < a.Is)
+    gate_up_rows<FMT, LPR, NR>(a, a.sgate.base, a.sup.base, a.Is, row0, a.T, tok, hrow);
+  touch_sink(a, pf);
+}
+
+// ----------------------------------------------------------------------------
+// K2: routed gate/up + SwiGLU. Every workgroup routes the T tokens from the
+// logits in LDS. The last grid row's workgroup 0 only publishes routing and
+// plan; workgroup (x, u < last row) computes rows of slot u's expert and pulls
+// a 1/gridDim.x share of that expert's down projection into the caches for K3.
+// ----------------------------------------------------------------------------
+template <int FMT, int LPR, int NR>
+__global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a) {
+  constexpr int RG = 64 / LPR;
+  __shared__ RouteSmem sm;
+  const bool publisher = blockIdx.y == gridDim.y - 1;
+  if (publisher && blockIdx.x > 0) return;
+  route_small_lds(r.logits, r.E1, r.E, r.k, r.norm, r.has_shared, r.T, sm);
+  if (publisher) {
+    publish_route(r.d, r.topk_w, r.sgw, sm);
+    return;
+  }
+  const int u = blockIdx.y;
+  if (u >= sm.nroute) return;
+  const int e = sm.slots[3 * u], start = sm.slots[3 * u + 1], count = sm.slots[3 * u + 2];
+  const int64_t per = (a.down.mat_bytes + gridDim.x - 1) / gridDim.x;
+  const int64_t lo = (int64_t)blockIdx.x * per, n = lo + per < a.down.mat_bytes ? per : a.down.mat_bytes - lo;
+  const Touch pf = n > 0 ? touch_lines(a.down.mat(e) + lo, n) : Touch{0u, 0u};
+  const int wave = threadIdx.x >> 6;
+  int tok[HX_DECODE_MAX_T], hrow[HX_DECODE_MAX_T];
+  for (int j = 0; j < count; j++) {
+    hrow[j] = start + j;
+    tok[j] = sm.perm[start + j] / a.k;
+  }
+  const int row0 = (blockIdx.x * 4 + wave) * (RG * NR) + lane_id() / LPR;
+  if (row0 - lane_id() / LPR < a.I)
+    gate_up_rows<FMT, LPR, NR>(a, a.gate.mat(e), a.up.mat(e), a.I, row0, count, tok, hrow);
+  touch_sink(a, pf);
+}
+
+// ----------------------------------------------------------------------------
+// down + combine: block = RG output rows; the 4 waves split the slots; per-slot
+// contributions w * (row . h) go to LDS and are summed in slot order (experts
+// ascending, then the shared expert).
+// ----------------------------------------------------------------------------
+template <int FMT, int LPR, int SPW>
+__global__ __launch_bounds__(256) void k_down_dec(ExpertArgs a) {
+  using D = DChunk<FMT>;
+  constexpr int RG = 64 / LPR;
+  extern __shared__ int32_t splan[];
+  load_plan(a, splan);
+  float* contrib = (float*)(splan + plan_ints(a.max_slots, a.F, a.T));
+  const int nslots = splan[0], T = a.T;
+  const int tok0 = 4 + 4 * a.max_slots, w0 = tok0 + a.F + a.T;
+  const int lane = lane_id(), wave = threadIdx.x >> 6, rg = lane / LPR, c = lane % LPR;
+  const int n0 = blockIdx.x * RG, row = n0 + rg;
+  for (int i = threadIdx.x; i < nslots * T * RG; i += 256) contrib[i] = 0.f;
+  __syncthreads();
+  for (int ub = wave; ub < nslots; ub += 4 * SPW) {
+    // every load of the batch first: the SPW slots' weight chunks and the
+    // activations of each slot's first token
+    typename D::Raw raw[SPW];
+    uint32_t xp0[SPW][D::NX];
+    float xs0[SPW][D::NS];
+#pragma unroll
+    for (int s = 0; s < SPW; s++) {
+      const int u = ub + 4 * s;
+      if (u < nslots) {
+        const int e = splan[4 + 4 * u], start = splan[4 + 4 * u + 1];
+        const bool sh = e == a.E;
+        const int K = sh ? a.Is : a.I;
+        if (row < a.H && c < K / 32) {
+          D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row, c, raw[s]);
+          D::template load_x<true>((const uint16_t*)a.hbf + (int64_t)start * a.hstride, c, xp0[s], xs0[s]);
+        }
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < SPW; s++) {
+      const int u = ub + 4 * s;
+      if (u >= nslots) break;
+      const int e = splan[4 + 4 * u], start = splan[4 + 4 * u + 1], count = splan[4 + 4 * u + 2];
+      const bool sh = e == a.E;
+      const int K = sh ? a.Is : a.I;
+      for (int j = 0; j < count; j++) {
+        const int hrow = start + j, t = splan[tok0 + hrow];
+        const float wgt = __int_as_float(splan[w0 + hrow]);
+        float p = 0.f;
+        if (c < K / 32) {
+          if (j == 0) {
+            p = D::dot(raw[s], xp0[s], xs0[s]);
+          } else {
+            uint32_t xp[D::NX];
+            float xs[D::NS];
+            D::template load_x<true>((const uint16_t*)a.hbf + (int64_t)hrow * a.hstride, c, xp, xs);
+            p = D::dot(raw[s], xp, xs);
+          }
+        }
+        p = wave_sum<LPR>(p);
+        if (c == 0 && row < a.H) contrib[((int64_t)u * T + t) * RG + rg] = wgt * p;
+      }
+    }
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < T * RG; i += 256) {
+    const int t = i / RG, r = i % RG;
+    if (n0 + r >= a.H) continue;
+    float y = 0.f;
+    for (int u = 0; u < nslots; u++) y += contrib[((int64_t)u * T + t) * RG + r];
+    ((uint16_t*)a.y)[(int64_t)t * a.H + n0 + r] = f32_to_bf16(y);
+  }
+}
+
+// ----------------------------------------------------------------------------
+// launchers: used for bf16 activations with Q8_0 / Q4_K / Q6_K weights whose
+// input dims give 16, 32 or 64 chunks of 32 per row (K = 512, 1024, 2048)
+// ----------------------------------------------------------------------------
+bool decode_fast_ok(const ExpertArgs& a) {
+  auto ok = [](int fmt, int K) {
+    return (fmt == HX_Q8_0 || fmt == HX_Q4_K || fmt == HX_Q6_K) && (K == 512 || K == 1024 || K == 2048);
+  };
+  const int Kd = a.I > a.Is ? a.I : a.Is;
+  return a.xbf && ok(a.gate.fmt, a.H) && ok(a.down.fmt, Kd) && (a.Is == 0 || a.Is == a.I);
+}
+
+template <int FMT>
+static hipError_t router_dec_fmt(const RouterArgs& r, const ExpertArgs& a, bool rbf, hipStream_t s) {
+  const int nch = a.H / 32, nrb = (r.E1 + 3) / 4;
+  constexpr int NR = 2;
+#define RD(LPR, RB, TT)                                                                     \
+  {                                                                                         \
+    constexpr int RG = 64 / LPR;                                                            \
+    const int nsb = a.Is > 0 ? (a.Is + 4 * RG * NR - 1) / (4 * RG * NR) : 0;                \
+    hipLaunchKernelGGL((k_router_dec<FMT, LPR, NR, RB, TT>), dim3(nrb + nsb), dim3(256), 0, s, r, a, nrb); \
+  }
+#define RD_T(LPR, RB) { if (r.T <= 1) RD(LPR, RB, 1) else if (r.T <= 2) RD(LPR, RB, 2) else if (r.T <= 4) RD(LPR, RB, 4) else RD(LPR, RB, 8) }
+#define RD_R(LPR) { if (rbf) RD_T(LPR, true) else RD_T(LPR, false) }
+  if (nch == 64) RD_R(64) else if (nch == 32) RD_R(32) else RD_R(16)
+#undef RD_R
+#undef RD_T
+#undef RD
+  return hipGetLastError();
+}
+
+template <int FMT>
+static hipError_t gate_up_dec_fmt(const RouterArgs& r, const ExpertArgs& a, hipStream_t s) {
+  const int nch = a.H / 32;
+  const int nroute = a.F < a.E ? a.F : a.E;
+  constexpr int NR = 2;
+#define GUD(LPR)                                                                          \
+  {                                                                                       \
+    constexpr int RG = 64 / LPR;                                                          \
+    dim3 grid((a.I + 4 * RG * NR - 1) / (4 * RG * NR), nroute + 1);                       \
+    hipLaunchKernelGGL((k_gate_up_dec<FMT, LPR, NR>), grid, dim3(256), 0, s, r, a);       \
+  }
+  if (nch == 64) GUD(64) else if (nch == 32) GUD(32) else GUD(16)
+#undef GUD
+  return hipGetLastError();
+}
+
+template <int FMT>
+static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
+  const int nch = (a.I > a.Is ? a.I : a.Is) / 32;
+#define DD(LPR)                                                                                   \
+  {                                                                                               \
+    constexpr int RG = 64 / LPR;                                                                  \
+    size_t lds = sizeof(int32_t) * plan_ints(a.max_slots, a.F, a.T) +                              \
+                 (size_t)a.max_slots * a.T * RG * sizeof(float);                                  \
+    hipLaunchKernelGGL((k_down_dec<FMT, LPR, 3>), dim3((a.H + RG - 1) / RG), dim3(256), lds, s, a); \
+  }
+  if (nch == 64) DD(64) else if (nch == 32) DD(32) else DD(16)
+#undef DD
+  return hipGetLastError();
+}
+
+hipError_t launch_router_dec(const RouterArgs& r, const ExpertArgs& a, bool rbf, hipStream_t s) {
+  switch (a.gate.fmt) {
+    case HX_Q8_0: return router_dec_fmt<HX_Q8_0>(r, a, rbf, s);
+    case HX_Q4_K: return router_dec_fmt<HX_Q4_K>(r, a, rbf, s);
+    case HX_Q6_K: return router_dec_fmt<HX_Q6_K>(r, a, rbf, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gate_up_dec(const RouterArgs& r, const ExpertArgs& a, hipStream_t s) {
+  switch (a.gate.fmt) {
+    case HX_Q8_0: return gate_up_dec_fmt<HX_Q8_0>(r, a, s);
+    case HX_Q4_K: return gate_up_dec_fmt<HX_Q4_K>(r, a, s);
+    case HX_Q6_K: return gate_up_dec_fmt<HX_Q6_K>(r, a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_down_dec(const ExpertArgs& a, hipStream_t s) {
+  switch (a.down.fmt) {
+    case HX_Q8_0: return down_dec_fmt<HX_Q8_0>(a, s);
+    case HX_Q4_K: return down_dec_fmt<HX_Q4_K>(a, s);
+    case HX_Q6_K: return down_dec_fmt<HX_Q6_K>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace hx

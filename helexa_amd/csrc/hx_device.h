@@ -103,6 +103,36 @@ HX_DEV unsigned long long wave_max_u64(unsigned long long v) {
 
 HX_DEV int lane_id() { return (int)(threadIdx.x & 63); }
 
+// DPP move of v from the lane picked by CTRL; rows outside ROWMASK keep v
+template <int CTRL, int ROWMASK = 0xf>
+HX_DEV int dpp_mov(int v) {
+  return __builtin_amdgcn_update_dpp(v, v, CTRL, ROWMASK, 0xf, false);
+}
+
+// Wave-wide max / min through DPP (quad swaps, half-row and row mirrors, then
+// the row 15 / row 31 broadcasts); exact for max and min, so the order of the
+// combination does not matter. The result is read from lane 63 and returned
+// to every lane.
+HX_DEV float wave_max_dpp(float v) {
+  v = fmaxf(v, __int_as_float(dpp_mov<0xB1>(__float_as_int(v))));   // quad_perm 1,0,3,2
+  v = fmaxf(v, __int_as_float(dpp_mov<0x4E>(__float_as_int(v))));   // quad_perm 2,3,0,1
+  v = fmaxf(v, __int_as_float(dpp_mov<0x141>(__float_as_int(v))));  // row_half_mirror
+  v = fmaxf(v, __int_as_float(dpp_mov<0x140>(__float_as_int(v))));  // row_mirror
+  v = fmaxf(v, __int_as_float(dpp_mov<0x142, 0xA>(__float_as_int(v))));  // row_bcast15
+  v = fmaxf(v, __int_as_float(dpp_mov<0x143, 0xC>(__float_as_int(v))));  // row_bcast31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+HX_DEV int wave_min_dpp(int v) {
+  v = min(v, dpp_mov<0xB1>(v));
+  v = min(v, dpp_mov<0x4E>(v));
+  v = min(v, dpp_mov<0x141>(v));
+  v = min(v, dpp_mov<0x140>(v));
+  v = min(v, dpp_mov<0x142, 0xA>(v));
+  v = min(v, dpp_mov<0x143, 0xC>(v));
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
 // activation element loads
 HX_DEV float ld_act(const void* p, int64_t i, bool bf16) {
   return bf16 ? bf16_to_f32(((const uint16_t*)p)[i]) : ((const float*)p)[i];

@@ -32,7 +32,17 @@ struct DispatchArgs {
   int32_t* slots;      // [(min(F,E)+1) * 3]: expert, start position, count
   int32_t* tiles;      // [max_tiles * 4]: slot, expert, start position, rows
   int32_t* counts;     // [2]: number of slots, number of tiles
+  int32_t* plan;       // decode plan (written by the decode routing tail), see plan_ints()
+  int max_slots;
 };
+
+// Decode plan: everything the decode expert kernels need about the routing, in
+// one contiguous int32 block they pull into LDS with a single coalesced load.
+//   [0]                         number of slots S (routed experts + shared)
+//   [4 + 4u + {0,1,2}]          slot u: expert (E = shared), start position, count
+//   [4 + 4*max_slots + p]       token of permuted position p (p < F + T; shared: F + t)
+//   [4 + 4*max_slots + F+T + p] routing weight of position p (f32 bits)
+__host__ __device__ inline int plan_ints(int max_slots, int F, int T) { return 4 + 4 * max_slots + 2 * (F + T); }
 
 struct RouterArgs {
   const void* x;       // [T, H] act dtype
@@ -44,7 +54,6 @@ struct RouterArgs {
   float* logits;       // [T, E1]
   float* topk_w;       // [T*k]
   float* sgw;          // [T] sigmoid of the shared-expert gate
-  unsigned* counter;   // zero between launches
   DispatchArgs d;
 };
 
@@ -73,20 +82,26 @@ struct ExpertArgs {
   const int32_t* counts;
   float* hbuf;         // [(F+T), hstride] SwiGLU activations, f32
   int hstride;
-  uint16_t* hbf;       // [(F+T), hstride] bf16 copy for the grouped GEMMs
+  uint16_t* hbf;       // [(F+T), hstride] 16-bit copy: f16 for the decode kernels, bf16 for the GEMMs
   void* obuf;          // [(F+T), H] weighted expert outputs (prefill): bf16 for bf16
                        // activations, f32 for f32 ones
   const int32_t* inv;
   const int32_t* topk_idx;
   void* y;             // [T, H] act dtype
   int max_slots, max_tiles;
+  const int32_t* plan;
 };
 
-void launch_router(const RouterArgs& a, bool xbf, bool rbf, bool tail, hipStream_t s);
+void launch_router(const RouterArgs& a, bool xbf, bool rbf, hipStream_t s);
+void launch_route_small(const RouterArgs& a, hipStream_t s);   // T <= HX_DECODE_MAX_T, one workgroup
 void launch_route_tokens(const RouterArgs& a, hipStream_t s);
 void launch_dispatch(const DispatchArgs& d, hipStream_t s);
 
 // decode (T <= HX_DECODE_MAX_T)
+bool decode_fast_ok(const ExpertArgs& a);   // bf16 activations, GGUF weights: f16 dot2 kernels
+hipError_t launch_router_dec(const RouterArgs& r, const ExpertArgs& a, bool rbf, hipStream_t s);  // router + shared gate/up
+hipError_t launch_gate_up_dec(const RouterArgs& r, const ExpertArgs& a, hipStream_t s);
+hipError_t launch_down_dec(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_gate_up_gemv(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_down_gemv_combine(const ExpertArgs& a, hipStream_t s);
 // prefill

@@ -5,15 +5,17 @@
 // TpQwen3_5MoeBlock::{load, forward_fused, forward}
 // (crates/neuron/src/harness/tp/tp_qwen3_5.rs:1060-1275).
 //
-// Decode (T <= HX_DECODE_MAX_T) runs three kernels: the router (whose last
-// block also does softmax / top-k / dispatch), gate/up + SwiGLU, and down +
-// combine. Prefill runs router, per-token routing, dispatch, gate/up, down
-// (weighted rows) and combine.
+// Decode (T <= HX_DECODE_MAX_T, bf16 activations, GGUF experts) runs three
+// kernels: router logits + the shared expert's gate/up; the routed gate/up,
+// each workgroup re-deriving the (small) routing from the logits; down +
+// combine. Other decode cases route in a separate one-workgroup kernel.
+// Prefill runs router, per-token routing, dispatch, gate/up, down (weighted
+// rows) and combine.
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
 
-#include "../../include/hx_moe.h"
+#include "hx_moe.h"
 #include "hx_internal.h"
 
 using namespace hx;
@@ -63,7 +65,6 @@ struct hx_moe {
   int rdt = HX_F32;   // dtype of the combined router rows
   void* router = nullptr;
   WMat gate, up, down, sgate, sup, sdown;
-  unsigned* counter = nullptr;
   void* own_ws = nullptr;
   size_t own_ws_bytes = 0;
   Timing tm;
@@ -72,7 +73,7 @@ struct hx_moe {
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct WsLayout {
-  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, hbuf, hbf, obuf, xn, ym, total;
+  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, hbuf, hbf, obuf, xn, ym, total;
   int hstride, max_slots, max_tiles;
 };
 
@@ -101,8 +102,9 @@ static WsLayout ws_layout(const hx_moe* m, int64_t T) {
   L.slots = take(sizeof(int32_t) * 3 * L.max_slots);
   L.tiles = take(sizeof(int32_t) * 4 * L.max_tiles);
   L.counts = take(sizeof(int32_t) * 4);
+  L.plan = take(sizeof(int32_t) * plan_ints(L.max_slots, (int)F, (int)T));
   L.hbuf = take(sizeof(float) * (F + T) * L.hstride);
-  L.hbf = decode ? 0 : take(sizeof(uint16_t) * (F + T) * L.hstride);
+  L.hbf = take(sizeof(uint16_t) * (F + T) * L.hstride);
   const size_t act = m->cfg.act_dtype == HX_BF16 ? 2 : 4;
   L.obuf = decode ? 0 : take(act * (F + T) * H);
   L.xn = take(act * T * H);
@@ -179,7 +181,6 @@ extern "C" int hx_moe_destroy(hx_moe* m) {
   free_mat(m->gate); free_mat(m->up); free_mat(m->down);
   free_mat(m->sgate); free_mat(m->sup); free_mat(m->sdown);
   if (m->router) (void)hipFree(m->router);
-  if (m->counter) (void)hipFree(m->counter);
   if (m->own_ws) (void)hipFree(m->own_ws);
   for (hipEvent_t e : m->tm.ev) (void)hipEventDestroy(e);
   delete m;
@@ -278,14 +279,6 @@ extern "C" int hx_moe_create(const hx_moe_config* cfg, const hx_moe_weights* w, 
     hx_moe_destroy(m);
     return rc;
   }
-  if (hipMalloc(&m->counter, 256) != hipSuccess) {
-    hx_moe_destroy(m);
-    return fail(HX_ERR_OUT_OF_MEMORY, "counter allocation");
-  }
-  if (hipMemset(m->counter, 0, 256) != hipSuccess || hipDeviceSynchronize() != hipSuccess) {
-    hx_moe_destroy(m);
-    return fail(HX_ERR_DEVICE, "counter initialisation");
-  }
   *out = m;
   return HX_OK;
 }
@@ -348,7 +341,6 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
   r.logits = (float*)(ws + L.logits);
   r.topk_w = (float*)(ws + L.topk_w);
   r.sgw = (float*)(ws + L.sgw);
-  r.counter = m->counter;
   DispatchArgs& d = r.d;
   d.topk_idx = (int32_t*)(ws + L.topk_idx);
   d.T = (int)T;
@@ -363,6 +355,8 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
   d.slots = (int32_t*)(ws + L.slots);
   d.tiles = (int32_t*)(ws + L.tiles);
   d.counts = (int32_t*)(ws + L.counts);
+  d.plan = (int32_t*)(ws + L.plan);
+  d.max_slots = L.max_slots;
   ExpertArgs& a = p.ea;
   a = ExpertArgs{};
   a.gate = m->gate; a.up = m->up; a.down = m->down;
@@ -386,6 +380,7 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
   a.y = y;
   a.max_slots = L.max_slots;
   a.max_tiles = L.max_tiles;
+  a.plan = d.plan;
 }
 
 // event helpers for the optional per-kernel timing
@@ -400,13 +395,18 @@ static void tm_mark(hx_moe* m, int slot, int which, hipStream_t s) {
   if (which == 1) t.used[(size_t)t.calls * N_SLOTS + slot] = 1;
 }
 
-static int run_routing(hx_moe* m, Plan& p, bool decode, hipStream_t s) {
+static int run_routing(hx_moe* m, Plan& p, hipStream_t s) {
   const bool xbf = m->cfg.act_dtype == HX_BF16, rbf = m->rdt == HX_BF16;
   tm_mark(m, SLOT_ROUTER, 0, s);
-  launch_router(p.ra, xbf, rbf, decode, s);
+  launch_router(p.ra, xbf, rbf, s);
   tm_mark(m, SLOT_ROUTER, 1, s);
   HX_HIP(hipGetLastError());
-  if (!decode) {
+  if (p.ra.T <= HX_DECODE_MAX_T) {
+    tm_mark(m, SLOT_ROUTE_TOKENS, 0, s);
+    launch_route_small(p.ra, s);
+    tm_mark(m, SLOT_ROUTE_TOKENS, 1, s);
+    HX_HIP(hipGetLastError());
+  } else {
     tm_mark(m, SLOT_ROUTE_TOKENS, 0, s);
     launch_route_tokens(p.ra, s);
     tm_mark(m, SLOT_ROUTE_TOKENS, 1, s);
@@ -427,8 +427,20 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
   Plan p;
   make_plan(m, x, T, y, (uint8_t*)ws, L, bias, p);
   const bool decode = T <= HX_DECODE_MAX_T;
-  if ((rc = run_routing(m, p, decode, s))) return rc;
-  if (decode) {
+  if (decode && decode_fast_ok(p.ea)) {
+    // three kernels: router + shared gate/up, routed gate/up (routing in its
+    // prologue), down + combine
+    tm_mark(m, SLOT_ROUTER, 0, s);
+    HX_HIP(launch_router_dec(p.ra, p.ea, m->rdt == HX_BF16, s));
+    tm_mark(m, SLOT_ROUTER, 1, s);
+    tm_mark(m, SLOT_GATE_UP, 0, s);
+    HX_HIP(launch_gate_up_dec(p.ra, p.ea, s));
+    tm_mark(m, SLOT_GATE_UP, 1, s);
+    tm_mark(m, SLOT_DOWN, 0, s);
+    HX_HIP(launch_down_dec(p.ea, s));
+    tm_mark(m, SLOT_DOWN, 1, s);
+  } else if (decode) {
+    if ((rc = run_routing(m, p, s))) return rc;
     tm_mark(m, SLOT_GATE_UP, 0, s);
     HX_HIP(launch_gate_up_gemv(p.ea, s));
     tm_mark(m, SLOT_GATE_UP, 1, s);
@@ -436,6 +448,7 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
     HX_HIP(launch_down_gemv_combine(p.ea, s));
     tm_mark(m, SLOT_DOWN, 1, s);
   } else {
+    if ((rc = run_routing(m, p, s))) return rc;
     tm_mark(m, SLOT_GATE_UP, 0, s);
     HX_HIP(launch_gate_up_prefill(p.ea, s));
     tm_mark(m, SLOT_GATE_UP, 1, s);
@@ -497,7 +510,7 @@ extern "C" int hx_moe_route(hx_moe* m, const void* x, int64_t n_tokens, const fl
   if (rc) return rc;
   Plan p;
   make_plan(m, x, n_tokens, nullptr, (uint8_t*)workspace, L, router_bias, p);
-  if ((rc = run_routing(m, p, n_tokens <= HX_DECODE_MAX_T, s))) return rc;
+  if ((rc = run_routing(m, p, s))) return rc;
   const int64_t F = n_tokens * m->cfg.num_experts_per_tok;
   if (topk_idx) HX_HIP(hipMemcpyAsync(topk_idx, p.ra.d.topk_idx, 4 * F, hipMemcpyDeviceToDevice, s));
   if (topk_w) HX_HIP(hipMemcpyAsync(topk_w, p.ra.topk_w, 4 * F, hipMemcpyDeviceToDevice, s));
@@ -521,7 +534,7 @@ extern "C" int hx_moe_router_logits(hx_moe* m, const void* x, int64_t n_tokens, 
   if (rc) return rc;
   Plan p;
   make_plan(m, x, n_tokens, nullptr, (uint8_t*)ws, L, router_bias, p);
-  launch_router(p.ra, m->cfg.act_dtype == HX_BF16, m->rdt == HX_BF16, false, s);
+  launch_router(p.ra, m->cfg.act_dtype == HX_BF16, m->rdt == HX_BF16, s);
   HX_HIP(hipGetLastError());
   const int E = m->cfg.num_experts, E1 = m->E1;
   HX_HIP(hipMemcpy2DAsync(logits, sizeof(float) * E, p.ra.logits, sizeof(float) * E1, sizeof(float) * E, n_tokens,

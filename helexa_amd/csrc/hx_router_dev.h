@@ -1,0 +1,96 @@
+// Router GEMV core shared by the routing and decode kernels.
+//
+// Canonical order of a router logit (restated by the CPU checker): the H inputs
+// are cut into groups of 8 (the last may be shorter); group g belongs to lane
+// g % 64; each lane runs an fmaf chain over its groups in increasing order; the
+// 64 partials are combined by the xor butterfly 32,16,8,4,2,1; the sum is
+// rounded to the activation dtype (candle's Linear returns the input dtype,
+// crates/neuron/src/harness/arch/qwen3_5/moe.rs:134); then the optional bias.
+#pragma once
+#include "hx_internal.h"
+
+namespace hx {
+
+template <bool BF>
+HX_DEV void load8(const void* base, int64_t row_elems, int64_t row, int h0, int H, bool vec, float* out) {
+  if (vec) {
+    if (BF) {
+      const uint4 q = *(const uint4*)((const uint16_t*)base + row * row_elems + h0);
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        out[2 * j] = __uint_as_float(w[j] << 16);
+        out[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+      }
+    } else {
+      const float4* p = (const float4*)((const float*)base + row * row_elems + h0);
+      const float4 a = p[0], b = p[1];
+      out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+      out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int h = h0 + i;
+      out[i] = h < H ? (BF ? bf16_to_f32(((const uint16_t*)base)[row * row_elems + h])
+                           : ((const float*)base)[row * row_elems + h])
+                     : 0.0f;
+    }
+  }
+}
+
+// one wave: logits of tokens t0 .. t0+TT-1 for router rows e0 .. e0+TE-1
+template <bool XBF, bool RBF, int TT, int TE>
+HX_DEV void router_rows(const RouterArgs& a, int e0, int t0) {
+  const int lane = lane_id();
+  const int H = a.H, G = (H + 7) / 8;
+  const bool vec = (H & 7) == 0;
+  if (e0 >= a.E1) return;
+  float acc[TT][TE];
+#pragma unroll
+  for (int i = 0; i < TT; i++)
+#pragma unroll
+    for (int j = 0; j < TE; j++) acc[i][j] = 0.0f;
+  for (int g = lane; g < G; g += 64) {
+    const int h0 = 8 * g;
+    float xv[TT][8], wv[TE][8];
+#pragma unroll
+    for (int j = 0; j < TE; j++) {
+      if (e0 + j < a.E1) load8<RBF>(a.R, H, e0 + j, h0, H, vec, wv[j]);
+      else
+#pragma unroll
+        for (int q = 0; q < 8; q++) wv[j][q] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < TT; i++) {
+      if (t0 + i < a.T) load8<XBF>(a.x, H, t0 + i, h0, H, vec, xv[i]);
+      else
+#pragma unroll
+        for (int q = 0; q < 8; q++) xv[i][q] = 0.0f;
+    }
+    const int n = H - h0 < 8 ? H - h0 : 8;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      if (q < n) {
+#pragma unroll
+        for (int i = 0; i < TT; i++)
+#pragma unroll
+          for (int j = 0; j < TE; j++) acc[i][j] = __builtin_fmaf(xv[i][q], wv[j][q], acc[i][j]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TT; i++)
+#pragma unroll
+    for (int j = 0; j < TE; j++) {
+      float v = wave_sum<64>(acc[i][j]);
+      const int t = t0 + i, e = e0 + j;
+      if (lane == i * TE + j && t < a.T && e < a.E1) {
+        if (XBF) v = bf16_to_f32(f32_to_bf16(v));
+        if (a.bias && e < a.E) v = v + a.bias[e];
+        a.logits[(int64_t)t * a.E1 + e] = v;
+      }
+    }
+}
+
+}  // namespace hx
