@@ -82,7 +82,8 @@ struct ExpertArgs {
   const int32_t* counts;
   float* hbuf;         // [(F+T), hstride] SwiGLU activations, f32
   int hstride;
-  uint16_t* hbf;       // [(F+T), hstride] 16-bit copy: f16 for the decode kernels, bf16 for the GEMMs
+  uint16_t* hbf;       // [(F+T), hstride] f16 copy (prefill: elements swizzled in groups of 4)
+  uint16_t* xh;        // [T, H] f16 tokens in the swizzled order (prefill)
   void* obuf;          // [(F+T), H] weighted expert outputs (prefill): bf16 for bf16
                        // activations, f32 for f32 ones
   const int32_t* inv;
@@ -105,6 +106,9 @@ hipError_t launch_down_dec(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_gate_up_gemv(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_down_gemv_combine(const ExpertArgs& a, hipStream_t s);
 // prefill
+bool prefill_mfma_ok(const ExpertArgs& a);   // bf16 activations, GGUF experts: MFMA grouped GEMMs
+hipError_t launch_gate_up_mfma(const ExpertArgs& a, hipStream_t s);
+hipError_t launch_down_mfma(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_gate_up_prefill(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_down_prefill(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_combine(const ExpertArgs& a, hipStream_t s);

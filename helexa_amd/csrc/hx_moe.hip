@@ -73,7 +73,7 @@ struct hx_moe {
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct WsLayout {
-  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, hbuf, hbf, obuf, xn, ym, total;
+  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, hbuf, hbf, xh, obuf, xn, ym, total;
   int hstride, max_slots, max_tiles;
 };
 
@@ -107,6 +107,7 @@ static WsLayout ws_layout(const hx_moe* m, int64_t T) {
   L.hbf = take(sizeof(uint16_t) * (F + T) * L.hstride);
   const size_t act = m->cfg.act_dtype == HX_BF16 ? 2 : 4;
   L.obuf = decode ? 0 : take(act * (F + T) * H);
+  L.xh = decode ? 0 : take(sizeof(uint16_t) * T * H);
   L.xn = take(act * T * H);
   L.ym = take(act * T * H);
   L.total = o;
@@ -375,6 +376,7 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
   a.hstride = L.hstride;
   a.hbf = L.hbf ? (uint16_t*)(ws + L.hbf) : nullptr;
   a.obuf = L.obuf ? (void*)(ws + L.obuf) : nullptr;
+  a.xh = L.xh ? (uint16_t*)(ws + L.xh) : nullptr;
   a.inv = d.inv;
   a.topk_idx = d.topk_idx;
   a.y = y;
@@ -449,11 +451,12 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
     tm_mark(m, SLOT_DOWN, 1, s);
   } else {
     if ((rc = run_routing(m, p, s))) return rc;
+    const bool mfma = prefill_mfma_ok(p.ea);
     tm_mark(m, SLOT_GATE_UP, 0, s);
-    HX_HIP(launch_gate_up_prefill(p.ea, s));
+    HX_HIP(mfma ? launch_gate_up_mfma(p.ea, s) : launch_gate_up_prefill(p.ea, s));
     tm_mark(m, SLOT_GATE_UP, 1, s);
     tm_mark(m, SLOT_DOWN, 0, s);
-    HX_HIP(launch_down_prefill(p.ea, s));
+    HX_HIP(mfma ? launch_down_mfma(p.ea, s) : launch_down_prefill(p.ea, s));
     tm_mark(m, SLOT_DOWN, 1, s);
     tm_mark(m, SLOT_COMBINE, 0, s);
     HX_HIP(launch_combine(p.ea, s));

@@ -1,1 +1,390 @@
-// grouped-GEMM prefill kernels (MFMA) -- filled in next
+// Prefill grouped GEMMs on the matrix cores (bf16 activations, GGUF experts).
+//
+// Reference: MaybeQuantLinear's prefill arm (dequantise W, then a GEMM;
+// crates/neuron/src/harness/tp/tp_linear.rs:111-118) inside the fused MoE path
+// (three grouped GEMMs over expert-sorted rows, the routing weights folded into
+// the down GEMM, then the sum over k; crates/neuron/src/harness/tp/tp_qwen3_5.rs:1192-1225).
+//
+// Work unit: one M tile of the dispatch tile list (<= 64 permuted rows of one
+// expert, or of the shared expert) x one N tile. Operands are f16: the tokens
+// are converted once (bf16 -> f16 is exact in f16's normal range), the SwiGLU
+// activations are stored as f16, and weights are dequantised to f16 with the
+// 0x6400 pattern (f16 1024 + u, exact) and packed f16 arithmetic. Along K the
+// elements of every group of 4 are stored in the order (0, 2, 1, 3) -- in the
+// activations and in the weights alike, so the dot products are unchanged --
+// which lets two 4-bit / 8-bit codes become an f16 pair in one operation.
+//
+// Per K chunk of 128 the workgroup stages both operands in LDS (rows padded by
+// 16 bytes: the 16 lanes of a fragment read hit distinct banks) and issues
+// v_mfma_f32_16x16x32_f16 (gfx950 layout: lane l holds A[l%16][8(l/16)+i],
+// B[8(l/16)+i][l%16] and D rows 4(l/16)+i of column l%16). The next chunk's
+// global loads are issued before the current chunk's MFMAs. 52 KB of LDS per
+// workgroup: three workgroups per CU.
+#include "hx_internal.h"
+
+namespace hx {
+
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int PM = 64;            // rows of an M tile
+constexpr int PKC = 128;          // K chunk (f16 elements)
+constexpr int PLD = PKC + 8;      // LDS row pitch (f16 elements)
+
+HX_DEV h2_t h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
+HX_DEV uint32_t u32(h2_t v) { return __builtin_bit_cast(uint32_t, v); }
+HX_DEV h2_t h2s(float f) {
+  const _Float16 h = (_Float16)f;
+  return h2_t{h, h};
+}
+// position of element i of a row in the swizzled storage order
+HX_DEV int swz(int i) { return (i & ~3) | ((i & 1) << 1) | ((i >> 1) & 1); }
+
+// (1024 + u) code pairs -> f16 weights a * u - b, two per operation
+HX_DEV uint32_t fma_pair(uint32_t codes, h2_t a, h2_t nb, h2_t off) {
+  return u32(__builtin_elementwise_fma(h2(codes) + off, a, nb));
+}
+HX_DEV uint32_t mul_pair(uint32_t codes, h2_t a, h2_t off) { return u32((h2(codes) + off) * a); }
+
+// ---------------------------------------------------------------- weight chunks
+// PRaw<FMT>: one thread's raw data for 64 weights (half of a 128-wide K chunk)
+// of one row; to_lds writes them, dequantised and swizzled, into the row.
+template <int FMT>
+struct PRaw;
+
+// Q4_K (GGUF): chunk kc = half (kc & 1) of superblock kc >> 1; part pt holds
+// the 32 qs bytes of 64-element group c = 2 (kc & 1) + pt: low nibbles are
+// sub-block 2c, high nibbles sub-block 2c + 1.
+template <>
+struct PRaw<HX_Q4_K> {
+  uint4 hdr, q0, q1;
+  int c;
+  HX_DEV void load(const uint8_t* mat, int R, int K, int row, int kc, int pt) {
+    const uint8_t* p = mat + ((int64_t)row * (K / 256) + (kc >> 1)) * 144;
+    c = 2 * (kc & 1) + pt;
+    hdr = *(const uint4*)p;
+    q0 = *(const uint4*)(p + 16 + 32 * c);
+    q1 = *(const uint4*)(p + 32 + 32 * c);
+  }
+  HX_DEV void to_lds(uint16_t* dst) const {
+    const float d = f16_to_f32((uint16_t)(hdr.x & 0xffffu)), dmin = f16_to_f32((uint16_t)(hdr.x >> 16));
+    int sc0, m0, sc1, m1;
+    Chunk<HX_Q4_K>::scale_min(hdr, 2 * c, sc0, m0);
+    Chunk<HX_Q4_K>::scale_min(hdr, 2 * c + 1, sc1, m1);
+    const h2_t a0 = h2s(d * (float)sc0), nb0 = h2s(-dmin * (float)m0);
+    const h2_t a1 = h2s(d * (float)sc1), nb1 = h2s(-dmin * (float)m1);
+    const h2_t off = h2s(-1024.0f);
+    const uint32_t w[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+    uint32_t lo[16], hi[16];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      lo[2 * j] = fma_pair((w[j] & 0x000F000Fu) | 0x64006400u, a0, nb0, off);
+      lo[2 * j + 1] = fma_pair(((w[j] >> 8) & 0x000F000Fu) | 0x64006400u, a0, nb0, off);
+      hi[2 * j] = fma_pair(((w[j] >> 4) & 0x000F000Fu) | 0x64006400u, a1, nb1, off);
+      hi[2 * j + 1] = fma_pair(((w[j] >> 12) & 0x000F000Fu) | 0x64006400u, a1, nb1, off);
+    }
+    uint4* o = (uint4*)dst;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      o[v] = make_uint4(lo[4 * v], lo[4 * v + 1], lo[4 * v + 2], lo[4 * v + 3]);
+      o[4 + v] = make_uint4(hi[4 * v], hi[4 * v + 1], hi[4 * v + 2], hi[4 * v + 3]);
+    }
+  }
+};
+
+// Q8_0 planar: part pt holds blocks 4 kc + 2 pt and + 1 (64 int8 + 2 scales)
+template <>
+struct PRaw<HX_Q8_0> {
+  uint4 q[4];
+  uint32_t d;
+  HX_DEV void load(const uint8_t* mat, int R, int K, int row, int kc, int pt) {
+    const int b0 = 4 * kc + 2 * pt;
+    const uint4* p = (const uint4*)(mat + (int64_t)row * K + 32 * b0);
+#pragma unroll
+    for (int v = 0; v < 4; v++) q[v] = p[v];
+    d = *(const uint32_t*)((const uint16_t*)(mat + (int64_t)R * K) + (int64_t)row * (K / 32) + b0);
+  }
+  HX_DEV void to_lds(uint16_t* dst) const {
+    const h2_t off = h2s(-1152.0f);
+    uint4* o = (uint4*)dst;
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+      const h2_t s = h2s(f16_to_f32((uint16_t)(d >> (16 * b))));
+      const uint32_t w[8] = {q[2 * b].x, q[2 * b].y, q[2 * b].z, q[2 * b].w,
+                             q[2 * b + 1].x, q[2 * b + 1].y, q[2 * b + 1].z, q[2 * b + 1].w};
+      uint32_t r[16];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const uint32_t u = w[j] ^ 0x80808080u;                     // int8 -> q + 128
+        r[2 * j] = mul_pair(__builtin_amdgcn_perm(u, 0x64646464u, 0x00060004u), s, off);
+        r[2 * j + 1] = mul_pair(__builtin_amdgcn_perm(u, 0x64646464u, 0x00070005u), s, off);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; v++) o[4 * b + v] = make_uint4(r[4 * v], r[4 * v + 1], r[4 * v + 2], r[4 * v + 3]);
+    }
+  }
+};
+
+// Q6_K planar: chunk kc = half n = kc & 1 of superblock kc >> 1 (quarters
+// s = 0..3 of 32 elements each); part pt holds quarters pt and pt + 2: ql bytes
+// 32 pt .. +31 of the half (low / high nibble) and the half's 32 qh bytes.
+template <>
+struct PRaw<HX_Q6_K> {
+  uint4 l0, l1, h0, h1;
+  uint32_t sc;
+  uint32_t d;
+  int pt;
+  HX_DEV void load(const uint8_t* mat, int R, int K, int row, int kc, int p) {
+    const int sb = kc >> 1, n = kc & 1;
+    pt = p;
+    const uint8_t* ql = mat + (int64_t)row * (K / 2) + sb * 128 + 64 * n + 32 * pt;
+    const uint8_t* qh = mat + (int64_t)R * (K / 2) + (int64_t)row * (K / 4) + sb * 64 + 32 * n;
+    const uint8_t* s = mat + (int64_t)R * (K / 2 + K / 4) + (int64_t)row * (K / 16) + sb * 16 + 8 * n;
+    l0 = *(const uint4*)ql;
+    l1 = *(const uint4*)(ql + 16);
+    h0 = *(const uint4*)qh;
+    h1 = *(const uint4*)(qh + 16);
+    // scales of quarter pt (2pt, 2pt+1) and quarter pt+2 (2pt+4, 2pt+5)
+    sc = (uint32_t)s[2 * pt] | ((uint32_t)s[2 * pt + 1] << 8) | ((uint32_t)s[2 * pt + 4] << 16) |
+         ((uint32_t)s[2 * pt + 5] << 24);
+    d = *((const uint16_t*)(mat + (int64_t)R * (K / 2 + K / 4 + K / 16)) + (int64_t)row * (K / 256) + sb);
+  }
+  HX_DEV void to_lds(uint16_t* dst) const {
+    const float dd = f16_to_f32((uint16_t)d);
+    const h2_t off = h2s(-1056.0f);
+    const uint32_t L[8] = {l0.x, l0.y, l0.z, l0.w, l1.x, l1.y, l1.z, l1.w};
+    const uint32_t Hq[8] = {h0.x, h0.y, h0.z, h0.w, h1.x, h1.y, h1.z, h1.w};
+#pragma unroll
+    for (int qq = 0; qq < 2; qq++) {       // quarter pt + 2 qq
+      const int s = pt + 2 * qq, hs = 2 * s;
+      uint32_t r[16];
+#pragma unroll
+      for (int j = 0; j < 8; j++) {        // elements l = 4j .. 4j+3
+        const h2_t a = h2s(dd * (float)(int8_t)((sc >> (16 * qq + 8 * (j >> 2))) & 0xffu));
+        const uint32_t lq = qq ? L[j] >> 4 : L[j];
+        const uint32_t hq = hs >= 4 ? Hq[j] >> (hs - 4) : Hq[j] << (4 - hs);   // bits hs..hs+1 -> 4..5
+        r[2 * j] = mul_pair((lq & 0x000F000Fu) | (hq & 0x00300030u) | 0x64006400u, a, off);
+        r[2 * j + 1] = mul_pair(((lq >> 8) & 0x000F000Fu) | ((hq >> 8) & 0x00300030u) | 0x64006400u, a, off);
+      }
+      uint4* o = (uint4*)(dst + 32 * s - 64 * pt);   // quarter s starts at element 32 s of the chunk
+#pragma unroll
+      for (int v = 0; v < 4; v++) o[v] = make_uint4(r[4 * v], r[4 * v + 1], r[4 * v + 2], r[4 * v + 3]);
+    }
+  }
+};
+
+// ---------------------------------------------------------------- A tile
+// 64 gathered f16 rows x 128 of K chunk kc; thread: row t/4, 32 elements
+struct ARaw {
+  uint4 v[4];
+  HX_DEV void load(const uint16_t* src, int64_t stride, const int* rowsrc, int rows, int kc) {
+    const int r = threadIdx.x >> 2, seg = threadIdx.x & 3;
+    if (r < rows) {
+      const uint4* s = (const uint4*)(src + (int64_t)rowsrc[r] * stride + kc * PKC + 32 * seg);
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[i] = s[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++) v[i] = make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  HX_DEV void to_lds(uint16_t* As) const {
+    uint4* d = (uint4*)(As + (threadIdx.x >> 2) * PLD + 32 * (threadIdx.x & 3));
+#pragma unroll
+    for (int i = 0; i < 4; i++) d[i] = v[i];
+  }
+};
+
+HX_DEV f16x8_t frag(const uint16_t* base) { return __builtin_bit_cast(f16x8_t, *(const uint4*)base); }
+
+// ---------------------------------------------------------------- gate/up
+// grid (I / 64, tiles): 64 rows x 64 intermediate columns; wave w owns columns
+// 16w .. 16w+15 of gate and of up for all 64 rows. h = silu(gate) * up is
+// written as f16 in the swizzled order.
+template <int FMT>
+__global__ __launch_bounds__(256) void k_gate_up_mfma(ExpertArgs a) {
+  __shared__ uint16_t As[PM * PLD];
+  __shared__ uint16_t Bs[128 * PLD];
+  __shared__ int rowsrc[PM];
+  const int tile = blockIdx.y;
+  if (tile >= a.counts[1]) return;
+  const int e = a.tiles[4 * tile + 1], p0 = a.tiles[4 * tile + 2], rows = a.tiles[4 * tile + 3];
+  const bool sh = e == a.E;
+  const int I = sh ? a.Is : a.I, n0 = blockIdx.x * 64;
+  if (n0 >= I) return;
+  const uint8_t* G = sh ? a.sgate.base : a.gate.mat(e);
+  const uint8_t* U = sh ? a.sup.base : a.up.mat(e);
+  const int K = a.H, nk = K / PKC;
+  if (threadIdx.x < PM) {
+    const int p = p0 + threadIdx.x;
+    rowsrc[threadIdx.x] = threadIdx.x < rows ? (sh ? p - a.F : a.perm[p] / a.k) : 0;
+  }
+  __syncthreads();
+  const int lane = lane_id(), wave = threadIdx.x >> 6, l16 = lane & 15, kq = lane >> 4;
+  const int brow = threadIdx.x >> 1, bpt = threadIdx.x & 1;
+  const uint8_t* Wm = brow < 64 ? G : U;
+  const int wrow = n0 + (brow & 63);
+  f32x4_t accg[4], accu[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    accg[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    accu[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  ARaw ar;
+  PRaw<FMT> br;
+  ar.load(a.xh, K, rowsrc, rows, 0);
+  br.load(Wm, I, K, wrow, 0, bpt);
+  for (int kc = 0; kc < nk; kc++) {
+    ar.to_lds(As);
+    br.to_lds(Bs + brow * PLD + 64 * bpt);
+    if (kc + 1 < nk) {
+      ar.load(a.xh, K, rowsrc, rows, kc + 1);
+      br.load(Wm, I, K, wrow, kc + 1, bpt);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < PKC / 32; ks++) {
+      const int ko = 32 * ks + 8 * kq;
+      const f16x8_t bg = frag(Bs + (16 * wave + l16) * PLD + ko);
+      const f16x8_t bu = frag(Bs + (64 + 16 * wave + l16) * PLD + ko);
+#pragma unroll
+      for (int mt = 0; mt < 4; mt++) {
+        const f16x8_t av = frag(As + (16 * mt + l16) * PLD + ko);
+        accg[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bg, accg[mt], 0, 0, 0);
+        accu[mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bu, accu[mt], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+  const int col = swz(n0 + 16 * wave + l16);
+#pragma unroll
+  for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int m = 16 * mt + 4 * kq + i;
+      if (m < rows) ((_Float16*)a.hbf)[(int64_t)(p0 + m) * a.hstride + col] = (_Float16)(siluf_(accg[mt][i]) * accu[mt][i]);
+    }
+}
+
+// ---------------------------------------------------------------- down
+// grid (H / 128, tiles): 64 rows x 128 output columns; wave w owns columns
+// 32w .. 32w+31. Rows are scaled by their routing weight (shared expert: the
+// sigmoid gate) and written to the per-assignment output rows.
+template <int FMT>
+__global__ __launch_bounds__(256) void k_down_mfma(ExpertArgs a) {
+  __shared__ uint16_t As[PM * PLD];
+  __shared__ uint16_t Bs[128 * PLD];
+  __shared__ int rowsrc[PM];
+  __shared__ float rw[PM];
+  const int tile = blockIdx.y;
+  if (tile >= a.counts[1]) return;
+  const int e = a.tiles[4 * tile + 1], p0 = a.tiles[4 * tile + 2], rows = a.tiles[4 * tile + 3];
+  const bool sh = e == a.E;
+  const int K = sh ? a.Is : a.I, n0 = blockIdx.x * 128, nk = K / PKC;
+  const uint8_t* W = sh ? a.sdown.base : a.down.mat(e);
+  if (threadIdx.x < PM) {
+    const int p = p0 + threadIdx.x;
+    rowsrc[threadIdx.x] = p0 + (threadIdx.x < rows ? threadIdx.x : 0);
+    rw[threadIdx.x] = threadIdx.x < rows ? (sh ? a.sgw[p - a.F] : a.topk_w[a.perm[p]]) : 0.f;
+  }
+  __syncthreads();
+  const int lane = lane_id(), wave = threadIdx.x >> 6, l16 = lane & 15, kq = lane >> 4;
+  const int brow = threadIdx.x >> 1, bpt = threadIdx.x & 1;
+  f32x4_t acc[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[j][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  ARaw ar;
+  PRaw<FMT> br;
+  ar.load(a.hbf, a.hstride, rowsrc, rows, 0);
+  br.load(W, a.H, K, n0 + brow, 0, bpt);
+  for (int kc = 0; kc < nk; kc++) {
+    ar.to_lds(As);
+    br.to_lds(Bs + brow * PLD + 64 * bpt);
+    if (kc + 1 < nk) {
+      ar.load(a.hbf, a.hstride, rowsrc, rows, kc + 1);
+      br.load(W, a.H, K, n0 + brow, kc + 1, bpt);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < PKC / 32; ks++) {
+      const int ko = 32 * ks + 8 * kq;
+      f16x8_t bv[2];
+#pragma unroll
+      for (int j = 0; j < 2; j++) bv[j] = frag(Bs + (32 * wave + 16 * j + l16) * PLD + ko);
+#pragma unroll
+      for (int mt = 0; mt < 4; mt++) {
+        const f16x8_t av = frag(As + (16 * mt + l16) * PLD + ko);
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv[j], acc[j][mt], 0, 0, 0);
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int col = n0 + 32 * wave + 16 * j + l16;
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int m = 16 * mt + 4 * kq + i;
+        if (m < rows) ((uint16_t*)a.obuf)[(int64_t)(p0 + m) * a.H + col] = f32_to_bf16(rw[m] * acc[j][mt][i]);
+      }
+  }
+}
+
+// ---------------------------------------------------------------- tokens -> f16
+// bf16 [T][H] -> f16 [T][H] in the swizzled element order; one thread per 8
+__global__ __launch_bounds__(256) void k_x_to_f16(const uint16_t* x, int64_t n8, uint16_t* xh) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const uint4 v = ((const uint4*)x)[i];
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+  uint32_t h[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const h2_t p = {(_Float16)__uint_as_float(w[j] << 16), (_Float16)__uint_as_float(w[j] & 0xffff0000u)};
+    h[j] = u32(p);
+  }
+  uint4 o;   // (e0,e1)(e2,e3) -> (e0,e2)(e1,e3)
+  o.x = __builtin_amdgcn_perm(h[1], h[0], 0x05040100u);
+  o.y = __builtin_amdgcn_perm(h[1], h[0], 0x07060302u);
+  o.z = __builtin_amdgcn_perm(h[3], h[2], 0x05040100u);
+  o.w = __builtin_amdgcn_perm(h[3], h[2], 0x07060302u);
+  ((uint4*)xh)[i] = o;
+}
+
+// ---------------------------------------------------------------- launchers
+bool prefill_mfma_ok(const ExpertArgs& a) {
+  auto q = [](int f) { return f == HX_Q4_K || f == HX_Q8_0 || f == HX_Q6_K; };
+  return a.xbf && q(a.gate.fmt) && q(a.down.fmt) && a.H % 256 == 0 && a.I % 256 == 0 && (a.Is == 0 || a.Is == a.I);
+}
+
+hipError_t launch_gate_up_mfma(const ExpertArgs& a, hipStream_t s) {
+  const int64_t n8 = (int64_t)a.T * a.H / 8;
+  hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, (const uint16_t*)a.x, n8, a.xh);
+  const dim3 grid(a.I / 64, a.max_tiles);
+  switch (a.gate.fmt) {
+    case HX_Q4_K: hipLaunchKernelGGL(k_gate_up_mfma<HX_Q4_K>, grid, dim3(256), 0, s, a); break;
+    case HX_Q8_0: hipLaunchKernelGGL(k_gate_up_mfma<HX_Q8_0>, grid, dim3(256), 0, s, a); break;
+    case HX_Q6_K: hipLaunchKernelGGL(k_gate_up_mfma<HX_Q6_K>, grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_down_mfma(const ExpertArgs& a, hipStream_t s) {
+  const dim3 grid(a.H / 128, a.max_tiles);
+  switch (a.down.fmt) {
+    case HX_Q4_K: hipLaunchKernelGGL(k_down_mfma<HX_Q4_K>, grid, dim3(256), 0, s, a); break;
+    case HX_Q8_0: hipLaunchKernelGGL(k_down_mfma<HX_Q8_0>, grid, dim3(256), 0, s, a); break;
+    case HX_Q6_K: hipLaunchKernelGGL(k_down_mfma<HX_Q6_K>, grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace hx

@@ -263,3 +263,26 @@ def test_invalid_configs_are_rejected():
     with pytest.raises(hx.HxError) as e:
         hx.Qwen3_5MoeBlock.load(qcfg, wq, act_dtype=hx.F32)
     assert e.value.code == 1
+
+
+def test_forward_q8_0_prefill_sampled_tokens(c2):
+    """prefill (MFMA grouped GEMMs) on the C2 block: 300 tokens, ragged M tiles"""
+    x = c2.x(300, seed=9)
+    y = c2.block.forward(x).float().cpu().numpy()
+    sample = np.array([0, 1, 57, 150, 299])
+    assert rel_err(y[sample], c2.oracle.forward(x_np(x)[sample])) <= TOL_BF16
+
+
+def test_forward_skewed_routing_prefill(c2):
+    """Zipf router bias: a few experts take most rows, so their segments span
+    several 64-row M tiles (the skewed-prefill shape)."""
+    _, synth = _hx()
+    bias = synth.zipf_bias(c2.cfg.num_experts, 1.1, 8.0, 5)
+    x = c2.x(700, seed=10)
+    r = c2.block.route(x, router_bias=bias)
+    counts = np.diff(r["offsets"].cpu().numpy())
+    assert counts.max() > 128                       # at least one expert spans 3+ tiles
+    y = c2.block.forward(x, router_bias=bias).float().cpu().numpy()
+    sample = np.array([3, 100, 350, 699])
+    ref = c2.oracle.forward(x_np(x)[sample], bias=bias.cpu().numpy())
+    assert rel_err(y[sample], ref) <= TOL_BF16
