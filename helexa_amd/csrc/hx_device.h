@@ -60,12 +60,11 @@ HX_DEV uint16_t f32_to_f16(float f) {
 // exp for the router softmax: Cody-Waite split of ln2 (0.693145751953125 +
 // 1.42860682030941723212e-6, the Cephes constants), degree-7 Taylor
 // polynomial in Horner form with fmaf, exact 2^n scaling. x < -87 -> 0,
-// x > 88.5 -> +inf.
+// x > 88.5 -> +inf, NaN -> NaN. Written with selects only (no branches): the
+// special cases are computed alongside and picked at the end.
 HX_DEV float expf_route(float x) {
-  if (x != x) return x;
-  if (x < -87.0f) return 0.0f;
-  if (x > 88.5f) return __builtin_inff();
   float n = __builtin_rintf(x * 1.44269504088896341f);
+  n = fminf(fmaxf(n, -127.0f), 128.0f);   // only reached for |x| outside the range handled below
   float r = __builtin_fmaf(n, -0.693145751953125f, x);
   r = __builtin_fmaf(n, -1.42860682030941723212e-6f, r);
   float p = 1.98412698412698413e-4f;
@@ -76,19 +75,85 @@ HX_DEV float expf_route(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  int ni = (int)n;
-  if (ni > 127) return p * __uint_as_float((uint32_t)(127 + 127) << 23) * 2.0f;
-  return p * __uint_as_float((uint32_t)(ni + 127) << 23);
+  const int ni = (int)n;
+  float res = p * __uint_as_float((uint32_t)((ni > 127 ? 127 : ni) + 127) << 23);
+  res = ni > 127 ? res * 2.0f : res;
+  res = x < -87.0f ? 0.0f : res;
+  res = x > 88.5f ? __builtin_inff() : res;
+  return x != x ? x : res;
+}
+
+// expf_route over N values, step by step across the N values so that the N
+// independent dependency chains interleave (a single wave is latency-bound on
+// one chain). Same arithmetic as expf_route.
+template <int N>
+HX_DEV void expf_route_n(float* x) {
+  float n[N], r[N], p[N];
+#pragma unroll
+  for (int i = 0; i < N; i++) n[i] = fminf(fmaxf(__builtin_rintf(x[i] * 1.44269504088896341f), -127.0f), 128.0f);
+#pragma unroll
+  for (int i = 0; i < N; i++) r[i] = __builtin_fmaf(n[i], -0.693145751953125f, x[i]);
+#pragma unroll
+  for (int i = 0; i < N; i++) r[i] = __builtin_fmaf(n[i], -1.42860682030941723212e-6f, r[i]);
+#pragma unroll
+  for (int i = 0; i < N; i++) p[i] = __builtin_fmaf(1.98412698412698413e-4f, r[i], 1.38888888888888889e-3f);
+#pragma unroll
+  for (int i = 0; i < N; i++) p[i] = __builtin_fmaf(p[i], r[i], 8.33333333333333333e-3f);
+#pragma unroll
+  for (int i = 0; i < N; i++) p[i] = __builtin_fmaf(p[i], r[i], 4.16666666666666667e-2f);
+#pragma unroll
+  for (int i = 0; i < N; i++) p[i] = __builtin_fmaf(p[i], r[i], 1.66666666666666667e-1f);
+#pragma unroll
+  for (int i = 0; i < N; i++) p[i] = __builtin_fmaf(p[i], r[i], 0.5f);
+#pragma unroll
+  for (int i = 0; i < N; i++) p[i] = __builtin_fmaf(p[i], r[i], 1.0f);
+#pragma unroll
+  for (int i = 0; i < N; i++) p[i] = __builtin_fmaf(p[i], r[i], 1.0f);
+#pragma unroll
+  for (int i = 0; i < N; i++) {
+    const int ni = (int)n[i];
+    float res = p[i] * __uint_as_float((uint32_t)((ni > 127 ? 127 : ni) + 127) << 23);
+    res = ni > 127 ? res * 2.0f : res;
+    res = x[i] < -87.0f ? 0.0f : res;
+    res = x[i] > 88.5f ? __builtin_inff() : res;
+    x[i] = x[i] != x[i] ? x[i] : res;
+  }
 }
 
 HX_DEV float sigmoidf_(float v) { return 1.0f / (1.0f + __expf(-v)); }
 HX_DEV float siluf_(float g) { return g / (1.0f + __expf(-g)); }
 
-// xor butterfly over the low `width` lanes (width a power of two <= 64)
+// Xor butterfly over aligned groups of WIDTH lanes (WIDTH a power of two <= 64):
+// for off = WIDTH/2 .. 1, every lane adds the value of lane (lane ^ off). Float
+// addition is commutative, so both lanes of a pair hold the same sum and the
+// result is the same in every lane of a group. Register-only exchanges:
+//   off 32 / 16: v_permlane32_swap / v_permlane16_swap of v with itself; the two
+//     results hold (own, partner) in some order in every lane;
+//   off 8: DPP row_ror:8, which is lane ^ 8 within a row of 16;
+//   off 4: DPP row_ror:4 gives lane (r + 4) mod 16, which is r ^ 4 or r ^ 4 ^ 8;
+//     once the off-8 step is done, lanes r ^ 4 and r ^ 4 ^ 8 hold equal values;
+//   off 2 / 1: DPP quad_perm [2,3,0,1] / [1,0,3,2].
+// Groups of 8 lanes use __shfl_xor for the off-4 step.
+template <int CTRL>
+HX_DEV float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+
 template <int WIDTH>
 HX_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int off = WIDTH / 2; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
+  if (WIDTH >= 64) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if (WIDTH >= 32) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+  if (WIDTH >= 16) v = v + dpp_f<0x128>(v);   // row_ror:8
+  if (WIDTH >= 16) v = v + dpp_f<0x124>(v);   // row_ror:4 (see above)
+  else if (WIDTH >= 8) v = v + __shfl_xor(v, 4, 64);
+  if (WIDTH >= 4) v = v + dpp_f<0x4E>(v);     // quad_perm [2,3,0,1]
+  if (WIDTH >= 2) v = v + dpp_f<0xB1>(v);     // quad_perm [1,0,3,2]
   return v;
 }
 
@@ -121,6 +186,18 @@ HX_DEV float wave_max_dpp(float v) {
   v = fmaxf(v, __int_as_float(dpp_mov<0x142, 0xA>(__float_as_int(v))));  // row_bcast15
   v = fmaxf(v, __int_as_float(dpp_mov<0x143, 0xC>(__float_as_int(v))));  // row_bcast31
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// wave-wide max of unsigned values (identity 0, so the DPP moves fold into
+// v_max_u32_dpp), returned to every lane
+HX_DEV uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x141, 0xf, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xf, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));
+  v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 HX_DEV int wave_min_dpp(int v) {

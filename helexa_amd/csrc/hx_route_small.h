@@ -25,11 +25,84 @@ struct RouteSmem {
   int nroute;
 };
 
+// Descending sort of one lane's EPL keys (hi = probability bits, lo = ~expert):
+// comparing (hi, lo) as one 64-bit value orders by probability, then by lower
+// expert id. Sorting networks: Batcher's odd-even merge sort for 8, bitonic
+// otherwise.
+HX_DEV void key_cas(uint32_t& ah, uint32_t& al, uint32_t& bh, uint32_t& bl) {
+  const uint64_t a = ((uint64_t)ah << 32) | al, b = ((uint64_t)bh << 32) | bl;
+  const bool sw = b > a;
+  const uint32_t th = sw ? bh : ah, tl = sw ? bl : al;
+  bh = sw ? ah : bh;
+  bl = sw ? al : bl;
+  ah = th;
+  al = tl;
+}
+
+template <int EPL>
+HX_DEV void sort_keys_desc(uint32_t* h, uint32_t* l) {
+  if (EPL == 8) {
+    constexpr int P[19][2] = {{0, 1}, {2, 3}, {4, 5}, {6, 7}, {0, 2}, {1, 3}, {4, 6}, {5, 7}, {1, 2}, {5, 6},
+                              {0, 4}, {1, 5}, {2, 6}, {3, 7}, {2, 4}, {3, 5}, {1, 2}, {3, 4}, {5, 6}};
+#pragma unroll
+    for (int c = 0; c < 19; c++) key_cas(h[P[c][0]], l[P[c][0]], h[P[c][1]], l[P[c][1]]);
+    return;
+  }
+#pragma unroll
+  for (int kk = 2; kk <= EPL; kk *= 2)
+#pragma unroll
+    for (int jj = kk / 2; jj > 0; jj /= 2)
+#pragma unroll
+      for (int i = 0; i < EPL; i++) {
+        const int q = i ^ jj;
+        if (q > i) {
+          if ((i & kk) == 0) key_cas(h[i], l[i], h[q], l[q]);
+          else key_cas(h[q], l[q], h[i], l[i]);
+        }
+      }
+}
+
 // One wave routes one token: softmax over E with expf_route and the
-// lane-strided butterfly sum, then k rounds of selection -- the largest
-// probability not yet taken, ties to the lowest expert id (a DPP max of the
-// per-lane best, then a DPP min of the ids holding it) -- and the sequential
-// renormalisation in rank order. Lane j < k returns rank j's (expert, weight).
+// lane-strided butterfly sum, then the k largest probabilities, ties to the
+// lowest expert id, and the sequential renormalisation in rank order. Lane
+// j < k returns rank j's (expert, weight).
+//
+// Selection: expert e lives in lane e % 64; each lane sorts its EPL keys
+// (probability bits, ~e) in descending order once (so a lane's equal
+// probabilities are ordered by expert id). Probabilities are >= 0, so their bit
+// patterns order like the values; padding (e >= E) has key (0, ~e).
+//   fast pass: each round takes the wave-wide largest head probability (one DPP
+//     reduction) and pops every lane whose head equals it; the round body is
+//     branch-free. It is exact unless two lanes ever hold that maximum at once;
+//   exact pass (only when that happened): each round reduces the heads as
+//     (probability, ~expert) pairs, so the lowest expert id wins a tie.
+template <int EPL>
+HX_DEV void route_rounds_exact(uint32_t* h, uint32_t* l, int k, float& my_p, int& my_e, float& tot) {
+  const int lane = lane_id();
+  for (int r = 0; r < k; r++) {
+    const uint32_t m = wave_max_u32(h[0]);
+    const unsigned long long hold = __ballot(h[0] == m);
+    uint32_t lo;
+    if (__popcll(hold) == 1)
+      lo = (uint32_t)__builtin_amdgcn_readlane((int)l[0], __ffsll((long long)hold) - 1);
+    else
+      lo = wave_max_u32(h[0] == m ? l[0] : 0u);
+    const int e = (int)~lo;
+    const uint32_t wm = (e & 63) == lane ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int j = 0; j + 1 < EPL; j++) {
+      h[j] = (h[j] & ~wm) | (h[j + 1] & wm);
+      l[j] = (l[j] & ~wm) | (l[j + 1] & wm);
+    }
+    h[EPL - 1] &= ~wm;
+    l[EPL - 1] &= ~wm;
+    const float pm = __uint_as_float(m);
+    tot = tot + pm;
+    my_p = lane == r ? pm : my_p;
+    my_e = lane == r ? e : my_e;
+  }
+}
+
 template <int EPL>
 HX_DEV void route_token_core(const float* lg, int E, int k, bool norm, int& out_e, float& out_w) {
   const int lane = lane_id();
@@ -38,46 +111,68 @@ HX_DEV void route_token_core(const float* lg, int E, int k, bool norm, int& out_
 #pragma unroll
   for (int j = 0; j < EPL; j++) {
     const int e = lane + 64 * j;
-    v[j] = e < E ? lg[e] : -__builtin_inff();
+    const float x = lg[e < E ? e : E - 1];
+    v[j] = e < E ? x : -__builtin_inff();
     mx = v[j] > mx ? v[j] : mx;
   }
   mx = wave_max_dpp(mx);
+#pragma unroll
+  for (int j = 0; j < EPL; j++) v[j] = v[j] - mx;
+  expf_route_n<EPL>(v);   // padding: exp(-inf) = 0
   float s = 0.0f;
 #pragma unroll
-  for (int j = 0; j < EPL; j++) {
-    if (lane + 64 * j < E) {
-      v[j] = expf_route(v[j] - mx);
-      s = s + v[j];
-    }
-  }
+  for (int j = 0; j < EPL; j++) s = s + v[j];
   s = wave_sum<64>(s);
+  uint32_t h[EPL], l[EPL], h0[EPL], l0[EPL];
 #pragma unroll
-  for (int j = 0; j < EPL; j++) v[j] = lane + 64 * j < E ? v[j] / s : -1.0f;
+  for (int j = 0; j < EPL; j++) {
+    h[j] = __float_as_uint(v[j] / s);   // padding: 0 / s = +0
+    l[j] = ~(uint32_t)(lane + 64 * j);
+  }
+  sort_keys_desc<EPL>(h, l);
+#pragma unroll
+  for (int j = 0; j < EPL; j++) {
+    h0[j] = h[j];
+    l0[j] = l[j];
+  }
   float my_p = 0.0f, tot = 0.0f;
   int my_e = 0;
-  uint32_t taken = 0;
+  unsigned long long multi = 0;
+  // The pop of round r is split: the head h[0] is replaced at once (the next
+  // reduction needs it); the rest of the shift is applied during the next
+  // round's reduction, which does not depend on it.
+  uint32_t pend = 0u;   // all-ones in the lanes popped by the previous round
   for (int r = 0; r < k; r++) {
-    float bm = -2.0f;
-    int bj = 0;
+    uint32_t x = h[0];
+    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xf, 0xf, false));
 #pragma unroll
-    for (int j = 0; j < EPL; j++)
-      if (!((taken >> j) & 1u) && v[j] > bm) {
-        bm = v[j];
-        bj = j;
-      }
-    const float m = wave_max_dpp(bm);
-    const unsigned long long holders = __ballot(bm == m);
-    int e;
-    if (__popcll(holders) == 1)   // the usual case: one lane holds the maximum
-      e = __builtin_amdgcn_readlane(lane + 64 * bj, __ffsll((long long)holders) - 1);
-    else                          // equal probabilities: the lowest expert id
-      e = wave_min_dpp(bm == m ? lane + 64 * bj : 0x7fffffff);
-    if ((e & 63) == lane) taken |= 1u << (e >> 6);
-    tot = tot + m;
-    if (lane == r) {
-      my_p = m;
-      my_e = e;
-    }
+    for (int j = 1; j + 1 < EPL; j++) h[j] = (h[j] & ~pend) | (h[j + 1] & pend);
+    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xf, 0xf, false));
+    if (EPL > 1) h[EPL - 1] &= ~pend;
+    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xf, 0xf, false));
+#pragma unroll
+    for (int j = 0; j + 1 < EPL; j++) l[j] = (l[j] & ~pend) | (l[j + 1] & pend);
+    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x140, 0xf, 0xf, false));
+    l[EPL - 1] &= ~pend;
+    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false));
+    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false));
+    const uint32_t m = (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+    const bool hit = h[0] == m;
+    pend = hit ? 0xffffffffu : 0u;
+    h[0] = EPL > 1 ? ((h[0] & ~pend) | (h[1] & pend)) : (h[0] & ~pend);
+    const unsigned long long hold = __ballot(hit);
+    multi |= hold & (hold - 1);
+    const int e = (int)~(uint32_t)__builtin_amdgcn_readlane((int)l[0], __ffsll((long long)hold) - 1);
+    const float pm = __uint_as_float(m);
+    tot = tot + pm;
+    my_p = lane == r ? pm : my_p;
+    my_e = lane == r ? e : my_e;
+  }
+  if (multi) {   // two lanes held an equal maximum: redo the selection exactly
+    my_p = 0.0f;
+    tot = 0.0f;
+    my_e = 0;
+    route_rounds_exact<EPL>(h0, l0, k, my_p, my_e, tot);
   }
   out_e = my_e;
   out_w = norm ? my_p / tot : my_p;

@@ -39,9 +39,81 @@ HX_DEV void load8(const void* base, int64_t row_elems, int64_t row, int h0, int 
   }
 }
 
-// one wave: logits of tokens t0 .. t0+TT-1 for router rows e0 .. e0+TE-1
+// One wave: logits of tokens t0 .. t0+TT-1 for router rows e0 .. e0+TE-1, for
+// H % 8 == 0 and at most 64 * NG groups of 8. Every load of the wave is issued
+// before the first multiply-add (addresses are clamped into range and the
+// values of out-of-range groups, rows and tokens replaced by zeros afterwards),
+// so a wave waits for memory once. Same arithmetic order as the loop version.
+template <bool XBF, bool RBF, int TT, int TE, int NG>
+HX_DEV void router_rows_u(const RouterArgs& a, int e0, int t0) {
+  constexpr int RW = RBF ? 4 : 8, XW = XBF ? 4 : 8;   // dwords per group of 8 values
+  const int lane = lane_id();
+  const int H = a.H, G = H / 8;
+  uint32_t wr[TE][NG][RW], xr[TT][NG][XW];
+#pragma unroll
+  for (int i = 0; i < NG; i++) {
+    const int g = min(lane + 64 * i, G - 1);
+#pragma unroll
+    for (int j = 0; j < TE; j++) {
+      const int64_t row = min(e0 + j, a.E1 - 1);
+      const uint4* p = (const uint4*)((const uint8_t*)a.R + (row * H + 8 * g) * (RBF ? 2 : 4));
+#pragma unroll
+      for (int q = 0; q < RW / 4; q++) {
+        const uint4 v = p[q];
+        wr[j][i][4 * q] = v.x; wr[j][i][4 * q + 1] = v.y; wr[j][i][4 * q + 2] = v.z; wr[j][i][4 * q + 3] = v.w;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+      const int64_t tok = min(t0 + t, a.T - 1);
+      const uint4* p = (const uint4*)((const uint8_t*)a.x + (tok * H + 8 * g) * (XBF ? 2 : 4));
+#pragma unroll
+      for (int q = 0; q < XW / 4; q++) {
+        const uint4 v = p[q];
+        xr[t][i][4 * q] = v.x; xr[t][i][4 * q + 1] = v.y; xr[t][i][4 * q + 2] = v.z; xr[t][i][4 * q + 3] = v.w;
+      }
+    }
+  }
+  float acc[TT][TE];
+#pragma unroll
+  for (int t = 0; t < TT; t++)
+#pragma unroll
+    for (int j = 0; j < TE; j++) acc[t][j] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NG; i++) {
+    if (lane + 64 * i >= G) break;   // this lane's remaining groups are past the end
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+#pragma unroll
+      for (int t = 0; t < TT; t++) {
+        const float xv = XBF ? __uint_as_float(q & 1 ? xr[t][i][q / 2] & 0xffff0000u : xr[t][i][q / 2] << 16)
+                             : __uint_as_float(xr[t][i][q]);
+#pragma unroll
+        for (int j = 0; j < TE; j++) {
+          const float wv = RBF ? __uint_as_float(q & 1 ? wr[j][i][q / 2] & 0xffff0000u : wr[j][i][q / 2] << 16)
+                               : __uint_as_float(wr[j][i][q]);
+          acc[t][j] = __builtin_fmaf(xv, wv, acc[t][j]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TT; t++)
+#pragma unroll
+    for (int j = 0; j < TE; j++) {
+      float v = wave_sum<64>(acc[t][j]);
+      const int tt = t0 + t, e = e0 + j;
+      if (lane == t * TE + j && tt < a.T && e < a.E1) {
+        if (XBF) v = bf16_to_f32(f32_to_bf16(v));
+        if (a.bias && e < a.E) v = v + a.bias[e];
+        a.logits[(int64_t)tt * a.E1 + e] = v;
+      }
+    }
+}
+
+// any H: groups loaded one at a time
 template <bool XBF, bool RBF, int TT, int TE>
-HX_DEV void router_rows(const RouterArgs& a, int e0, int t0) {
+HX_DEV void router_rows_loop(const RouterArgs& a, int e0, int t0) {
   const int lane = lane_id();
   const int H = a.H, G = (H + 7) / 8;
   const bool vec = (H & 7) == 0;
@@ -91,6 +163,19 @@ HX_DEV void router_rows(const RouterArgs& a, int e0, int t0) {
         a.logits[(int64_t)t * a.E1 + e] = v;
       }
     }
+}
+
+// one wave: logits of tokens t0 .. t0+TT-1 for router rows e0 .. e0+TE-1
+template <bool XBF, bool RBF, int TT, int TE>
+HX_DEV void router_rows(const RouterArgs& a, int e0, int t0) {
+  if (e0 >= a.E1) return;
+  if ((a.H & 7) == 0) {
+    const int G = a.H / 8;
+    if (G <= 64) { router_rows_u<XBF, RBF, TT, TE, 1>(a, e0, t0); return; }
+    if (G <= 128) { router_rows_u<XBF, RBF, TT, TE, 2>(a, e0, t0); return; }
+    if (G <= 256) { router_rows_u<XBF, RBF, TT, TE, 4>(a, e0, t0); return; }
+  }
+  router_rows_loop<XBF, RBF, TT, TE>(a, e0, t0);
 }
 
 }  // namespace hx
