@@ -39,6 +39,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
 MFMA_BF16_PEAK_TFS = 2516.6     # dense bf16: 256 CU x 4096 flop/clk x 2.4 GHz
 METRIC = "MoE-layer decode µs + % HBM peak; prefill tok/s + % MFMA peak (Q4_K_M)"
+KERNEL_NAMES = {"router": "k_router_dec", "gate_up": "k_gate_up_dec", "down": "k_down_dec"}
 
 
 def log(*a):
@@ -51,17 +52,22 @@ def gguf_bytes(fmt, rows, cols):
 
 
 def step_bytes(cfg, fmts, unique_experts, T):
-    """algorithmic HBM bytes of one forward (every touched weight byte once, the
-    tokens in and out once) and per kernel (each kernel's weights plus the
-    activations it must read or write)"""
+    """Algorithmic HBM bytes of one decode forward (every touched weight byte once,
+    the tokens in and out once), in total and per kernel of the decode path:
+      router  -- router rows + shared-expert gate row (bf16), the shared expert's
+                 gate/up projections, the tokens;
+      gate_up -- the routed experts' gate/up projections, the tokens;
+      down    -- the routed and shared down projections, the output rows.
+    The SwiGLU activations passed between kernels are intermediates and are not
+    counted."""
     H, E, I, Is = cfg.hidden_size, cfg.num_experts, cfg.moe_intermediate_size, cfg.shared_expert_intermediate_size
     act = T * H * 2
-    router_w = (E + 1) * H * 2                  # router rows + shared-expert gate row, bf16
-    gate_up_w = (unique_experts * (gguf_bytes(fmts["gate"], I, H) + gguf_bytes(fmts["up"], I, H))
-                 + gguf_bytes(fmts["sgate"], Is, H) + gguf_bytes(fmts["sup"], Is, H))
+    router_w = (E + 1) * H * 2
+    shared_gu = gguf_bytes(fmts["sgate"], Is, H) + gguf_bytes(fmts["sup"], Is, H)
+    routed_gu = unique_experts * (gguf_bytes(fmts["gate"], I, H) + gguf_bytes(fmts["up"], I, H))
     down_w = unique_experts * gguf_bytes(fmts["down"], H, I) + gguf_bytes(fmts["sdown"], H, Is)
-    total = router_w + gate_up_w + down_w + 2 * act
-    return total, {"router": router_w + act, "gate_up": gate_up_w + act, "down": down_w + act}
+    total = router_w + shared_gu + routed_gu + down_w + 2 * act
+    return total, {"router": router_w + shared_gu + act, "gate_up": routed_gu + act, "down": down_w + act}
 
 
 def build_layers(cfg, fmts, n_layers, seed, keep_host_copy_of_first=False):
@@ -158,6 +164,8 @@ def bench_decode(args):
     d_us = kern_us.get(dominant, float("nan"))
     achieved = kbytes[dominant] / (d_us * 1e-6) / 1e9
     layer_gbs = total_bytes / (us_per_layer * 1e-6) / 1e9
+    from helexa_amd.profsum import read_pmc
+    traffic = read_pmc(os.path.join(ROOT, "profiles", "c2_decode_pmc.txt"), KERNEL_NAMES[dominant])
 
     # the graph's last write of ys[0] came from layer 0 on xs[0]: it must equal an
     # eager forward bit for bit
@@ -166,7 +174,9 @@ def bench_decode(args):
     out = {
         "metric": METRIC, "value": round(us_per_layer, 3), "unit": "us/layer (C2 decode)",
         "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(us_per_layer / 1e3, 6),
-        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+        "dtype_note": "expert products f16 x f16 (Q8_0 codes exact in f16, bf16 tokens converted) with f32 "
+                      "accumulation; router bf16 x bf16 f32 fmaf",
         "data": "synthetic (seeded N(0,0.02) weights quantised to GGUF Q8_0 on device; bf16 N(0,1) tokens)",
         "config": {"workload": "C2: Qwen3-Next-80B-A3B MoE layer decode, T=1, Q8_0 experts, bf16 router+acts",
                    "hidden": cfg.hidden_size, "experts": cfg.num_experts, "top_k": cfg.num_experts_per_tok,
@@ -175,7 +185,10 @@ def bench_decode(args):
                    "layers_rotated": args.layers, "unique_experts_per_step": U,
                    "graph_steps": G, "kernels_per_step": 3, "graph_replay_matches_eager": graph_ok},
         "roofline": {"bound": "hbm", "kernel": dominant, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": int(traffic) if traffic else None,
+                     "traffic_source": "profiles/c2_decode_pmc.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)"
+                     if traffic else None,
                      "algorithmic_bytes_per_launch": int(kbytes[dominant]), "avg_launch_us": round(d_us, 3)},
         "layer": {"algorithmic_bytes": int(total_bytes), "achieved_GBs": round(layer_gbs, 1),
                   "hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4),
@@ -244,6 +257,30 @@ def bench_prefill(T=2048, reps=5):
             "kernel_us": {k: round(v, 1) for k, v in kern.items()}}
 
 
+def probe(args):
+    """Workload for the rocprofv3 --pmc runs: 48 eager decode steps over 16 rotated
+    layers, then the runtime's device-to-device copy of COPY_BYTES bytes (the
+    counter calibration)."""
+    import torch
+    import helexa_amd as hx
+    from helexa_amd import synth
+    cfg, fmts = synth.A3B, synth.FMT_Q8_0
+    blocks, _ = build_layers(cfg, fmts, 16, 1000)
+    xs = [synth.make_x(cfg, 1, 50 + i) for i in range(16)]
+    for i in range(48):
+        blocks[i % 16].forward(xs[i % 16])
+    torch.cuda.synchronize()
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"probe": "c2_decode", "steps": 48, "copy_bytes": COPY_BYTES}), flush=True)
+
+
+COPY_BYTES = 256 << 20
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -253,6 +290,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--probe", action="store_true", help="short workload for rocprofv3 --pmc runs")
+    ap.add_argument("--prefill-only", action="store_true", help="only the C3 prefill line (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -263,6 +302,12 @@ def main():
         print("bench.py needs an MI355X (cuda:0)", file=sys.stderr)
         sys.exit(2)
     from helexa_amd import synth
+    if args.probe:
+        probe(args)
+        return
+    if args.prefill_only:
+        print(json.dumps(bench_prefill()), flush=True)
+        return
     out, blocks, host0, xs = bench_decode(args)
     log(f"[bench] decode {out['value']} us/layer; kernels {out['layer']['kernel_us']}")
     if not args.no_cpu:

@@ -299,8 +299,9 @@ __global__ __launch_bounds__(256) void k_router_dec(RouterArgs r, ExpertArgs a, 
 // ----------------------------------------------------------------------------
 // K2: routed gate/up + SwiGLU. Every workgroup routes the T tokens from the
 // logits in LDS. The last grid row's workgroup 0 only publishes routing and
-// plan; workgroup (x, u < last row) computes rows of slot u's expert and pulls
-// a 1/gridDim.x share of that expert's down projection into the caches for K3.
+// plan; workgroup (x, u < last row) computes rows of slot u's expert. (Pulling
+// the expert's down projection into the caches here as well was measured to
+// cost more in this kernel than it saved in the next.)
 // ----------------------------------------------------------------------------
 template <int FMT, int LPR, int NR>
 __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a) {
@@ -308,7 +309,7 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
   __shared__ RouteSmem sm;
   const bool publisher = blockIdx.y == gridDim.y - 1;
   if (publisher && blockIdx.x > 0) return;
-  route_small_lds(r.logits, r.E1, r.E, r.k, r.norm, r.has_shared, r.T, sm);
+  route_small_lds(r.logits, r.E1, r.E, r.k, r.norm, publisher && r.has_shared, r.T, sm);
   if (publisher) {
     publish_route(r.d, r.topk_w, r.sgw, sm);
     return;
@@ -316,9 +317,6 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
   const int u = blockIdx.y;
   if (u >= sm.nroute) return;
   const int e = sm.slots[3 * u], start = sm.slots[3 * u + 1], count = sm.slots[3 * u + 2];
-  const int64_t per = (a.down.mat_bytes + gridDim.x - 1) / gridDim.x;
-  const int64_t lo = (int64_t)blockIdx.x * per, n = lo + per < a.down.mat_bytes ? per : a.down.mat_bytes - lo;
-  const Touch pf = n > 0 ? touch_lines(a.down.mat(e) + lo, n) : Touch{0u, 0u};
   const int wave = threadIdx.x >> 6;
   int tok[HX_DECODE_MAX_T], hrow[HX_DECODE_MAX_T];
   for (int j = 0; j < count; j++) {
@@ -328,7 +326,6 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
   const int row0 = (blockIdx.x * 4 + wave) * (RG * NR) + lane_id() / LPR;
   if (row0 - lane_id() / LPR < a.I)
     gate_up_rows<FMT, LPR, NR>(a, a.gate.mat(e), a.up.mat(e), a.I, row0, count, tok, hrow);
-  touch_sink(a, pf);
 }
 
 // ----------------------------------------------------------------------------

@@ -179,7 +179,8 @@ HX_DEV void route_token_core(const float* lg, int E, int k, bool norm, int& out_
 }
 
 template <int EPL>
-HX_DEV void route_token_lds_t(const float* lg, int E, int k, bool norm, bool has_shared, int t, RouteSmem& sm) {
+HX_DEV void route_token_lds_t(const float* lg, int E, int k, bool norm, bool want_sgw, int t, RouteSmem& sm) {
+  const float sg = want_sgw ? lg[E] : 0.0f;   // issued with the logits, used at the end
   int e;
   float w;
   route_token_core<EPL>(lg, E, k, norm, e, w);
@@ -188,56 +189,100 @@ HX_DEV void route_token_lds_t(const float* lg, int E, int k, bool norm, bool has
     sm.idx[t * k + lane] = e;
     sm.w[t * k + lane] = w;
   }
-  if (lane == 0) sm.sgw[t] = has_shared ? sigmoidf_(lg[E]) : 0.0f;
+  if (lane == 0) sm.sgw[t] = want_sgw ? sigmoidf_(sg) : 0.0f;
 }
 
-HX_DEV void route_token_lds(const float* lg, int E, int k, bool norm, bool has_shared, int t, RouteSmem& sm) {
-  if (E <= 64) route_token_lds_t<1>(lg, E, k, norm, has_shared, t, sm);
-  else if (E <= 128) route_token_lds_t<2>(lg, E, k, norm, has_shared, t, sm);
-  else if (E <= 256) route_token_lds_t<4>(lg, E, k, norm, has_shared, t, sm);
-  else if (E <= 512) route_token_lds_t<8>(lg, E, k, norm, has_shared, t, sm);
-  else route_token_lds_t<16>(lg, E, k, norm, has_shared, t, sm);
+// One token in wave 0 of the workgroup, dispatch included: the k experts of a
+// token are distinct, so expert-sorted position = rank of the expert id, every
+// entry starts its own slot, and slot = position.
+template <int EPL>
+HX_DEV void route_one_token(const float* lg, int E, int k, bool norm, bool want_sgw, RouteSmem& sm) {
+  const float sg = want_sgw ? lg[E] : 0.0f;
+  int e;
+  float w;
+  route_token_core<EPL>(lg, E, k, norm, e, w);
+  const int lane = lane_id();
+  int pos = 0;
+  for (int j = 0; j < k; j++) pos += __builtin_amdgcn_readlane(e, j) < e;
+  if (lane < k) {
+    sm.idx[lane] = e;
+    sm.w[lane] = w;
+    sm.pos[lane] = pos;
+    sm.perm[pos] = lane;
+    sm.first[lane] = 1;
+    sm.slots[3 * pos + 0] = e;
+    sm.slots[3 * pos + 1] = pos;
+    sm.slots[3 * pos + 2] = 1;
+  }
+  if (lane == 0) {
+    sm.sgw[0] = want_sgw ? sigmoidf_(sg) : 0.0f;
+    sm.nroute = k;
+  }
 }
 
-// full routing of T tokens from logits [T][E1]; ends with a barrier
-HX_DEV void route_small_lds(const float* logits, int E1, int E, int k, bool norm, bool has_shared, int T,
+HX_DEV void route_token_lds(const float* lg, int E, int k, bool norm, bool want_sgw, int t, RouteSmem& sm) {
+  if (E <= 64) route_token_lds_t<1>(lg, E, k, norm, want_sgw, t, sm);
+  else if (E <= 128) route_token_lds_t<2>(lg, E, k, norm, want_sgw, t, sm);
+  else if (E <= 256) route_token_lds_t<4>(lg, E, k, norm, want_sgw, t, sm);
+  else if (E <= 512) route_token_lds_t<8>(lg, E, k, norm, want_sgw, t, sm);
+  else route_token_lds_t<16>(lg, E, k, norm, want_sgw, t, sm);
+}
+
+HX_DEV void route_one_token_lds(const float* lg, int E, int k, bool norm, bool want_sgw, RouteSmem& sm) {
+  if (E <= 64) route_one_token<1>(lg, E, k, norm, want_sgw, sm);
+  else if (E <= 128) route_one_token<2>(lg, E, k, norm, want_sgw, sm);
+  else if (E <= 256) route_one_token<4>(lg, E, k, norm, want_sgw, sm);
+  else if (E <= 512) route_one_token<8>(lg, E, k, norm, want_sgw, sm);
+  else route_one_token<16>(lg, E, k, norm, want_sgw, sm);
+}
+
+// Full routing of T tokens from logits [T][E1] into RouteSmem; ends with a
+// barrier. The shared-expert gate sigmoid is computed only when want_sgw.
+HX_DEV void route_small_lds(const float* logits, int E1, int E, int k, bool norm, bool want_sgw, int T,
                             RouteSmem& sm) {
   const int tid = threadIdx.x, wave = tid >> 6;
   const int F = T * k;
+  if (T == 1) {
+    if (wave == 0) route_one_token_lds(logits, E, k, norm, want_sgw, sm);
+    __syncthreads();
+    return;
+  }
   if (tid == 0) sm.nroute = 0;
-  for (int t = wave; t < T; t += 4) route_token_lds(logits + (int64_t)t * E1, E, k, norm, has_shared, t, sm);
+  for (int t = wave; t < T; t += 4) route_token_lds(logits + (int64_t)t * E1, E, k, norm, want_sgw, t, sm);
   __syncthreads();
   if (F <= 64) {
-    // one wave: entry f in lane f, the other entries' experts via readlane
+    // one wave, entry f in lane f: its position is the number of entries with
+    // a smaller (expert, f) key; it opens a slot when no earlier entry has its
+    // expert; its slot is the number of slot-opening entries with smaller experts
     if (wave == 0) {
       const int lane = lane_id();
-      const int e = lane < F ? sm.idx[lane] : 0x7fffffff;
-      int less = 0, before = 0;
+      const int e = lane < F ? sm.idx[lane] : 0x7fff;   // experts < 1024
+      const int key = (e << 6) | lane;
+      int pos = 0, before = 0;
       for (int j = 0; j < F; j++) {
-        const int ej = __builtin_amdgcn_readlane(e, j);
-        less += ej < e;
-        before += (ej == e) & (j < lane);
+        const int kj = __builtin_amdgcn_readlane(key, j);
+        pos += kj < key;
+        before += (kj >> 6) == e && j < lane;
       }
       const bool first = lane < F && before == 0;
+      const unsigned long long fm = __ballot(first);
       int slot = 0, count = 0;
       for (int j = 0; j < F; j++) {
-        const int ej = __builtin_amdgcn_readlane(e, j);
-        const int fj = __builtin_amdgcn_readlane((int)first, j);
-        slot += fj & (ej < e);
+        const int ej = __builtin_amdgcn_readlane(key, j) >> 6;
+        slot += (int)((fm >> j) & 1ull) & (ej < e);
         count += ej == e;
       }
       if (lane < F) {
-        sm.pos[lane] = less + before;
-        sm.perm[less + before] = lane;
+        sm.pos[lane] = pos;
+        sm.perm[pos] = lane;
         sm.first[lane] = first;
       }
       if (first) {
         sm.slots[3 * slot + 0] = e;
-        sm.slots[3 * slot + 1] = less;
+        sm.slots[3 * slot + 1] = pos;
         sm.slots[3 * slot + 2] = count;
       }
-      const int nfirst = __popcll(__ballot(first));
-      if (lane == 0) sm.nroute = nfirst;
+      if (lane == 0) sm.nroute = __popcll(fm);
     }
     __syncthreads();
     return;
