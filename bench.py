@@ -210,7 +210,7 @@ def cpu_baseline(cfg, fmts, host0, x0, budget_s):
     while True:
         orc.forward(xn, nthreads=threads)
         n += 1
-        if time.perf_counter() - t0 > budget_s or n >= 200:
+        if time.perf_counter() - t0 > budget_s or n >= 20000:
             break
     dt = (time.perf_counter() - t0) / n
     return {"value": round(dt * 1e6, 1), "unit": "us/layer (C2 decode)", "cores": threads, "kind": "port",
@@ -287,7 +287,7 @@ def main():
     ap.add_argument("--steps", type=int, default=4096)
     ap.add_argument("--warmup", type=int, default=512)
     ap.add_argument("--layers", type=int, default=16)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--probe", action="store_true", help="short workload for rocprofv3 --pmc runs")

@@ -35,6 +35,29 @@
  *   - renormalisation: sequential sum in rank order, IEEE division.
  * Everything here is compiled with -ffp-contract=off so that no multiply-add is
  * fused unless fmaf is written explicitly.
+ *
+ * How each part is pinned (tests/test_oracle.py):
+ *   - f16 / bf16 conversions: exhaustive / numpy / torch comparisons.
+ *   - hxo_expf: error bound against libm in double, special values.
+ *   - GGUF dequantisation: hand-built known-answer blocks for every sub-block
+ *     of Q8_0, Q4_K, Q6_K (the public ggml layout), row sizes, divisibility.
+ *   - router / softmax / top-k / renorm: closed forms (zero weights), brute
+ *     force in double on small shapes, tie and no-renorm cases, and the
+ *     reference's own unit tests (moe.rs:223-303, 309-359) restated.
+ *   - dispatch: permutation invariants and brute-force stable sort.
+ *   - forward: uniform routing = mean of experts, TP partial-sum identity
+ *     (tp_qwen3_5.rs:2460-2496), quantised == forward on dequantised weights,
+ *     token independence, and an f32 golden from transformers'
+ *     Qwen3NextSparseMoeBlock on the C1 shape.
+ *   - rmsnorm: closed forms.
+ * Parity unpinned (no reference vector or buildable reference exists here):
+ *   - hxo_quantize's per-block scale search is the library's own rule; byte
+ *     parity with candle's GgmlType::from_float is unpinned (forward parity
+ *     never depends on it: both sides are fed the same GGUF bytes).
+ *   - candle's quantised-matmul arithmetic (QMatMul activation quantisation to
+ *     Q8_K / Q8_0 at m <= 64, the f16 path at m > 64) is not restated; the
+ *     forward here accumulates dequantised weights in double, and agreement
+ *     with candle is only to the tolerance the tests state.
  */
 #include <math.h>
 #include <stdint.h>
