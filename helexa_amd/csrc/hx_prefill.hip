@@ -175,31 +175,47 @@ struct PRaw<HX_Q6_K> {
 };
 
 // ---------------------------------------------------------------- A tile
-// 64 gathered f16 rows x 128 of K chunk kc; thread: row t/4, 32 elements
+// 64 gathered f16 rows x 128 of K chunk kc, as 1024 16-byte pieces: piece
+// q = thread + 256 i is row q / 16, piece q % 16. Sixteen consecutive lanes
+// cover one row (coalesced 256-byte reads) and any 8 consecutive lanes write
+// 8 different bank groups of LDS.
 struct ARaw {
   uint4 v[4];
   HX_DEV void load(const uint16_t* src, int64_t stride, const int* rowsrc, int rows, int kc) {
-    const int r = threadIdx.x >> 2, seg = threadIdx.x & 3;
-    if (r < rows) {
-      const uint4* s = (const uint4*)(src + (int64_t)rowsrc[r] * stride + kc * PKC + 32 * seg);
 #pragma unroll
-      for (int i = 0; i < 4; i++) v[i] = s[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; i++) v[i] = make_uint4(0u, 0u, 0u, 0u);
+    for (int i = 0; i < 4; i++) {
+      const int q = threadIdx.x + 256 * i, r = q >> 4, seg = q & 15;
+      v[i] = r < rows ? *(const uint4*)(src + (int64_t)rowsrc[r] * stride + kc * PKC + 8 * seg)
+                      : make_uint4(0u, 0u, 0u, 0u);
     }
   }
   HX_DEV void to_lds(uint16_t* As) const {
-    uint4* d = (uint4*)(As + (threadIdx.x >> 2) * PLD + 32 * (threadIdx.x & 3));
 #pragma unroll
-    for (int i = 0; i < 4; i++) d[i] = v[i];
+    for (int i = 0; i < 4; i++) {
+      const int q = threadIdx.x + 256 * i, r = q >> 4, seg = q & 15;
+      *(uint4*)(As + r * PLD + 8 * seg) = v[i];
+    }
   }
 };
+
+// XCD-aware work mapping. Workgroups are dealt to the 8 XCDs round-robin by
+// linear id (XCD = id % 8), each with its own L2. The launch grid is
+// (NX, tiles rounded up to 8); linear id L is mapped so that the NX workgroups
+// of one M tile (its N tiles) land on the same XCD: the gathered activation
+// rows of the tile are then fetched into one L2 and read from there by all
+// NX workgroups.
+HX_DEV void xcd_tile(int& nt, int& tile) {
+  const int NX = gridDim.x, L = blockIdx.y * NX + blockIdx.x;
+  const int group = L / (8 * NX), xcd = L & 7;
+  nt = (L >> 3) % NX;
+  tile = group * 8 + xcd;
+}
 
 HX_DEV f16x8_t frag(const uint16_t* base) { return __builtin_bit_cast(f16x8_t, *(const uint4*)base); }
 
 // ---------------------------------------------------------------- gate/up
-// grid (I / 64, tiles): 64 rows x 64 intermediate columns; wave w owns columns
+// grid (I / 64, tiles rounded up to 8), mapped by xcd_tile: 64 rows x 64
+// intermediate columns; wave w owns columns
 // 16w .. 16w+15 of gate and of up for all 64 rows. h = silu(gate) * up is
 // written as f16 in the swizzled order.
 template <int FMT>
@@ -207,11 +223,12 @@ __global__ __launch_bounds__(256) void k_gate_up_mfma(ExpertArgs a) {
   __shared__ uint16_t As[PM * PLD];
   __shared__ uint16_t Bs[128 * PLD];
   __shared__ int rowsrc[PM];
-  const int tile = blockIdx.y;
+  int nt, tile;
+  xcd_tile(nt, tile);
   if (tile >= a.counts[1]) return;
   const int e = a.tiles[4 * tile + 1], p0 = a.tiles[4 * tile + 2], rows = a.tiles[4 * tile + 3];
   const bool sh = e == a.E;
-  const int I = sh ? a.Is : a.I, n0 = blockIdx.x * 64;
+  const int I = sh ? a.Is : a.I, n0 = nt * 64;
   if (n0 >= I) return;
   const uint8_t* G = sh ? a.sgate.base : a.gate.mat(e);
   const uint8_t* U = sh ? a.sup.base : a.up.mat(e);
@@ -222,6 +239,8 @@ __global__ __launch_bounds__(256) void k_gate_up_mfma(ExpertArgs a) {
   }
   __syncthreads();
   const int lane = lane_id(), wave = threadIdx.x >> 6, l16 = lane & 15, kq = lane >> 4;
+  // B rows: thread t dequantises half t % 2 of row t / 2 (rows 0..63 gate,
+  // 64..127 up): the two threads of a row read adjacent bytes
   const int brow = threadIdx.x >> 1, bpt = threadIdx.x & 1;
   const uint8_t* Wm = brow < 64 ? G : U;
   const int wrow = n0 + (brow & 63);
@@ -268,7 +287,8 @@ __global__ __launch_bounds__(256) void k_gate_up_mfma(ExpertArgs a) {
 }
 
 // ---------------------------------------------------------------- down
-// grid (H / 128, tiles): 64 rows x 128 output columns; wave w owns columns
+// grid (H / 128, tiles rounded up to 8), mapped by xcd_tile: 64 rows x 128
+// output columns; wave w owns columns
 // 32w .. 32w+31. Rows are scaled by their routing weight (shared expert: the
 // sigmoid gate) and written to the per-assignment output rows.
 template <int FMT>
@@ -277,11 +297,12 @@ __global__ __launch_bounds__(256) void k_down_mfma(ExpertArgs a) {
   __shared__ uint16_t Bs[128 * PLD];
   __shared__ int rowsrc[PM];
   __shared__ float rw[PM];
-  const int tile = blockIdx.y;
+  int nt, tile;
+  xcd_tile(nt, tile);
   if (tile >= a.counts[1]) return;
   const int e = a.tiles[4 * tile + 1], p0 = a.tiles[4 * tile + 2], rows = a.tiles[4 * tile + 3];
   const bool sh = e == a.E;
-  const int K = sh ? a.Is : a.I, n0 = blockIdx.x * 128, nk = K / PKC;
+  const int K = sh ? a.Is : a.I, n0 = nt * 128, nk = K / PKC;
   const uint8_t* W = sh ? a.sdown.base : a.down.mat(e);
   if (threadIdx.x < PM) {
     const int p = p0 + threadIdx.x;
@@ -290,7 +311,7 @@ __global__ __launch_bounds__(256) void k_down_mfma(ExpertArgs a) {
   }
   __syncthreads();
   const int lane = lane_id(), wave = threadIdx.x >> 6, l16 = lane & 15, kq = lane >> 4;
-  const int brow = threadIdx.x >> 1, bpt = threadIdx.x & 1;
+  const int brow = threadIdx.x >> 1, bpt = threadIdx.x & 1;   // as in the gate/up kernel
   f32x4_t acc[2][4];
 #pragma unroll
   for (int j = 0; j < 2; j++)
@@ -366,7 +387,7 @@ bool prefill_mfma_ok(const ExpertArgs& a) {
 hipError_t launch_gate_up_mfma(const ExpertArgs& a, hipStream_t s) {
   const int64_t n8 = (int64_t)a.T * a.H / 8;
   hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, (const uint16_t*)a.x, n8, a.xh);
-  const dim3 grid(a.I / 64, a.max_tiles);
+  const dim3 grid(a.I / 64, (a.max_tiles + 7) / 8 * 8);
   switch (a.gate.fmt) {
     case HX_Q4_K: hipLaunchKernelGGL(k_gate_up_mfma<HX_Q4_K>, grid, dim3(256), 0, s, a); break;
     case HX_Q8_0: hipLaunchKernelGGL(k_gate_up_mfma<HX_Q8_0>, grid, dim3(256), 0, s, a); break;
@@ -377,7 +398,7 @@ hipError_t launch_gate_up_mfma(const ExpertArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_down_mfma(const ExpertArgs& a, hipStream_t s) {
-  const dim3 grid(a.H / 128, a.max_tiles);
+  const dim3 grid(a.H / 128, (a.max_tiles + 7) / 8 * 8);
   switch (a.down.fmt) {
     case HX_Q4_K: hipLaunchKernelGGL(k_down_mfma<HX_Q4_K>, grid, dim3(256), 0, s, a); break;
     case HX_Q8_0: hipLaunchKernelGGL(k_down_mfma<HX_Q8_0>, grid, dim3(256), 0, s, a); break;
