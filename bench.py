@@ -14,16 +14,21 @@ Method
     kernels per decode step on the capturing stream) and the graph is replayed;
     the timed region is bracketed by torch.cuda.synchronize() on both sides.
   * Kernel durations for the roofline come from HIP events the library records
-    around each of its kernels (hx_moe_timing_*), captured into a second graph
-    of the same steps and read after each replay.
+    around each of its kernels (hx_moe_timing_*) on the stream it launches on,
+    over the same steps launched eagerly behind a sleep kernel (so the GPU runs
+    them back to back).
   * Algorithmic bytes per step are computed from the actual routing (unique
     experts touched) and the GGUF sizes of what must be read once.
   * cpu_baseline: the CPU restatement of the reference's candle path (oracle/)
     on the host cores, on a bounded sample of the same workload.
   * `prefill` (secondary): C3, 2048 tokens of the same layer in Q4_K_M (gate/up
     Q4_K, down Q6_K), tokens/s with its MFMA and HBM fractions.
+  * `c5_skew` (secondary): C5, 4096 tokens with a Zipf(1.1) router bias
+    calibrated so the top 8 experts take ~40% of the assignments.
+  * `c4_stack` (secondary): C4, the 48-layer Q4_K_M stack with RMSNorm and
+    residual (attention skipped), decode at B = 1, 4, 8, per token.
 
-    python bench.py [--steps K] [--warmup W] [--layers L] [--no-cpu] [--no-prefill]
+    python bench.py [--steps K] [--warmup W] [--layers L] [--no-cpu] [--no-prefill] [--no-c4] [--no-c5]
 """
 from __future__ import annotations
 
@@ -257,6 +262,140 @@ def bench_prefill(T=2048, reps=5):
             "kernel_us": {k: round(v, 1) for k, v in kern.items()}}
 
 
+def bench_c4(n_layers=48, batches=(1, 4, 8), reps=20):
+    """C4: 48-layer stack of the 80B-A3B MoE block in Q4_K_M with residual adds and
+    attention skipped: per layer x <- x + moe(rmsnorm(x)) (decoder.rs:129-132), the
+    RMSNorm weight stored as 1.0 with the reference's (1 + w) scaling
+    (rmsnorm.rs:76-77), eps 1e-6. Each batch size's 48 layers are captured in one
+    HIP graph; time per token = step time / B."""
+    import torch
+    import helexa_amd as hx
+    from helexa_amd import synth
+    cfg, fmts = synth.A3B, synth.FMT_Q4_K_M
+    t0 = time.time()
+    blocks, _ = build_layers(cfg, fmts, n_layers, 7000)
+    log(f"[bench] C4: {n_layers} Q4_K_M layers ready in {time.time() - t0:.1f}s")
+    norm_w = torch.ones(cfg.hidden_size, dtype=torch.float32, device="cuda")
+    H, I, Is = cfg.hidden_size, cfg.moe_intermediate_size, cfg.shared_expert_intermediate_size
+    per_expert = gguf_bytes(fmts["gate"], I, H) * 2 + gguf_bytes(fmts["down"], H, I)
+    shared = gguf_bytes(fmts["sgate"], Is, H) * 2 + gguf_bytes(fmts["sdown"], H, Is)
+    router = (cfg.num_experts + 1) * H * 2
+    out = {"workload": f"C4: {n_layers}-layer Q4_K_M MoE stack decode (residual + RMSNorm, attention skipped), bf16",
+           "layers": n_layers, "batches": {}}
+    for B in batches:
+        x0 = synth.make_x(cfg, B, 900 + B)
+        ws = torch.empty(max(b.workspace_size(B) for b in blocks[:1]), dtype=torch.uint8, device="cuda")
+        # algorithmic bytes of one step: the unique experts each layer touches on
+        # this input (eager pass, layer by layer)
+        x = x0.clone()
+        step_bytes_ = 0
+        for b in blocks:
+            U = int(torch.unique(b.route(b_rms(x, norm_w))["topk_idx"]).numel())
+            step_bytes_ += U * per_expert + shared + router + 2 * B * H * 2
+            b.decoder_mlp_(x, norm_w, 1e-6, workspace=ws)
+        eager = x.clone()
+        xg = x0.clone()
+        g = torch.cuda.CUDAGraph()
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            with torch.cuda.graph(g, stream=st):
+                for b in blocks:
+                    b.decoder_mlp_(xg, norm_w, 1e-6, workspace=ws, stream=st)
+        torch.cuda.current_stream().wait_stream(st)
+        xg.copy_(x0)
+        g.replay()
+        torch.cuda.synchronize()
+        graph_ok = bool(torch.equal(xg, eager))
+        for _ in range(3):
+            g.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            g.replay()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / reps
+        out["batches"][str(B)] = {"us_per_step": round(dt * 1e6, 1), "us_per_token": round(dt * 1e6 / B, 1),
+                                  "us_per_layer": round(dt * 1e6 / n_layers, 2),
+                                  "algorithmic_bytes_per_step": int(step_bytes_),
+                                  "hbm_frac": round(step_bytes_ / dt / (HBM_PEAK_GBS * 1e9), 4),
+                                  "graph_matches_eager": graph_ok}
+        log(f"[bench] C4 B={B}: {out['batches'][str(B)]}")
+    for b in blocks:
+        b.close()
+    return out
+
+
+def b_rms(x, w, eps=1e-6):
+    """the stack's RMSNorm on the device (f32 math, bf16 out), (1 + w) scaling --
+    only used to find which experts a layer routes to for the byte count"""
+    import torch
+    xf = x.float()
+    y = xf * torch.rsqrt((xf * xf).mean(-1, keepdim=True) + eps) * (1.0 + w)
+    return y.to(x.dtype)
+
+
+def bench_c5(T=4096, target_share=0.40, reps=5):
+    """C5: 4096-token prefill of the Q4_K_M layer with a seeded Zipf(1.1) router
+    bias (router_bias[e] = alpha ln p_{pi(e)}), alpha calibrated on this layer so
+    the top 8 experts take about 40% of the assignments."""
+    import numpy as np
+    import torch
+    import helexa_amd as hx
+    from helexa_amd import synth
+    cfg, fmts = synth.A3B, synth.FMT_Q4_K_M
+    w = synth.make_weights(cfg, fmts, 4243)
+    blk = hx.Qwen3_5MoeBlock.load(cfg, w, act_dtype=hx.BF16)
+    del w
+    x = synth.make_x(cfg, T, 78)
+    E, k = cfg.num_experts, cfg.num_experts_per_tok
+    base = synth.zipf_bias(E, 1.1, 1.0, 11)
+    top8 = torch.argsort(base, descending=True)[:8]
+
+    def share(alpha):
+        idx = blk.route(x, router_bias=base * alpha)["topk_idx"]
+        return float(torch.isin(idx, top8).float().mean())
+
+    lo, hi = 0.0, 2.0
+    for _ in range(14):
+        mid = 0.5 * (lo + hi)
+        if share(mid) < target_share:
+            lo = mid
+        else:
+            hi = mid
+    alpha = 0.5 * (lo + hi)
+    bias = base * alpha
+    achieved = share(alpha)
+    r = blk.route(x, router_bias=bias)
+    counts = np.diff(r["offsets"].cpu().numpy())
+    U = int((counts > 0).sum())
+    ws = torch.empty(blk.workspace_size(T), dtype=torch.uint8, device="cuda")
+    y = torch.empty_like(x)
+    for _ in range(2):
+        blk.forward(x, router_bias=bias, workspace=ws, out=y)
+    torch.cuda.synchronize()
+    blk.timing_begin(reps)
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        blk.forward(x, router_bias=bias, workspace=ws, out=y)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / reps
+    kern = {kk: v[0] / v[1] * 1e3 for kk, v in blk.timing_end().items() if v[1]}
+    H, I, Is = cfg.hidden_size, cfg.moe_intermediate_size, cfg.shared_expert_intermediate_size
+    flops = 2 * T * k * 3 * H * I + 2 * T * 3 * H * Is + 2 * T * H * E
+    nbytes = (U * (gguf_bytes(fmts["gate"], I, H) * 2 + gguf_bytes(fmts["down"], H, I))
+              + gguf_bytes(fmts["sgate"], Is, H) * 2 + gguf_bytes(fmts["sdown"], H, Is)
+              + (E + 1) * H * 2 + 2 * T * H * 2)
+    blk.close()
+    return {"workload": f"C5: {T}-token prefill, Q4_K_M, Zipf(1.1) router bias", "tokens": T,
+            "alpha": round(alpha, 4), "top8_share": round(achieved, 4), "max_expert_rows": int(counts.max()),
+            "unique_experts": U, "us": round(dt * 1e6, 1), "tok_per_s": round(T / dt, 1),
+            "mfma_frac": round(flops / dt / (MFMA_BF16_PEAK_TFS * 1e12), 4),
+            "hbm_frac": round(nbytes / dt / (HBM_PEAK_GBS * 1e9), 4),
+            "algorithmic_flops": flops, "algorithmic_bytes": nbytes,
+            "kernel_us": {kk: round(v, 1) for kk, v in kern.items()}}
+
+
 def probe(args):
     """Workload for the rocprofv3 --pmc runs: 48 eager decode steps over 16 rotated
     layers, then the runtime's device-to-device copy of COPY_BYTES bytes (the
@@ -292,6 +431,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--probe", action="store_true", help="short workload for rocprofv3 --pmc runs")
     ap.add_argument("--prefill-only", action="store_true", help="only the C3 prefill line (for profiling)")
+    ap.add_argument("--no-c4", action="store_true", help="skip the 48-layer stack line")
+    ap.add_argument("--no-c5", action="store_true", help="skip the skewed 4096-token prefill line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -322,6 +463,14 @@ def main():
     if not args.no_prefill:
         log("[bench] prefill")
         out["prefill"] = bench_prefill()
+        torch.cuda.empty_cache()
+    if not args.no_c5:
+        log("[bench] C5 skewed prefill")
+        out["c5_skew"] = bench_c5()
+        torch.cuda.empty_cache()
+    if not args.no_c4:
+        log("[bench] C4 stack")
+        out["c4_stack"] = bench_c4()
     print(json.dumps(out), flush=True)
 
 

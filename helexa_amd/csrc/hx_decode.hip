@@ -209,7 +209,7 @@ struct DChunk<HX_Q6_K> {
 // the decode plan, pulled into LDS by the whole workgroup in one pass
 HX_DEV void load_plan(const ExpertArgs& a, int32_t* splan) {
   const int np = plan_ints(a.max_slots, a.F, a.T);
-  for (int i = threadIdx.x; i < np; i += 256) splan[i] = a.plan[i];
+  for (int i = threadIdx.x; i < np; i += blockDim.x) splan[i] = a.plan[i];
   __syncthreads();
 }
 
@@ -329,12 +329,36 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
 }
 
 // ----------------------------------------------------------------------------
+// K2 for T > 1: the routing and plan were published by one workgroup
+// (k_route_small); grid row u computes rows of slot u's expert from the plan.
+// The shared expert's slot (the last) was computed by the router kernel.
+// ----------------------------------------------------------------------------
+template <int FMT, int LPR, int NR>
+__global__ __launch_bounds__(256) void k_gate_up_plan(ExpertArgs a) {
+  constexpr int RG = 64 / LPR;
+  const int u = blockIdx.y;
+  const int nslots = a.plan[0];
+  const int e = a.plan[4 + 4 * u], start = a.plan[4 + 4 * u + 1], count = a.plan[4 + 4 * u + 2];
+  if (u >= nslots || e >= a.E) return;
+  const int tok0 = 4 + 4 * a.max_slots;
+  int tok[HX_DECODE_MAX_T], hrow[HX_DECODE_MAX_T];
+  for (int j = 0; j < count; j++) {
+    hrow[j] = start + j;
+    tok[j] = a.plan[tok0 + start + j];
+  }
+  const int wave = threadIdx.x >> 6;
+  const int row0 = (blockIdx.x * 4 + wave) * (RG * NR) + lane_id() / LPR;
+  if (row0 - lane_id() / LPR < a.I)
+    gate_up_rows<FMT, LPR, NR>(a, a.gate.mat(e), a.up.mat(e), a.I, row0, count, tok, hrow);
+}
+
+// ----------------------------------------------------------------------------
 // down + combine: block = RG output rows; the 4 waves split the slots; per-slot
 // contributions w * (row . h) go to LDS and are summed in slot order (experts
 // ascending, then the shared expert).
 // ----------------------------------------------------------------------------
-template <int FMT, int LPR, int SPW>
-__global__ __launch_bounds__(256) void k_down_dec(ExpertArgs a) {
+template <int FMT, int LPR, int SPW, int NW>
+__global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
   using D = DChunk<FMT>;
   constexpr int RG = 64 / LPR;
   extern __shared__ int32_t splan[];
@@ -344,9 +368,9 @@ __global__ __launch_bounds__(256) void k_down_dec(ExpertArgs a) {
   const int tok0 = 4 + 4 * a.max_slots, w0 = tok0 + a.F + a.T;
   const int lane = lane_id(), wave = threadIdx.x >> 6, rg = lane / LPR, c = lane % LPR;
   const int n0 = blockIdx.x * RG, row = n0 + rg;
-  for (int i = threadIdx.x; i < nslots * T * RG; i += 256) contrib[i] = 0.f;
+  for (int i = threadIdx.x; i < nslots * T * RG; i += 64 * NW) contrib[i] = 0.f;
   __syncthreads();
-  for (int ub = wave; ub < nslots; ub += 4 * SPW) {
+  for (int ub = wave; ub < nslots; ub += NW * SPW) {
     // every load of the batch first: the SPW slots' weight chunks and the
     // activations of each slot's first token
     typename D::Raw raw[SPW];
@@ -354,7 +378,7 @@ __global__ __launch_bounds__(256) void k_down_dec(ExpertArgs a) {
     float xs0[SPW][D::NS];
 #pragma unroll
     for (int s = 0; s < SPW; s++) {
-      const int u = ub + 4 * s;
+      const int u = ub + NW * s;
       if (u < nslots) {
         const int e = splan[4 + 4 * u], start = splan[4 + 4 * u + 1];
         const bool sh = e == a.E;
@@ -367,7 +391,7 @@ __global__ __launch_bounds__(256) void k_down_dec(ExpertArgs a) {
     }
 #pragma unroll
     for (int s = 0; s < SPW; s++) {
-      const int u = ub + 4 * s;
+      const int u = ub + NW * s;
       if (u >= nslots) break;
       const int e = splan[4 + 4 * u], start = splan[4 + 4 * u + 1], count = splan[4 + 4 * u + 2];
       const bool sh = e == a.E;
@@ -392,7 +416,7 @@ __global__ __launch_bounds__(256) void k_down_dec(ExpertArgs a) {
     }
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < T * RG; i += 256) {
+  for (int i = threadIdx.x; i < T * RG; i += 64 * NW) {
     const int t = i / RG, r = i % RG;
     if (n0 + r >= a.H) continue;
     float y = 0.f;
@@ -449,6 +473,21 @@ static hipError_t gate_up_dec_fmt(const RouterArgs& r, const ExpertArgs& a, hipS
 }
 
 template <int FMT>
+static hipError_t gate_up_plan_fmt(const ExpertArgs& a, hipStream_t s) {
+  const int nch = a.H / 32;
+  constexpr int NR = 2;
+#define GUP(LPR)                                                                          \
+  {                                                                                       \
+    constexpr int RG = 64 / LPR;                                                          \
+    dim3 grid((a.I + 4 * RG * NR - 1) / (4 * RG * NR), a.max_slots);                      \
+    hipLaunchKernelGGL((k_gate_up_plan<FMT, LPR, NR>), grid, dim3(256), 0, s, a);         \
+  }
+  if (nch == 64) GUP(64) else if (nch == 32) GUP(32) else GUP(16)
+#undef GUP
+  return hipGetLastError();
+}
+
+template <int FMT>
 static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
   const int nch = (a.I > a.Is ? a.I : a.Is) / 32;
 #define DD(LPR)                                                                                   \
@@ -456,7 +495,7 @@ static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
     constexpr int RG = 64 / LPR;                                                                  \
     size_t lds = sizeof(int32_t) * plan_ints(a.max_slots, a.F, a.T) +                              \
                  (size_t)a.max_slots * a.T * RG * sizeof(float);                                  \
-    hipLaunchKernelGGL((k_down_dec<FMT, LPR, 3>), dim3((a.H + RG - 1) / RG), dim3(256), lds, s, a); \
+    hipLaunchKernelGGL((k_down_dec<FMT, LPR, 3, 4>), dim3((a.H + RG - 1) / RG), dim3(256), lds, s, a); \
   }
   if (nch == 64) DD(64) else if (nch == 32) DD(32) else DD(16)
 #undef DD
@@ -477,6 +516,15 @@ hipError_t launch_gate_up_dec(const RouterArgs& r, const ExpertArgs& a, hipStrea
     case HX_Q8_0: return gate_up_dec_fmt<HX_Q8_0>(r, a, s);
     case HX_Q4_K: return gate_up_dec_fmt<HX_Q4_K>(r, a, s);
     case HX_Q6_K: return gate_up_dec_fmt<HX_Q6_K>(r, a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_gate_up_plan(const ExpertArgs& a, hipStream_t s) {
+  switch (a.gate.fmt) {
+    case HX_Q8_0: return gate_up_plan_fmt<HX_Q8_0>(a, s);
+    case HX_Q4_K: return gate_up_plan_fmt<HX_Q4_K>(a, s);
+    case HX_Q6_K: return gate_up_plan_fmt<HX_Q6_K>(a, s);
     default: return hipErrorInvalidValue;
   }
 }

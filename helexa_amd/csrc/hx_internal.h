@@ -101,7 +101,8 @@ void launch_dispatch(const DispatchArgs& d, hipStream_t s);
 // decode (T <= HX_DECODE_MAX_T)
 bool decode_fast_ok(const ExpertArgs& a);   // bf16 activations, GGUF weights: f16 dot2 kernels
 hipError_t launch_router_dec(const RouterArgs& r, const ExpertArgs& a, bool rbf, hipStream_t s);  // router + shared gate/up
-hipError_t launch_gate_up_dec(const RouterArgs& r, const ExpertArgs& a, hipStream_t s);
+hipError_t launch_gate_up_dec(const RouterArgs& r, const ExpertArgs& a, hipStream_t s);   // T == 1: routes in its prologue
+hipError_t launch_gate_up_plan(const ExpertArgs& a, hipStream_t s);   // T > 1: reads the published plan
 hipError_t launch_down_dec(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_gate_up_gemv(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_down_gemv_combine(const ExpertArgs& a, hipStream_t s);

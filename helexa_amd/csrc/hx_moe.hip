@@ -430,14 +430,24 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
   make_plan(m, x, T, y, (uint8_t*)ws, L, bias, p);
   const bool decode = T <= HX_DECODE_MAX_T;
   if (decode && decode_fast_ok(p.ea)) {
-    // three kernels: router + shared gate/up, routed gate/up (routing in its
-    // prologue), down + combine
+    // router + shared gate/up; routed gate/up (one token: routing in its
+    // prologue; more: routed once by one workgroup, then the plan); down + combine
     tm_mark(m, SLOT_ROUTER, 0, s);
     HX_HIP(launch_router_dec(p.ra, p.ea, m->rdt == HX_BF16, s));
     tm_mark(m, SLOT_ROUTER, 1, s);
-    tm_mark(m, SLOT_GATE_UP, 0, s);
-    HX_HIP(launch_gate_up_dec(p.ra, p.ea, s));
-    tm_mark(m, SLOT_GATE_UP, 1, s);
+    if (T == 1) {
+      tm_mark(m, SLOT_GATE_UP, 0, s);
+      HX_HIP(launch_gate_up_dec(p.ra, p.ea, s));
+      tm_mark(m, SLOT_GATE_UP, 1, s);
+    } else {
+      tm_mark(m, SLOT_ROUTE_TOKENS, 0, s);
+      launch_route_small(p.ra, s);
+      HX_HIP(hipGetLastError());
+      tm_mark(m, SLOT_ROUTE_TOKENS, 1, s);
+      tm_mark(m, SLOT_GATE_UP, 0, s);
+      HX_HIP(launch_gate_up_plan(p.ea, s));
+      tm_mark(m, SLOT_GATE_UP, 1, s);
+    }
     tm_mark(m, SLOT_DOWN, 0, s);
     HX_HIP(launch_down_dec(p.ea, s));
     tm_mark(m, SLOT_DOWN, 1, s);

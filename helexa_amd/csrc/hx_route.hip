@@ -182,8 +182,9 @@ __global__ __launch_bounds__(256) void k_router(RouterArgs a) {
   router_rows<XBF, RBF, TT, TE>(a, (blockIdx.x * 4 + wave) * TE, blockIdx.y * TT);
 }
 
-// routing of a few tokens in one workgroup, published to global memory
-__global__ __launch_bounds__(256) void k_route_small(RouterArgs a) {
+// routing of a few tokens in one workgroup (256 or 512 threads: one wave per
+// token up to 8), published to global memory
+__global__ __launch_bounds__(512) void k_route_small(RouterArgs a) {
   __shared__ RouteSmem sm;
   route_small_lds(a.logits, a.E1, a.E, a.k, a.norm, a.has_shared, a.T, sm);
   publish_route(a.d, a.topk_w, a.sgw, sm);
@@ -212,7 +213,7 @@ void launch_router(const RouterArgs& a, bool xbf, bool rbf, hipStream_t s) {
 }
 
 void launch_route_small(const RouterArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_route_small, dim3(1), dim3(256), 0, s, a);
+  hipLaunchKernelGGL(k_route_small, dim3(1), dim3(a.T > 4 ? 512 : 256), 0, s, a);
 }
 
 void launch_route_tokens(const RouterArgs& a, hipStream_t s) {

@@ -247,8 +247,9 @@ HX_DEV void route_small_lds(const float* logits, int E1, int E, int k, bool norm
     __syncthreads();
     return;
   }
+  const int nw = blockDim.x >> 6, nt = blockDim.x;
   if (tid == 0) sm.nroute = 0;
-  for (int t = wave; t < T; t += 4) route_token_lds(logits + (int64_t)t * E1, E, k, norm, want_sgw, t, sm);
+  for (int t = wave; t < T; t += nw) route_token_lds(logits + (int64_t)t * E1, E, k, norm, want_sgw, t, sm);
   __syncthreads();
   if (F <= 64) {
     // one wave, entry f in lane f: its position is the number of entries with
@@ -287,32 +288,70 @@ HX_DEV void route_small_lds(const float* logits, int E1, int E, int k, bool norm
     __syncthreads();
     return;
   }
-  // stable sort by expert: pos(f) = #{e_j < e_f} + #{j < f, e_j == e_f}
-  for (int f = tid; f < F; f += 256) {
-    const int e = sm.idx[f];
-    int less = 0, before = 0;
-    for (int j = 0; j < F; j++) {
-      const int ej = sm.idx[j];
-      less += ej < e;
-      before += (ej == e) & (j < f);
+  // stable sort by expert, one entry per thread: key = (expert, f), position =
+  // number of smaller keys; an entry opens a slot when no earlier entry has its
+  // expert; its slot is the number of distinct experts below it. Inner loops
+  // unrolled by 8 so the LDS reads of a thread are in flight together.
+  // (callers launch >= 256 threads, so a thread holds at most RPT entries)
+  constexpr int RPT = (HX_SMALL_F + 255) / 256;
+  for (int f = tid; f < F; f += nt) sm.perm[f] = (sm.idx[f] << 16) | f;   // keys (perm reused)
+  __syncthreads();
+  int my_pos[RPT], my_cnt[RPT];
+  bool my_first[RPT];
+#pragma unroll
+  for (int r = 0; r < RPT; r++) {
+    const int f = tid + r * nt;
+    my_pos[r] = my_cnt[r] = 0;
+    my_first[r] = false;
+    if (f >= F) continue;
+    const int key = sm.perm[f], e = key >> 16;
+    int pos = 0, cnt = 0, before = 0;
+    int j = 0;
+    for (; j + 8 <= F; j += 8) {
+      int kj[8];
+#pragma unroll
+      for (int q = 0; q < 8; q++) kj[q] = sm.perm[j + q];
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        pos += kj[q] < key;
+        const bool same = (kj[q] >> 16) == e;
+        cnt += same;
+        before += same && (j + q) < f;
+      }
     }
-    sm.pos[f] = less + before;
-    sm.perm[less + before] = f;
-    sm.first[f] = before == 0;
+    for (; j < F; j++) {
+      const int kj = sm.perm[j];
+      pos += kj < key;
+      const bool same = (kj >> 16) == e;
+      cnt += same;
+      before += same && j < f;
+    }
+    my_pos[r] = pos;
+    my_cnt[r] = cnt;
+    my_first[r] = before == 0;
   }
   __syncthreads();
-  for (int f = tid; f < F; f += 256) {
-    if (!sm.first[f]) continue;
-    const int e = sm.idx[f];
-    int slot = 0, count = 0;
-    for (int j = 0; j < F; j++) {
-      const int ej = sm.idx[j];
-      slot += sm.first[j] & (ej < e);
-      count += ej == e;
+#pragma unroll
+  for (int r = 0; r < RPT; r++) {
+    const int f = tid + r * nt;
+    if (f < F) {
+      sm.pos[f] = my_pos[r];
+      sm.first[f] = my_first[r];
     }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < RPT; r++) {
+    const int f = tid + r * nt;
+    if (f >= F) continue;
+    sm.perm[my_pos[r]] = f;
+    if (!my_first[r]) continue;
+    const int e = sm.idx[f];
+    int slot = 0;
+    for (int j = 0; j < F; j++) slot += sm.first[j] & (sm.idx[j] < e);
     sm.slots[3 * slot + 0] = e;
-    sm.slots[3 * slot + 1] = sm.pos[f];
-    sm.slots[3 * slot + 2] = count;
+    sm.slots[3 * slot + 1] = my_pos[r];
+    sm.slots[3 * slot + 2] = my_cnt[r];
     atomicAdd(&sm.nroute, 1);
   }
   __syncthreads();
@@ -320,10 +359,10 @@ HX_DEV void route_small_lds(const float* logits, int E1, int E, int k, bool norm
 
 // write the routing (and the decode plan) of RouteSmem to global memory
 HX_DEV void publish_route(const DispatchArgs& d, float* topk_w, float* sgw, const RouteSmem& sm) {
-  const int tid = threadIdx.x, F = d.F, T = d.T, E = d.E;
+  const int tid = threadIdx.x, nt = blockDim.x, F = d.F, T = d.T, E = d.E;
   const int ns = sm.nroute + (d.has_shared ? 1 : 0);
   const int tok0 = 4 + 4 * d.max_slots, w0 = tok0 + F + T;
-  for (int f = tid; f < F; f += 256) {
+  for (int f = tid; f < F; f += nt) {
     const int p = sm.pos[f];
     d.topk_idx[f] = sm.idx[f];
     topk_w[f] = sm.w[f];
@@ -332,22 +371,28 @@ HX_DEV void publish_route(const DispatchArgs& d, float* topk_w, float* sgw, cons
     d.plan[tok0 + p] = f / d.k;
     d.plan[w0 + p] = __float_as_int(sm.w[f]);
   }
-  for (int t = tid; t < T; t += 256) {
+  for (int t = tid; t < T; t += nt) {
     sgw[t] = sm.sgw[t];
     d.plan[tok0 + F + t] = t;
     d.plan[w0 + F + t] = __float_as_int(sm.sgw[t]);
   }
-  for (int u = tid; u < sm.nroute; u += 256) {
+  for (int u = tid; u < sm.nroute; u += nt) {
     for (int q = 0; q < 3; q++) {
       d.slots[3 * u + q] = sm.slots[3 * u + q];
       d.plan[4 + 4 * u + q] = sm.slots[3 * u + q];
     }
   }
-  // offsets[e] = number of entries routed to experts below e
-  for (int e = tid; e <= E; e += 256) {
-    int less = 0;
-    for (int j = 0; j < F; j++) less += sm.idx[j] < e;
-    d.offsets[e] = less;
+  // offsets[e] = number of entries routed to experts below e = start of the
+  // first slot whose expert is >= e (F if none): binary search of the slots,
+  // which are in ascending expert order
+  for (int e = tid; e <= E; e += nt) {
+    int lo = 0, hi = sm.nroute;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (sm.slots[3 * mid] < e) lo = mid + 1;
+      else hi = mid;
+    }
+    d.offsets[e] = lo < sm.nroute ? sm.slots[3 * lo + 1] : F;
   }
   if (tid == 0) {
     if (d.has_shared) {

@@ -286,3 +286,51 @@ def test_forward_skewed_routing_prefill(c2):
     sample = np.array([3, 100, 350, 699])
     ref = c2.oracle.forward(x_np(x)[sample], bias=bias.cpu().numpy())
     assert rel_err(y[sample], ref) <= TOL_BF16
+
+
+# ------------------------------------------------------------------ C4 / C5 shapes
+def test_c4_stack_layers_q4_k_m():
+    """Two Q4_K_M layers of the C4 stack (x <- x + moe(rmsnorm(x)), RMSNorm weight
+    stored as 1.0 with the (1 + w) scaling, attention skipped) at B = 1, 4, 8: each
+    layer's output against the oracle applied to that layer's bf16 input."""
+    _, synth = _hx()
+    layers = [Case(synth.A3B, synth.FMT_Q4_K_M, 40 + i, O.BF16) for i in range(2)]
+    w = torch.ones(synth.A3B.hidden_size, device="cuda")
+    wn = w.cpu().numpy()
+    for B in (1, 4, 8):
+        x = layers[0].x(B, seed=20 + B)
+        for c in layers:
+            xin = x_np(x)
+            xn = O.f32_to_bf16_bits(O.rmsnorm(xin, wn, 1e-6, O.BF16))
+            moe = O.bf16_bits_to_f32(O.f32_to_bf16_bits(c.oracle.forward(xn)))
+            ref = O.bf16_bits_to_f32(xin) + moe
+            print(f"[c4] B={B} layer seed={c.seed}", flush=True)
+            x = c.block.decoder_mlp_(x, w, 1e-6)
+            assert rel_err(x.float().cpu().numpy(), ref) <= TOL_BF16
+
+
+def test_c5_skewed_prefill_4096():
+    """C5 shape: 4096 tokens, Q4_K_M, Zipf(1.1) router bias scaled so the top 8
+    experts take roughly 40% of the assignments. Routing bit-exact for every
+    token, outputs on sampled tokens."""
+    _, synth = _hx()
+    c = Case(synth.A3B, synth.FMT_Q4_K_M, 13, O.BF16)
+    T = 4096
+    base = synth.zipf_bias(c.cfg.num_experts, 1.1, 1.0, 11)
+    bias = base * 0.58
+    x = c.x(T, seed=12)
+    r = c.block.route(x, router_bias=bias)
+    _, _, ix, wt = c.oracle.route(x_np(x), bias=bias.cpu().numpy())
+    got_ix = r["topk_idx"].cpu().numpy()
+    assert np.array_equal(got_ix, ix)
+    assert np.array_equal(r["topk_w"].cpu().numpy().view(np.int32), wt.view(np.int32))
+    top8 = torch.argsort(base, descending=True)[:8].cpu().numpy()
+    share = np.isin(got_ix, top8).mean()
+    assert 0.3 < share < 0.5
+    perm, offsets, inv = O.dispatch(ix, c.cfg.num_experts)
+    assert np.array_equal(r["perm"].cpu().numpy(), perm)
+    assert np.array_equal(r["offsets"].cpu().numpy(), offsets)
+    y = c.block.forward(x, router_bias=bias).float().cpu().numpy()
+    sample = np.linspace(0, T - 1, 10).astype(int)
+    ref = c.oracle.forward(x_np(x)[sample], bias=bias.cpu().numpy())
+    assert rel_err(y[sample], ref) <= TOL_BF16
