@@ -272,51 +272,62 @@ __global__ __launch_bounds__(256) void k_down_rows(ExpertArgs a) {
 // ----------------------------------------------------------------------------
 // combine: y[t] = sum of the token's k weighted expert rows in ascending expert
 // order (= ascending permuted position), then the shared expert's row.
-// One thread per (token, 8 consecutive outputs).
+// Grid (T, ceil(H / 2048)): a block serves one token and up to 2048 outputs,
+// 8 per thread. Wave 0 sorts the token's k positions once (rank of each among
+// the k, into LDS); every thread then issues all k + 1 row loads together.
 // ----------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_combine(ExpertArgs a) {
-  const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int per = a.H / 8;
-  if (gid >= (int64_t)a.T * per) return;
-  const int t = (int)(gid / per), n0 = (int)(gid % per) * 8;
-  int pos[HX_MAX_TOPK];
-  for (int j = 0; j < a.k; j++) {
-    int p = a.inv[(int64_t)t * a.k + j], q = j - 1;
-    while (q >= 0 && pos[q] > p) {
-      pos[q + 1] = pos[q];
-      q--;
-    }
-    pos[q + 1] = p;
+  __shared__ int spos[HX_MAX_TOPK + 1];
+  const int t = blockIdx.x, k = a.k;
+  if (threadIdx.x < 64) {
+    const int lane = threadIdx.x;
+    const int p = lane < k ? a.inv[(int64_t)t * k + lane] : 0x7fffffff;
+    int rank = 0;
+    for (int j = 0; j < k; j++) rank += __builtin_amdgcn_readlane(p, j) < p;
+    if (lane < k) spos[rank] = p;
+    if (lane == 0) spos[k] = a.F + t;   // the shared expert's row (used when Is > 0)
   }
+  __syncthreads();
+  const int n0 = (blockIdx.y * 256 + threadIdx.x) * 8;
+  if (n0 >= a.H) return;
+  const int nrows = k + (a.Is > 0 ? 1 : 0);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  const int nrows = a.k + (a.Is > 0 ? 1 : 0);
-  for (int j = 0; j < nrows; j++) {
-    const int r = j < a.k ? pos[j] : a.F + t;
-    if (a.xbf) {
-      uint4 q = *(const uint4*)((const uint16_t*)a.obuf + (int64_t)r * a.H + n0);
-      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  if (a.xbf) {
+    // rows loaded B at a time without branches: indices past the last row are
+    // clamped to it and their values masked to +0 (adding +0 changes nothing)
+    constexpr int B = 12;
+    for (int j0 = 0; j0 < nrows; j0 += B) {
+      uint4 q[B];
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        acc[2 * i] += __uint_as_float(w[i] << 16);
-        acc[2 * i + 1] += __uint_as_float(w[i] & 0xffff0000u);
+      for (int j = 0; j < B; j++) {
+        const int r = spos[min(j0 + j, nrows - 1)];
+        q[j] = *(const uint4*)((const uint16_t*)a.obuf + (int64_t)r * a.H + n0);
       }
-    } else {
-      const float4* q = (const float4*)((const float*)a.obuf + (int64_t)r * a.H + n0);
-      float4 u = q[0], v = q[1];
+#pragma unroll
+      for (int j = 0; j < B; j++) {
+        const uint32_t m = j0 + j < nrows ? 0xffffffffu : 0u;
+        const uint32_t w[4] = {q[j].x & m, q[j].y & m, q[j].z & m, q[j].w & m};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          acc[2 * i] += __uint_as_float(w[i] << 16);
+          acc[2 * i + 1] += __uint_as_float(w[i] & 0xffff0000u);
+        }
+      }
+    }
+    uint4 o;
+    o.x = f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
+    o.y = f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
+    o.z = f32_to_bf16(acc[4]) | ((uint32_t)f32_to_bf16(acc[5]) << 16);
+    o.w = f32_to_bf16(acc[6]) | ((uint32_t)f32_to_bf16(acc[7]) << 16);
+    *(uint4*)((uint16_t*)a.y + (int64_t)t * a.H + n0) = o;
+  } else {
+    for (int j = 0; j < nrows; j++) {
+      const float4* q = (const float4*)((const float*)a.obuf + (int64_t)spos[j] * a.H + n0);
+      const float4 u = q[0], v = q[1];
       acc[0] += u.x; acc[1] += u.y; acc[2] += u.z; acc[3] += u.w;
       acc[4] += v.x; acc[5] += v.y; acc[6] += v.z; acc[7] += v.w;
     }
-  }
-  const int64_t o = (int64_t)t * a.H + n0;
-  if (a.xbf) {
-    uint4 q;
-    q.x = f32_to_bf16(acc[0]) | ((uint32_t)f32_to_bf16(acc[1]) << 16);
-    q.y = f32_to_bf16(acc[2]) | ((uint32_t)f32_to_bf16(acc[3]) << 16);
-    q.z = f32_to_bf16(acc[4]) | ((uint32_t)f32_to_bf16(acc[5]) << 16);
-    q.w = f32_to_bf16(acc[6]) | ((uint32_t)f32_to_bf16(acc[7]) << 16);
-    *(uint4*)((uint16_t*)a.y + o) = q;
-  } else {
-    float4* p = (float4*)((float*)a.y + o);
+    float4* p = (float4*)((float*)a.y + (int64_t)t * a.H + n0);
     p[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
     p[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
   }
@@ -435,8 +446,8 @@ hipError_t launch_down_prefill(const ExpertArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_combine(const ExpertArgs& a, hipStream_t s) {
-  const int64_t n = (int64_t)a.T * (a.H / 8);
-  hipLaunchKernelGGL(k_combine, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, a);
+  // H % 8 == 0 holds for every block this library creates with a combine step
+  hipLaunchKernelGGL(k_combine, dim3((unsigned)a.T, (unsigned)((a.H / 8 + 255) / 256)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -34,7 +34,12 @@ struct DispatchArgs {
   int32_t* counts;     // [2]: number of slots, number of tiles
   int32_t* plan;       // decode plan (written by the decode routing tail), see plan_ints()
   int max_slots;
+  int32_t* hist;       // [dispatch_blocks(F)][E] per-block expert counts (multi-block dispatch)
 };
+
+// Multi-block dispatch: entries per block and block count.
+#define HX_DISPATCH_CHUNK 2048
+__host__ __device__ inline int dispatch_blocks(int F) { return (F + HX_DISPATCH_CHUNK - 1) / HX_DISPATCH_CHUNK; }
 
 // Decode plan: everything the decode expert kernels need about the routing, in
 // one contiguous int32 block they pull into LDS with a single coalesced load.

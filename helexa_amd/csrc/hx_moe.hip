@@ -73,7 +73,7 @@ struct hx_moe {
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct WsLayout {
-  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, hbuf, hbf, xh, obuf, xn, ym, total;
+  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, hist, hbuf, hbf, xh, obuf, xn, ym, total;
   int hstride, max_slots, max_tiles;
 };
 
@@ -103,6 +103,7 @@ static WsLayout ws_layout(const hx_moe* m, int64_t T) {
   L.tiles = take(sizeof(int32_t) * 4 * L.max_tiles);
   L.counts = take(sizeof(int32_t) * 4);
   L.plan = take(sizeof(int32_t) * plan_ints(L.max_slots, (int)F, (int)T));
+  L.hist = decode ? 0 : take(sizeof(int32_t) * (size_t)dispatch_blocks((int)F) * E);
   L.hbuf = take(sizeof(float) * (F + T) * L.hstride);
   L.hbf = take(sizeof(uint16_t) * (F + T) * L.hstride);
   const size_t act = m->cfg.act_dtype == HX_BF16 ? 2 : 4;
@@ -239,6 +240,8 @@ extern "C" int hx_moe_create(const hx_moe_config* cfg, const hx_moe_weights* w, 
                 c.num_experts_per_tok, c.num_experts);
   if (c.hidden_size <= 0 || c.shared_expert_intermediate_size < 0)
     return fail(HX_ERR_INVALID_ARGUMENT, "bad hidden_size / shared_expert_intermediate_size");
+  if (c.hidden_size % 8 != 0)   // the combine and router kernels move 8 elements per lane
+    return fail(HX_ERR_UNSUPPORTED, "hidden_size (%d) must be a multiple of 8", c.hidden_size);
   if (c.num_experts > HX_MAX_EXPERTS || c.num_experts_per_tok > HX_MAX_TOPK)
     return fail(HX_ERR_UNSUPPORTED, "at most %d experts and top-%d are supported", HX_MAX_EXPERTS, HX_MAX_TOPK);
   if (c.act_dtype != HX_F32 && c.act_dtype != HX_BF16)
@@ -358,6 +361,7 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
   d.counts = (int32_t*)(ws + L.counts);
   d.plan = (int32_t*)(ws + L.plan);
   d.max_slots = L.max_slots;
+  d.hist = L.hist ? (int32_t*)(ws + L.hist) : nullptr;
   ExpertArgs& a = p.ea;
   a = ExpertArgs{};
   a.gate = m->gate; a.up = m->up; a.down = m->down;

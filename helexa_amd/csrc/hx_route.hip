@@ -157,6 +157,155 @@ __global__ __launch_bounds__(1024) void k_dispatch(DispatchArgs a) {
   dispatch_block<1024>(a, sm);
 }
 
+// ----------------------------------------------------------------------------
+// Multi-block dispatch for large F (prefill): the same outputs as k_dispatch.
+//   k_disp_hist    block b counts the experts of entries [2048 b, 2048 b + 2048)
+//   k_disp_scan    one block: per expert, the exclusive prefix over blocks and
+//                  the total; offsets = exclusive scan of the totals; slots and
+//                  M-tiles as in dispatch_block
+//   k_disp_scatter block b places its entries stably: position = offsets[e] +
+//                  (entries of e in earlier blocks) + (rank within the block)
+// ----------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_disp_hist(DispatchArgs a) {
+  __shared__ int cnt[HX_MAX_EXPERTS];
+  const int b = blockIdx.x, E = a.E;
+  for (int e = threadIdx.x; e < E; e += 256) cnt[e] = 0;
+  __syncthreads();
+  const int f0 = b * HX_DISPATCH_CHUNK, f1 = min(a.F, f0 + HX_DISPATCH_CHUNK);
+  for (int f = f0 + threadIdx.x; f < f1; f += 256) atomicAdd(&cnt[a.topk_idx[f]], 1);
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 256) a.hist[(int64_t)b * E + e] = cnt[e];
+}
+
+// exclusive scan of one value per thread over a 1024-thread block; *total gets
+// the sum (sh: 17 ints of LDS)
+HX_DEV int block_scan_1024(int v, int* sh, int* total) {
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) sh[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    for (int w = 0; w < 16; w++) {
+      const int c = sh[w];
+      sh[w] = run;
+      run += c;
+    }
+    sh[16] = run;
+  }
+  __syncthreads();
+  const int r = sh[wave] + x - v;
+  *total = sh[16];
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(1024) void k_disp_scan(DispatchArgs a) {
+  __shared__ int sh[17];
+  const int e = threadIdx.x, E = a.E, nb = dispatch_blocks(a.F);
+  int count = 0;
+  if (e < E) {
+    for (int b = 0; b < nb; b++) {
+      const int h = a.hist[(int64_t)b * E + e];
+      a.hist[(int64_t)b * E + e] = count;
+      count += h;
+    }
+  }
+  int tot;
+  const int off = block_scan_1024(e < E ? count : 0, sh, &tot);
+  const int slot = block_scan_1024(e < E && count > 0 ? 1 : 0, sh, &tot);
+  const int nslot = tot;
+  const int ntile_e = e < E ? (count + a.tile_m - 1) / a.tile_m : 0;
+  const int tile0 = block_scan_1024(ntile_e, sh, &tot);
+  const int ntile = tot;
+  if (e < E) {
+    a.offsets[e] = off;
+    // per-block bases: offsets[e] + entries of e in earlier blocks
+    for (int b = 0; b < nb; b++) a.hist[(int64_t)b * E + e] += off;
+    if (count > 0) {
+      a.slots[3 * slot + 0] = e;
+      a.slots[3 * slot + 1] = off;
+      a.slots[3 * slot + 2] = count;
+      for (int m0 = 0, i = 0; m0 < count; m0 += a.tile_m, i++) {
+        a.tiles[4 * (tile0 + i) + 0] = slot;
+        a.tiles[4 * (tile0 + i) + 1] = e;
+        a.tiles[4 * (tile0 + i) + 2] = off + m0;
+        a.tiles[4 * (tile0 + i) + 3] = count - m0 < a.tile_m ? count - m0 : a.tile_m;
+      }
+    }
+  }
+  if (e == 0) a.offsets[E] = a.F;
+  int ns = nslot, nt = ntile;
+  if (a.has_shared) {
+    const int nst = (a.T + a.tile_m - 1) / a.tile_m;
+    for (int i = threadIdx.x; i < nst; i += 1024) {
+      const int m0 = i * a.tile_m;
+      a.tiles[4 * (ntile + i) + 0] = nslot;
+      a.tiles[4 * (ntile + i) + 1] = E;
+      a.tiles[4 * (ntile + i) + 2] = a.F + m0;
+      a.tiles[4 * (ntile + i) + 3] = a.T - m0 < a.tile_m ? a.T - m0 : a.tile_m;
+    }
+    if (threadIdx.x == 0) {
+      a.slots[3 * nslot + 0] = E;
+      a.slots[3 * nslot + 1] = a.F;
+      a.slots[3 * nslot + 2] = a.T;
+    }
+    ns++;
+    nt += nst;
+  }
+  if (threadIdx.x == 0) {
+    a.counts[0] = ns;
+    a.counts[1] = nt;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_disp_scatter(DispatchArgs a) {
+  __shared__ int cnt[HX_MAX_EXPERTS];
+  __shared__ uint8_t whist[4][HX_MAX_EXPERTS];
+  const int b = blockIdx.x, E = a.E, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  for (int e = tid; e < E; e += 256) {
+    cnt[e] = a.hist[(int64_t)b * E + e];
+    whist[0][e] = whist[1][e] = whist[2][e] = whist[3][e] = 0;
+  }
+  __syncthreads();
+  const int f0 = b * HX_DISPATCH_CHUNK, f1 = min(a.F, f0 + HX_DISPATCH_CHUNK);
+  const int nbits = 32 - __clz(E);
+  const unsigned long long lt = (1ull << lane) - 1ull;
+  for (int base = f0; base < f1; base += 256) {
+    const int f = base + tid;
+    const bool valid = f < f1;
+    const int e = valid ? a.topk_idx[f] : 0;
+    unsigned long long mask = __ballot(valid);
+    for (int bit = 0; bit < nbits; bit++) {
+      const int v = (e >> bit) & 1;
+      const unsigned long long m = __ballot(v);
+      mask &= v ? m : ~m;
+    }
+    const int rank = __popcll(mask & lt), wcount = __popcll(mask);
+    const bool leader = valid && rank == 0;
+    if (leader) whist[wave][e] = (uint8_t)wcount;
+    __syncthreads();
+    if (valid) {
+      int pre = 0;
+      for (int w = 0; w < wave; w++) pre += whist[w][e];
+      const int pos = cnt[e] + pre + rank;
+      a.perm[pos] = f;
+      if (a.inv) a.inv[f] = pos;
+    }
+    __syncthreads();
+    if (leader) {
+      atomicAdd(&cnt[e], wcount);
+      whist[wave][e] = 0;
+    }
+    __syncthreads();
+  }
+}
+
 // per-token routing for any T: one wave per token
 template <int EPL>
 __global__ __launch_bounds__(256) void k_route_tokens(const float* logits, int E1, int T, int E, int k, bool norm,
@@ -175,11 +324,17 @@ __global__ __launch_bounds__(256) void k_route_tokens(const float* logits, int E
   if (has_shared && lane == 0) sgw[t] = sigmoidf_(lg[E]);
 }
 
-// router logits for any T: each wave owns TT tokens x TE router rows
+// router logits for any T: each wave owns TT tokens x TE router rows. Grid
+// (row groups, token groups rounded up to 8); the linear workgroup id is mapped
+// so that all row groups of one token group run on the same XCD (workgroups go
+// to XCD id % 8): the token group's rows are fetched into that XCD's L2 once.
 template <bool XBF, bool RBF, int TT, int TE>
 __global__ __launch_bounds__(256) void k_router(RouterArgs a) {
   const int wave = threadIdx.x >> 6;
-  router_rows<XBF, RBF, TT, TE>(a, (blockIdx.x * 4 + wave) * TE, blockIdx.y * TT);
+  const int NX = gridDim.x, L = blockIdx.y * NX + blockIdx.x;
+  const int rg = (L >> 3) % NX, tg = (L / (8 * NX)) * 8 + (L & 7);
+  if (tg * TT >= a.T) return;
+  router_rows<XBF, RBF, TT, TE>(a, (rg * 4 + wave) * TE, tg * TT);
 }
 
 // routing of a few tokens in one workgroup (256 or 512 threads: one wave per
@@ -193,14 +348,14 @@ __global__ __launch_bounds__(512) void k_route_small(RouterArgs a) {
 template <bool XBF, bool RBF>
 static void launch_router_t(const RouterArgs& a, hipStream_t s) {
   if (a.T <= 2) {
-    dim3 grid((a.E1 + 3) / 4, (a.T + 1) / 2);
+    dim3 grid((a.E1 + 3) / 4, ((a.T + 1) / 2 + 7) / 8 * 8);
     hipLaunchKernelGGL((k_router<XBF, RBF, 2, 1>), grid, dim3(256), 0, s, a);
   } else if (a.T <= HX_DECODE_MAX_T) {
-    dim3 grid((a.E1 + 3) / 4, (a.T + 7) / 8);
+    dim3 grid((a.E1 + 3) / 4, ((a.T + 7) / 8 + 7) / 8 * 8);
     hipLaunchKernelGGL((k_router<XBF, RBF, 8, 1>), grid, dim3(256), 0, s, a);
   } else {
     constexpr int TT = 8, TE = 4;
-    dim3 grid((a.E1 + 4 * TE - 1) / (4 * TE), (a.T + TT - 1) / TT);
+    dim3 grid((a.E1 + 4 * TE - 1) / (4 * TE), ((a.T + TT - 1) / TT + 7) / 8 * 8);
     hipLaunchKernelGGL((k_router<XBF, RBF, TT, TE>), grid, dim3(256), 0, s, a);
   }
 }
@@ -230,7 +385,14 @@ void launch_route_tokens(const RouterArgs& a, hipStream_t s) {
 }
 
 void launch_dispatch(const DispatchArgs& d, hipStream_t s) {
-  hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, d);
+  const int nb = dispatch_blocks(d.F);
+  if (nb <= 1 || !d.hist || d.E > 1024) {
+    hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, d);
+    return;
+  }
+  hipLaunchKernelGGL(k_disp_hist, dim3(nb), dim3(256), 0, s, d);
+  hipLaunchKernelGGL(k_disp_scan, dim3(1), dim3(1024), 0, s, d);
+  hipLaunchKernelGGL(k_disp_scatter, dim3(nb), dim3(256), 0, s, d);
 }
 
 }  // namespace hx
