@@ -269,9 +269,10 @@ HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U
 }
 
 // ----------------------------------------------------------------------------
-// K1: router logits (blocks [0, nrb)) and the shared expert's gate/up + SwiGLU
-// (blocks [nrb, ...)), which needs only the tokens. The shared blocks also pull
-// the shared down projection into the caches for K3.
+// K1: router logits (blocks [0, nrb)) and, for T > 1, the shared expert's
+// gate/up + SwiGLU (blocks [nrb, ...)), which needs only the tokens; those
+// blocks also pull the shared down projection into the caches for K3. For
+// T == 1 the shared expert is computed inside K2 while it routes.
 // ----------------------------------------------------------------------------
 template <int FMT, int LPR, int NR, bool RBF, int TT>
 __global__ __launch_bounds__(256) void k_router_dec(RouterArgs r, ExpertArgs a, int nrb) {
@@ -297,17 +298,33 @@ __global__ __launch_bounds__(256) void k_router_dec(RouterArgs r, ExpertArgs a, 
 }
 
 // ----------------------------------------------------------------------------
-// K2: routed gate/up + SwiGLU. Every workgroup routes the T tokens from the
-// logits in LDS. The last grid row's workgroup 0 only publishes routing and
-// plan; workgroup (x, u < last row) computes rows of slot u's expert. (Pulling
-// the expert's down projection into the caches here as well was measured to
-// cost more in this kernel than it saved in the next.)
+// K2 (T == 1): routed gate/up + SwiGLU. Every workgroup routes the token from
+// the logits in LDS (wave 0) while its other waves compute shared-expert rows.
+// The last grid row's workgroup 0 only publishes routing and plan; workgroup
+// (x, u < last row) computes rows of slot u's expert. (Pulling the expert's
+// down projection into the caches here as well was measured to cost more in
+// this kernel than it saved in the next.)
 // ----------------------------------------------------------------------------
 template <int FMT, int LPR, int NR>
 __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a) {
   constexpr int RG = 64 / LPR;
   __shared__ RouteSmem sm;
   const bool publisher = blockIdx.y == gridDim.y - 1;
+  const int wave = threadIdx.x >> 6;
+  if (wave > 0 && a.Is > 0) {
+    // waves 1..3 compute the shared expert's gate/up rows (RG * NR per wave, in
+    // linear workgroup order) while wave 0 routes
+    const int task = (blockIdx.y * gridDim.x + blockIdx.x) * 3 + wave - 1;
+    const int r0 = task * (RG * NR);
+    if (r0 < a.Is) {
+      int tok[HX_DECODE_MAX_T], hrow[HX_DECODE_MAX_T];
+      for (int j = 0; j < a.T; j++) {
+        tok[j] = j;
+        hrow[j] = a.F + j;
+      }
+      gate_up_rows<FMT, LPR, NR>(a, a.sgate.base, a.sup.base, a.Is, r0 + lane_id() / LPR, a.T, tok, hrow);
+    }
+  }
   if (publisher && blockIdx.x > 0) return;
   route_small_lds(r.logits, r.E1, r.E, r.k, r.norm, publisher && r.has_shared, r.T, sm);
   if (publisher) {
@@ -317,7 +334,6 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
   const int u = blockIdx.y;
   if (u >= sm.nroute) return;
   const int e = sm.slots[3 * u], start = sm.slots[3 * u + 1], count = sm.slots[3 * u + 2];
-  const int wave = threadIdx.x >> 6;
   int tok[HX_DECODE_MAX_T], hrow[HX_DECODE_MAX_T];
   for (int j = 0; j < count; j++) {
     hrow[j] = start + j;
@@ -444,7 +460,7 @@ static hipError_t router_dec_fmt(const RouterArgs& r, const ExpertArgs& a, bool 
 #define RD(LPR, RB, TT)                                                                     \
   {                                                                                         \
     constexpr int RG = 64 / LPR;                                                            \
-    const int nsb = a.Is > 0 ? (a.Is + 4 * RG * NR - 1) / (4 * RG * NR) : 0;                \
+    const int nsb = a.Is > 0 && a.T > 1 ? (a.Is + 4 * RG * NR - 1) / (4 * RG * NR) : 0;    \
     hipLaunchKernelGGL((k_router_dec<FMT, LPR, NR, RB, TT>), dim3(nrb + nsb), dim3(256), 0, s, r, a, nrb); \
   }
 #define RD_T(LPR, RB) { if (r.T <= 1) RD(LPR, RB, 1) else if (r.T <= 2) RD(LPR, RB, 2) else if (r.T <= 4) RD(LPR, RB, 4) else RD(LPR, RB, 8) }
