@@ -28,17 +28,9 @@ HX_DEV uint16_t f32_to_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 
-// exact for every f16 value (normal, subnormal, inf, nan)
-HX_DEV float f16_to_f32(uint16_t h) {
-  uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
-  uint32_t e = (h >> 10) & 0x1fu, m = h & 0x3ffu;
-  if (e == 0) {
-    float v = (float)m * 5.9604644775390625e-8f;
-    return sign ? -v : v;
-  }
-  if (e == 31) return __uint_as_float(sign | 0x7f800000u | (m << 13));
-  return __uint_as_float(sign | ((e + 112u) << 23) | (m << 13));
-}
+// exact for every f16 value (normal, subnormal, inf, nan): v_cvt_f32_f16 with
+// f16 denormals kept (the default mode of HIP kernels)
+HX_DEV float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
 // round-to-nearest-even f32 -> f16 bits, subnormals kept, overflow -> inf
 HX_DEV uint16_t f32_to_f16(float f) {
@@ -130,7 +122,7 @@ HX_DEV float siluf_(float g) { return g / (1.0f + __expf(-g)); }
 //   off 32 / 16: v_permlane32_swap / v_permlane16_swap of v with itself; the two
 //     results hold (own, partner) in some order in every lane;
 //   off 8: DPP row_ror:8, which is lane ^ 8 within a row of 16;
-//   off 4: DPP row_ror:4 gives lane (r + 4) mod 16, which is r ^ 4 or r ^ 4 ^ 8;
+//   off 4: DPP row_ror:4 reads lane (r - 4) mod 16, which is r ^ 4 or r ^ 4 ^ 8;
 //     once the off-8 step is done, lanes r ^ 4 and r ^ 4 ^ 8 hold equal values;
 //   off 2 / 1: DPP quad_perm [2,3,0,1] / [1,0,3,2].
 // Groups of 8 lanes use __shfl_xor for the off-4 step.
@@ -156,6 +148,47 @@ HX_DEV float wave_sum(float v) {
   if (WIDTH >= 2) v = v + dpp_f<0xB1>(v);     // quad_perm [1,0,3,2]
   return v;
 }
+
+// The butterfly of wave_sum<64> applied to 64 values at once, as a
+// reduce-scatter: at each step a lane adds its partner's copy of only the half
+// of its live values it keeps (the half selected by the lane's bit for that
+// step), so every addition is one the butterfly performs and the sums are the
+// same bit for bit; lane l ends with the sum of v[l]. 141 instructions instead
+// of 64 butterflies. Lane semantics used: permlane32_swap(x, y) returns
+// (own x, x of lane + 32) in lanes 0..31 and (y of lane - 32, own y) in lanes
+// 32..63, permlane16_swap the same for rows 0/1 and 2/3; DPP row_ror:N reads
+// lane (r - N) mod 16 of the row.
+HX_DEV float reduce_scatter64(float (&v)[64]) {
+  const int l = __lane_id();
+#pragma unroll
+  for (int k = 0; k < 32; k++) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 32]), false, false);
+    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int k = 0; k < 16; k++) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[k]), __float_as_uint(v[k + 16]), false, false);
+    v[k] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+#pragma unroll
+  for (int k = 0; k < 8; k++) {   // lane ^ 8: row_ror:8
+    const float s1 = v[k] + dpp_f<0x128>(v[k]), s2 = v[k + 8] + dpp_f<0x128>(v[k + 8]);
+    v[k] = (l & 8) ? s2 : s1;
+  }
+#pragma unroll
+  for (int k = 0; k < 4; k++) {   // lane ^ 4: lane + 4 (row_ror:12) where bit 2 is clear, lane - 4 (row_ror:4) where set
+    const float s1 = v[k] + dpp_f<0x12C>(v[k]), s2 = v[k + 4] + dpp_f<0x124>(v[k + 4]);
+    v[k] = (l & 4) ? s2 : s1;
+  }
+#pragma unroll
+  for (int k = 0; k < 2; k++) {   // lane ^ 2: quad_perm [2,3,0,1]
+    const float s1 = v[k] + dpp_f<0x4E>(v[k]), s2 = v[k + 2] + dpp_f<0x4E>(v[k + 2]);
+    v[k] = (l & 2) ? s2 : s1;
+  }
+  const float s1 = v[0] + dpp_f<0xB1>(v[0]), s2 = v[1] + dpp_f<0xB1>(v[1]);   // lane ^ 1: quad_perm [1,0,3,2]
+  return (l & 1) ? s2 : s1;
+}
+
 
 HX_DEV unsigned long long wave_max_u64(unsigned long long v) {
 #pragma unroll

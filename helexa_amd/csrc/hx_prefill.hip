@@ -213,6 +213,278 @@ HX_DEV void xcd_tile(int& nt, int& tile) {
 
 HX_DEV f16x8_t frag(const uint16_t* base) { return __builtin_bit_cast(f16x8_t, *(const uint4*)base); }
 
+// ---------------------------------------------------------------- Q4_K gate/up, streamed
+// k_gate_up_q4k<FPW, NW>: the gate/up GEMM for Q4_K weights, operands
+// streamed into LDS by the memory unit (global_load_lds_dwordx4: lane l's 16
+// bytes land at the wave's LDS base + 16 l, no registers involved) through a
+// ring of NST K-chunk stages, NST - 1 chunks ahead of the MFMAs.
+// Tile: 64 gathered rows x 16 FPW NW gate + as many up columns; wave w owns
+// gate and up columns 16 (FPW w + j) .. + 15, j < FPW.
+//   stage: A = 64 token rows x 128 K (f16, 16 KB), the 16-byte pieces of row r
+//          stored at piece p ^ (r % 16) so the 16 rows of an MFMA fragment read
+//          hit different LDS banks;
+//          B = the raw GGUF bytes the chunk needs of each of the 32 FPW NW
+//          weight rows (gate rows, then up rows): the superblock header (16 B) and the
+//          64 qs bytes of the chunk's half superblock, 80 B per row.
+// Each wave dequantises its own B fragments from the raw bytes in LDS, so the
+// activations are the only operand every wave reads in full.
+// LDS: FPW = 1 with 4 waves, 3 stages of 26 KB (2 workgroups per CU, about
+// 100 KB in flight per CU). Measured on MI355X for the A3B shapes, this beats
+// 8 waves over 128 + 128 columns (4 stages of 36 KB, one workgroup per CU)
+// and 4 waves with FPW = 2: fewer waves per SIMD hide less of the LDS and
+// dequantisation latency than the halved activation traffic saves.
+// The DMA instructions are issued from inline assembly (M0 saved and restored
+// around them) because the compiler, not knowing which LDS bytes a DMA writes,
+// would otherwise wait for every outstanding one before each LDS read; the
+// waits are placed by hand: before the barrier of chunk kc, a wave waits until
+// only its DMAs of the chunks after kc are outstanding.
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+HX_DEV uint4 lds_ld16(const lds_u8* p) {
+  const u32x4_t v = *(const __attribute__((address_space(3))) u32x4_t*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+HX_DEV uint2 lds_ld8(const lds_u8* p) {
+  const u32x2_t v = *(const __attribute__((address_space(3))) u32x2_t*)p;
+  return make_uint2(v.x, v.y);
+}
+
+HX_DEV void dma16(const void* g, uint32_t lds_base) {
+  uint32_t save;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(save) : "v"(g), "s"(lds_base) : "memory");
+}
+
+constexpr int QA_BYTES = PM * 128 * 2;   // A stage
+constexpr int QB_ROW = 80;                // B bytes per weight row per chunk
+
+// FPW: B fragments per matrix per wave; NW: waves per workgroup
+template <int FPW, int NW>
+struct Q4k {
+  static constexpr int FPW_ = FPW;
+  static constexpr int NT = 64 * NW;
+  static constexpr int COLS = 16 * FPW * NW;             // gate (and up) columns of a tile
+  static constexpr int BROWS = 2 * COLS;                 // gate + up weight rows
+  static constexpr int STAGE = QA_BYTES + BROWS * QB_ROW;
+  static constexpr int NST = STAGE <= 27 * 1024 ? 3 : 4;
+  static constexpr int NA = 1024 / NT;                   // A DMA rounds
+  static constexpr int BPIECES = 5 * BROWS;              // 16-byte pieces of B per chunk
+  static constexpr int NBI = (BPIECES + NT - 1) / NT;    // B DMA rounds
+  // DMA instructions per chunk of wave w
+  HX_DEV static int per_wave(int w) { return NA + (BPIECES - NT * (NBI - 1) > 64 * w ? NBI : NBI - 1); }
+};
+
+// Per-thread DMA sources of chunk 0; chunk kc adds 256 kc bytes to the A
+// sources and (kc / 2) 144 bytes (+ 64 for odd kc on qs pieces) to the B ones.
+// A: thread t moves piece t % 16 (stored at slot t % 16, holding K segment
+// (t % 16) ^ (row % 16)) of rows t / 16 + (NT / 16) i.  B: piece q = NT i + t
+// is part q % 5 of weight row q / 5: the header (part 0) or 16 qs bytes
+// (parts 1..4).
+template <class Q>
+struct Q4kSrc {
+  const uint8_t* a[Q::NA];
+  const uint8_t* b[Q::NBI];
+  uint32_t bq;   // bit i: b[i] is a qs piece
+};
+
+template <class Q>
+HX_DEV Q4kSrc<Q> q4k_sources(const uint16_t* xh, int H, const int* rowsrc, const uint8_t* G, const uint8_t* U,
+                             int n0, int K) {
+  const int tid = threadIdx.x;
+  Q4kSrc<Q> src;
+  const int sl = tid & 15, r0 = tid >> 4, seg = sl ^ (r0 & 15);
+#pragma unroll
+  for (int i = 0; i < Q::NA; i++) src.a[i] = (const uint8_t*)(xh + (int64_t)rowsrc[r0 + (Q::NT / 16) * i] * H + 8 * seg);
+  src.bq = 0;
+#pragma unroll
+  for (int i = 0; i < Q::NBI; i++) {
+    const int q = i * Q::NT + tid < Q::BPIECES ? i * Q::NT + tid : 0, row = q / 5, part = q - 5 * row;
+    const uint8_t* mat = row < Q::COLS ? G : U;
+    const uint8_t* sbp = mat + (int64_t)(n0 + (row < Q::COLS ? row : row - Q::COLS)) * (K / 256) * 144;
+    src.b[i] = part == 0 ? sbp : sbp + 16 * part;
+    src.bq |= (part != 0 ? 1u : 0u) << i;
+  }
+  return src;
+}
+
+// DMA of chunk kc into stage st
+template <class Q>
+HX_DEV void q4k_issue(uint32_t lds0, int st, const Q4kSrc<Q>& src, int kc, int wave_u) {
+  const uint32_t sbase = lds0 + (uint32_t)(st * Q::STAGE + wave_u * 64 * 16);
+#pragma unroll
+  for (int i = 0; i < Q::NA; i++) dma16(src.a[i] + 256 * kc, sbase + (uint32_t)(i * Q::NT * 16));
+  const int hdr_off = (kc >> 1) * 144, qs_off = hdr_off + 64 * (kc & 1);
+#pragma unroll
+  for (int i = 0; i < Q::NBI; i++) {
+    if (i * Q::NT + 64 * wave_u >= Q::BPIECES) break;   // the last round may cover fewer waves
+    dma16(src.b[i] + ((src.bq >> i) & 1 ? qs_off : hdr_off), sbase + (uint32_t)(QA_BYTES + i * Q::NT * 16));
+  }
+}
+
+// v_and_or_b32 with its two constants in registers (a VOP3 instruction on this
+// target takes no literal operand; left to itself the compiler splits the
+// operation into an and and an or, each with a literal)
+HX_DEV uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(o));
+  return r;
+}
+
+// f16 (a, nb) of sub-blocks 4 PAR .. 4 PAR + 3 of a Q4_K superblock header:
+// a = d sc, nb = -dmin m, each one f16 rounding of the exact product (as in
+// h2s(d * (float)sc)); the 6-bit sc and m of the four sub-blocks are
+// gathered into the bytes of one word, turned into exact f16 integers by the
+// 1024 magic and scaled two at a time.
+template <int PAR>
+HX_DEV void q4k_scales(const uint4& hdr, uint32_t kbyte, uint32_t kmagic, h2_t* a, h2_t* nb) {
+  uint32_t scb, mb;
+  if (PAR == 0) {
+    scb = hdr.y & 0x3F3F3F3Fu;
+    mb = hdr.z & 0x3F3F3F3Fu;
+  } else {
+    scb = (hdr.w & 0x0F0F0F0Fu) | ((hdr.y >> 2) & 0x30303030u);
+    mb = ((hdr.w >> 4) & 0x0F0F0F0Fu) | ((hdr.z >> 2) & 0x30303030u);
+  }
+  const h2_t dm = h2(hdr.x), off = h2s(-1024.0f);
+  const h2_t d2 = __builtin_shufflevector(dm, dm, 0, 0), nm2 = -__builtin_shufflevector(dm, dm, 1, 1);
+  const h2_t s02 = (h2(and_or(scb, kbyte, kmagic)) + off) * d2, s13 = (h2(and_or(scb >> 8, kbyte, kmagic)) + off) * d2;
+  const h2_t m02 = (h2(and_or(mb, kbyte, kmagic)) + off) * nm2, m13 = (h2(and_or(mb >> 8, kbyte, kmagic)) + off) * nm2;
+  a[0] = __builtin_shufflevector(s02, s02, 0, 0);
+  a[1] = __builtin_shufflevector(s13, s13, 0, 0);
+  a[2] = __builtin_shufflevector(s02, s02, 1, 1);
+  a[3] = __builtin_shufflevector(s13, s13, 1, 1);
+  nb[0] = __builtin_shufflevector(m02, m02, 0, 0);
+  nb[1] = __builtin_shufflevector(m13, m13, 0, 0);
+  nb[2] = __builtin_shufflevector(m02, m02, 1, 1);
+  nb[3] = __builtin_shufflevector(m13, m13, 1, 1);
+}
+
+template <class Q, int PAR>   // chunk parity: sub-blocks 4 PAR .. 4 PAR + 3 of the superblock
+HX_DEV void q4k_compute(const lds_u8* st, f32x4_t (*accg)[Q::FPW_], f32x4_t (*accu)[Q::FPW_], int wave, int l16, int kq,
+                        uint32_t knib, uint32_t kbyte, uint32_t kmagic) {
+  constexpr int NF = Q::FPW_;
+  const lds_u8* B = st + QA_BYTES;
+  constexpr int NB = 2 * NF;   // B fragments of the wave: gate j, then up j
+  uint4 hdr[NB];
+  uint2 qs[NB][2];
+#pragma unroll
+  for (int f = 0; f < NB; f++) {
+    const int row = (f < NF ? 0 : Q::COLS) + 16 * (NF * wave + f % NF) + l16;
+    hdr[f] = lds_ld16(B + row * QB_ROW);
+#pragma unroll
+    for (int g = 0; g < 2; g++) qs[f][g] = lds_ld8(B + row * QB_ROW + 16 + 32 * g + 8 * kq);
+  }
+  h2_t a[NB][4], nb[NB][4];
+#pragma unroll
+  for (int f = 0; f < NB; f++) q4k_scales<PAR>(hdr[f], kbyte, kmagic, a[f], nb[f]);
+  const h2_t off = h2s(-1024.0f);
+#pragma unroll
+  for (int s = 0; s < 4; s++) {
+    const int g = s >> 1, hi = s & 1;
+    f16x8_t bf[NB];
+#pragma unroll
+    for (int f = 0; f < NB; f++) {
+      const uint32_t w0 = qs[f][g].x >> (4 * hi), w1 = qs[f][g].y >> (4 * hi);
+      bf[f] = __builtin_bit_cast(f16x8_t, make_uint4(fma_pair(and_or(w0, knib, kmagic), a[f][s], nb[f][s], off),
+                                                     fma_pair(and_or(w0 >> 8, knib, kmagic), a[f][s], nb[f][s], off),
+                                                     fma_pair(and_or(w1, knib, kmagic), a[f][s], nb[f][s], off),
+                                                     fma_pair(and_or(w1 >> 8, knib, kmagic), a[f][s], nb[f][s], off)));
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++) {
+      const int row = 16 * mt + l16, seg = 4 * s + kq;
+      const f16x8_t av = __builtin_bit_cast(f16x8_t, *(const __attribute__((address_space(3))) u32x4_t*)(st + row * 256 + ((seg ^ l16) << 4)));
+#pragma unroll
+      for (int j = 0; j < NF; j++) {
+        accg[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[j], accg[mt][j], 0, 0, 0);
+        accu[mt][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf[NF + j], accu[mt][j], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// wait until at most `ahead` chunks of this wave's DMAs are outstanding;
+// `ahead` and the count are wave-uniform, so the branches are scalar
+template <class Q>
+HX_DEV void q4k_wait(int ahead, int wave_u) {
+  const int n = ahead * Q::per_wave(wave_u);
+  switch (n) {
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 7: asm volatile("s_waitcnt vmcnt(7)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+    case 18: asm volatile("s_waitcnt vmcnt(18)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+  }
+}
+
+// grid (I / COLS, tiles rounded up to 8), mapped by xcd_tile
+template <int FPW, int NW>
+__global__ __launch_bounds__(64 * NW, (Q4k<FPW, NW>::NST == 3 ? 2 : 1)) void k_gate_up_q4k(ExpertArgs a) {
+  using Q = Q4k<FPW, NW>;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[Q::NST * Q::STAGE];
+  __shared__ int rowsrc[PM];
+  int nt, tile;
+  xcd_tile(nt, tile);
+  if (tile >= a.counts[1]) return;
+  const int e = a.tiles[4 * tile + 1], p0 = a.tiles[4 * tile + 2], rows = a.tiles[4 * tile + 3];
+  const bool sh = e == a.E;
+  const int n0 = nt * Q::COLS;
+  const uint8_t* G = sh ? a.sgate.base : a.gate.mat(e);
+  const uint8_t* U = sh ? a.sup.base : a.up.mat(e);
+  const int K = a.H, nk = K / 128;
+  if (threadIdx.x < PM) {
+    const int p = p0 + (threadIdx.x < rows ? threadIdx.x : 0);   // padding rows repeat row 0
+    rowsrc[threadIdx.x] = sh ? p - a.F : a.perm[p] / a.k;
+  }
+  __syncthreads();
+  const int lane = lane_id(), wave = threadIdx.x >> 6, l16 = lane & 15, kq = lane >> 4;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)ring;
+  f32x4_t accg[4][FPW], accu[4][FPW];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < FPW; j++) {
+      accg[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      accu[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+  const Q4kSrc<Q> src = q4k_sources<Q>(a.xh, a.H, rowsrc, G, U, n0, K);
+  // dequantisation constants, kept in registers for v_and_or_b32
+  const uint32_t knib = __builtin_amdgcn_readfirstlane(0x000F000Fu), kbyte = __builtin_amdgcn_readfirstlane(0x00FF00FFu);
+  uint32_t kmagic;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(kmagic));
+#pragma unroll
+  for (int c = 0; c < Q::NST - 1; c++)
+    if (c < nk) q4k_issue<Q>(lds0, c, src, c, wave_u);
+  for (int kc = 0; kc < nk; kc++) {
+    const int ahead = min(Q::NST - 2, nk - 1 - kc);
+    q4k_wait<Q>(ahead, wave_u);
+    __syncthreads();   // chunk kc is in LDS for every wave; stage (kc - 1) % NST is free
+    if (kc + Q::NST - 1 < nk) q4k_issue<Q>(lds0, (kc + Q::NST - 1) % Q::NST, src, kc + Q::NST - 1, wave_u);
+    const lds_u8* st = (const lds_u8*)ring + (kc % Q::NST) * Q::STAGE;
+    if (kc & 1) q4k_compute<Q, 1>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
+    else q4k_compute<Q, 0>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
+  }
+#pragma unroll
+  for (int j = 0; j < FPW; j++) {
+    const int col = swz(n0 + 16 * (FPW * wave + j) + l16);
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int m = 16 * mt + 4 * kq + i;
+        if (m < rows)
+          ((_Float16*)a.hbf)[(int64_t)(p0 + m) * a.hstride + col] = (_Float16)(siluf_(accg[mt][j][i]) * accu[mt][j][i]);
+      }
+  }
+}
+
 // ---------------------------------------------------------------- gate/up
 // grid (I / 64, tiles rounded up to 8), mapped by xcd_tile: 64 rows x 64
 // intermediate columns; wave w owns columns
@@ -389,7 +661,7 @@ hipError_t launch_gate_up_mfma(const ExpertArgs& a, hipStream_t s) {
   hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, (const uint16_t*)a.x, n8, a.xh);
   const dim3 grid(a.I / 64, (a.max_tiles + 7) / 8 * 8);
   switch (a.gate.fmt) {
-    case HX_Q4_K: hipLaunchKernelGGL(k_gate_up_mfma<HX_Q4_K>, grid, dim3(256), 0, s, a); break;
+    case HX_Q4_K: hipLaunchKernelGGL((k_gate_up_q4k<1, 4>), grid, dim3(256), 0, s, a); break;
     case HX_Q8_0: hipLaunchKernelGGL(k_gate_up_mfma<HX_Q8_0>, grid, dim3(256), 0, s, a); break;
     case HX_Q6_K: hipLaunchKernelGGL(k_gate_up_mfma<HX_Q6_K>, grid, dim3(256), 0, s, a); break;
     default: return hipErrorInvalidValue;

@@ -337,6 +337,18 @@ __global__ __launch_bounds__(256) void k_router(RouterArgs a) {
   router_rows<XBF, RBF, TT, TE>(a, (rg * 4 + wave) * TE, tg * TT);
 }
 
+// prefill router: one wave per 8 tokens x 8 router rows, four waves per
+// workgroup along the rows; XCD-aware order as in k_router
+template <bool XBF, bool RBF, int NG>
+__global__ __launch_bounds__(256) void k_router88(RouterArgs a) {
+  const int wave = threadIdx.x >> 6;
+  const int NX = gridDim.x, L = blockIdx.y * NX + blockIdx.x;
+  const int rg = (L >> 3) % NX, tg = (L / (8 * NX)) * 8 + (L & 7);
+  const int e0 = (rg * 4 + wave) * 8;
+  if (tg * 8 >= a.T || e0 >= a.E1) return;
+  router_tile88<XBF, RBF, NG>(a, e0, tg * 8);
+}
+
 // routing of a few tokens in one workgroup (256 or 512 threads: one wave per
 // token up to 8), published to global memory
 __global__ __launch_bounds__(512) void k_route_small(RouterArgs a) {
@@ -353,6 +365,11 @@ static void launch_router_t(const RouterArgs& a, hipStream_t s) {
   } else if (a.T <= HX_DECODE_MAX_T) {
     dim3 grid((a.E1 + 3) / 4, ((a.T + 7) / 8 + 7) / 8 * 8);
     hipLaunchKernelGGL((k_router<XBF, RBF, 8, 1>), grid, dim3(256), 0, s, a);
+  } else if (a.H % 8 == 0 && a.H <= 8 * 256) {
+    dim3 grid((a.E1 + 31) / 32, ((a.T + 7) / 8 + 7) / 8 * 8);
+    if (a.H <= 8 * 64) hipLaunchKernelGGL((k_router88<XBF, RBF, 1>), grid, dim3(256), 0, s, a);
+    else if (a.H <= 8 * 128) hipLaunchKernelGGL((k_router88<XBF, RBF, 2>), grid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((k_router88<XBF, RBF, 4>), grid, dim3(256), 0, s, a);
   } else {
     constexpr int TT = 8, TE = 4;
     dim3 grid((a.E1 + 4 * TE - 1) / (4 * TE), ((a.T + TT - 1) / TT + 7) / 8 * 8);

@@ -111,6 +111,75 @@ HX_DEV void router_rows_u(const RouterArgs& a, int e0, int t0) {
     }
 }
 
+// One wave: logits of tokens t0 .. t0+7 for router rows e0 .. e0+7, for
+// H % 8 == 0 and at most 64 * NG groups of 8; same arithmetic order as
+// router_rows_u. The loads of group i + 1 are issued before the multiply-adds
+// of group i; the 64 partial sums of a lane are combined by reduce_scatter64,
+// after which lane l holds the logit of token t0 + l / 8, row e0 + l % 8.
+template <bool XBF, bool RBF, int NG>
+HX_DEV void router_tile88(const RouterArgs& a, int e0, int t0) {
+  constexpr int RW = RBF ? 4 : 8, XW = XBF ? 4 : 8;   // dwords per group of 8 values
+  const int lane = lane_id();
+  const int H = a.H, G = H / 8;
+  uint32_t wr[2][8][RW], xr[2][8][XW];
+  auto load = [&](int i, int b) {
+    const int g = min(lane + 64 * i, G - 1);
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int64_t row = min(e0 + j, a.E1 - 1);
+      const uint4* p = (const uint4*)((const uint8_t*)a.R + (row * H + 8 * g) * (RBF ? 2 : 4));
+#pragma unroll
+      for (int q = 0; q < RW / 4; q++) {
+        const uint4 v = p[q];
+        wr[b][j][4 * q] = v.x; wr[b][j][4 * q + 1] = v.y; wr[b][j][4 * q + 2] = v.z; wr[b][j][4 * q + 3] = v.w;
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 8; t++) {
+      const int64_t tok = min(t0 + t, a.T - 1);
+      const uint4* p = (const uint4*)((const uint8_t*)a.x + (tok * H + 8 * g) * (XBF ? 2 : 4));
+#pragma unroll
+      for (int q = 0; q < XW / 4; q++) {
+        const uint4 v = p[q];
+        xr[b][t][4 * q] = v.x; xr[b][t][4 * q + 1] = v.y; xr[b][t][4 * q + 2] = v.z; xr[b][t][4 * q + 3] = v.w;
+      }
+    }
+  };
+  float acc[64];
+#pragma unroll
+  for (int k = 0; k < 64; k++) acc[k] = 0.0f;
+  load(0, 0);
+#pragma unroll
+  for (int i = 0; i < NG; i++) {
+    const int b = i & 1;
+    if (i + 1 < NG) load(i + 1, b ^ 1);
+    if (lane + 64 * i < G) {   // lanes past the end have no group i
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        float wv[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+          wv[j] = RBF ? __uint_as_float(q & 1 ? wr[b][j][q / 2] & 0xffff0000u : wr[b][j][q / 2] << 16)
+                      : __uint_as_float(wr[b][j][q]);
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+          const float xv = XBF ? __uint_as_float(q & 1 ? xr[b][t][q / 2] & 0xffff0000u : xr[b][t][q / 2] << 16)
+                               : __uint_as_float(xr[b][t][q]);
+#pragma unroll
+          for (int j = 0; j < 8; j++) acc[8 * t + j] = __builtin_fmaf(xv, wv[j], acc[8 * t + j]);
+        }
+      }
+    }
+  }
+  float v = reduce_scatter64(acc);
+  const int tt = t0 + (lane >> 3), e = e0 + (lane & 7);
+  if (tt < a.T && e < a.E1) {
+    if (XBF) v = bf16_to_f32(f32_to_bf16(v));
+    if (a.bias && e < a.E) v = v + a.bias[e];
+    a.logits[(int64_t)tt * a.E1 + e] = v;
+  }
+}
+
 // any H: groups loaded one at a time
 template <bool XBF, bool RBF, int TT, int TE>
 HX_DEV void router_rows_loop(const RouterArgs& a, int e0, int t0) {

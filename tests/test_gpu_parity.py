@@ -116,6 +116,24 @@ def test_routing_and_dispatch_bit_exact(router_case, T):
     assert np.array_equal(r["inv"].cpu().numpy(), inv)
 
 
+@pytest.mark.parametrize("H,fmt,act", [(1032, "FMT_BF16", O.BF16), (2048, "FMT_F32", O.F32),
+                                       (200, "FMT_F32", O.F32), (520, "FMT_BF16", O.BF16)])
+def test_prefill_router_logits_bit_exact_shapes(H, fmt, act):
+    """Prefill router tiles (more than 8 tokens): hidden sizes whose groups of 8
+    leave the last pass of 64 lanes partly empty, and f32 inputs and weights."""
+    hx, synth = _hx()
+    cfg = hx.TextConfig(hidden_size=H, num_experts=40, num_experts_per_tok=4, moe_intermediate_size=32,
+                        shared_expert_intermediate_size=32, norm_topk_prob=True)
+    w = synth.make_weights(cfg, getattr(synth, fmt), 5)
+    blk = hx.Qwen3_5MoeBlock.load(cfg, w, act_dtype=act)
+    o = oracle_for(cfg, synth.to_numpy(w), act)
+    for T in (9, 301):
+        x = synth.make_x(cfg, T, 17 + T, act)
+        got = blk.router_logits(x).cpu().numpy()
+        ref = o.logits(x_np(x))
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (H, T)
+
+
 def test_routing_ties_break_to_lower_id():
     """Duplicate router rows give exactly tied logits; the lower id must win."""
     hx, synth = _hx()
