@@ -437,7 +437,12 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
     if (n0 + r >= a.H) continue;
     float y = 0.f;
     for (int u = 0; u < nslots; u++) y += contrib[((int64_t)u * T + t) * RG + r];
-    ((uint16_t*)a.y)[(int64_t)t * a.H + n0 + r] = f32_to_bf16(y);
+    if (a.resid) {
+      uint16_t* px = a.resid + (int64_t)t * a.H + n0 + r;
+      *px = f32_to_bf16(bf16_to_f32(*px) + bf16_to_f32(f32_to_bf16(y)));
+    } else {
+      ((uint16_t*)a.y)[(int64_t)t * a.H + n0 + r] = f32_to_bf16(y);
+    }
   }
 }
 

@@ -60,6 +60,12 @@ struct RouterArgs {
   float* topk_w;       // [T*k]
   float* sgw;          // [T] sigmoid of the shared-expert gate
   DispatchArgs d;
+  // decoder RMSNorm folded into the router (decode, bf16): x is the layer input,
+  // the logits use x * rsqrt(mean(x^2) + eps) * (1 + norm_w) rounded to bf16,
+  // and workgroup 0 writes that row to xn_out for the expert kernels
+  const float* norm_w = nullptr;
+  float eps = 0.f;
+  uint16_t* xn_out = nullptr;
 };
 
 // One projection stack: E matrices of [rows][K] in the internal layout.
@@ -96,6 +102,9 @@ struct ExpertArgs {
   void* y;             // [T, H] act dtype
   int max_slots, max_tiles;
   const int32_t* plan;
+  // decoder residual folded into the decode down kernel: resid[t] becomes
+  // bf16(resid[t] + bf16(y[t])) in place of writing y (bf16 activations)
+  uint16_t* resid = nullptr;
 };
 
 void launch_router(const RouterArgs& a, bool xbf, bool rbf, hipStream_t s);

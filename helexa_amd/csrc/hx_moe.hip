@@ -425,15 +425,38 @@ static int run_routing(hx_moe* m, Plan& p, hipStream_t s) {
   return HX_OK;
 }
 
+// the decoder's RMSNorm and residual around the block (hx_moe_decoder_mlp)
+struct DecoderFuse {
+  const float* norm_w;
+  float eps;
+  void* x;   // layer input; receives x + block(rmsnorm(x))
+};
+
 static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, size_t ws_bytes,
-                        const float* bias, hipStream_t s) {
+                        const float* bias, hipStream_t s, const DecoderFuse* fz = nullptr) {
   WsLayout L;
   int rc = get_ws(m, T, ws, ws_bytes, L);
   if (rc) return rc;
   Plan p;
   make_plan(m, x, T, y, (uint8_t*)ws, L, bias, p);
   const bool decode = T <= HX_DECODE_MAX_T;
-  if (decode && decode_fast_ok(p.ea)) {
+  const bool fast = decode && decode_fast_ok(p.ea);
+  const bool bf = m->cfg.act_dtype == HX_BF16;
+  const int H = m->cfg.hidden_size;
+  uint16_t* xn = (uint16_t*)((uint8_t*)ws + L.xn);
+  if (fz && fast && T == 1 && H <= 8 * 256) {
+    // RMSNorm inside the router kernel, residual inside the down kernel
+    p.ra.norm_w = fz->norm_w;
+    p.ra.eps = fz->eps;
+    p.ra.xn_out = xn;
+    p.ea.x = xn;
+    p.ea.resid = (uint16_t*)fz->x;
+  } else if (fz) {
+    HX_HIP(launch_rmsnorm(fz->x, bf, T, H, fz->norm_w, fz->eps, xn, s));
+    p.ra.x = p.ea.x = xn;
+    if (fast) p.ea.resid = (uint16_t*)fz->x;   // the down kernel adds the residual
+  }
+  if (fast) {
     // router + shared gate/up; routed gate/up (one token: routing in its
     // prologue; more: routed once by one workgroup, then the plan); down + combine
     tm_mark(m, SLOT_ROUTER, 0, s);
@@ -476,6 +499,7 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
     HX_HIP(launch_combine(p.ea, s));
     tm_mark(m, SLOT_COMBINE, 1, s);
   }
+  if (fz && !p.ea.resid) HX_HIP(launch_residual_add(fz->x, y, bf, T * H, s));
   if (m->tm.on && m->tm.calls < m->tm.max_calls) m->tm.calls++;
   return HX_OK;
 }
@@ -569,12 +593,8 @@ extern "C" int hx_moe_decoder_mlp(hx_moe* m, void* x, int64_t n_tokens, const fl
   int rc = get_ws(m, n_tokens, workspace, workspace_bytes, L);
   if (rc) return rc;
   uint8_t* ws = (uint8_t*)workspace;
-  const bool bf = m->cfg.act_dtype == HX_BF16;
-  const int64_t H = m->cfg.hidden_size;
-  HX_HIP(launch_rmsnorm(x, bf, n_tokens, H, norm_w, eps, ws + L.xn, s));
-  if ((rc = forward_impl(m, ws + L.xn, n_tokens, ws + L.ym, workspace, workspace_bytes, nullptr, s))) return rc;
-  HX_HIP(launch_residual_add(x, ws + L.ym, bf, n_tokens * H, s));
-  return HX_OK;
+  const DecoderFuse fz{norm_w, eps, x};
+  return forward_impl(m, x, n_tokens, ws + L.ym, workspace, workspace_bytes, nullptr, s, &fz);
 }
 
 extern "C" int hx_quantize(int dtype, const float* src, int64_t rows, int64_t cols, void* dst, void* stream) {

@@ -14,7 +14,7 @@ namespace hx {
 
 constexpr int HX_SMALL_F = HX_DECODE_MAX_T * HX_MAX_TOPK;
 
-struct RouteSmem {
+struct alignas(16) RouteSmem {
   int idx[HX_SMALL_F];       // expert of flat entry f = t*k + j
   float w[HX_SMALL_F];       // routing weight of entry f
   int pos[HX_SMALL_F];       // permuted position of entry f
@@ -24,6 +24,8 @@ struct RouteSmem {
   float sgw[HX_DECODE_MAX_T];
   int nroute;
 };
+// the dispatch reads perm four ints at a time
+static_assert(offsetof(RouteSmem, perm) % 16 == 0 && HX_SMALL_F % 4 == 0, "RouteSmem.perm alignment");
 
 // Descending sort of one lane's EPL keys (hi = probability bits, lo = ~expert):
 // comparing (hi, lo) as one 64-bit value orders by probability, then by lower
@@ -69,40 +71,17 @@ HX_DEV void sort_keys_desc(uint32_t* h, uint32_t* l) {
 //
 // Selection: expert e lives in lane e % 64; each lane sorts its EPL keys
 // (probability bits, ~e) in descending order once (so a lane's equal
-// probabilities are ordered by expert id). Probabilities are >= 0, so their bit
-// patterns order like the values; padding (e >= E) has key (0, ~e).
-//   fast pass: each round takes the wave-wide largest head probability (one DPP
-//     reduction) and pops every lane whose head equals it; the round body is
-//     branch-free. It is exact unless two lanes ever hold that maximum at once;
-//   exact pass (only when that happened): each round reduces the heads as
-//     (probability, ~expert) pairs, so the lowest expert id wins a tie.
-template <int EPL>
-HX_DEV void route_rounds_exact(uint32_t* h, uint32_t* l, int k, float& my_p, int& my_e, float& tot) {
-  const int lane = lane_id();
-  for (int r = 0; r < k; r++) {
-    const uint32_t m = wave_max_u32(h[0]);
-    const unsigned long long hold = __ballot(h[0] == m);
-    uint32_t lo;
-    if (__popcll(hold) == 1)
-      lo = (uint32_t)__builtin_amdgcn_readlane((int)l[0], __ffsll((long long)hold) - 1);
-    else
-      lo = wave_max_u32(h[0] == m ? l[0] : 0u);
-    const int e = (int)~lo;
-    const uint32_t wm = (e & 63) == lane ? 0xffffffffu : 0u;
-#pragma unroll
-    for (int j = 0; j + 1 < EPL; j++) {
-      h[j] = (h[j] & ~wm) | (h[j + 1] & wm);
-      l[j] = (l[j] & ~wm) | (l[j + 1] & wm);
-    }
-    h[EPL - 1] &= ~wm;
-    l[EPL - 1] &= ~wm;
-    const float pm = __uint_as_float(m);
-    tot = tot + pm;
-    my_p = lane == r ? pm : my_p;
-    my_e = lane == r ? e : my_e;
-  }
-}
-
+// probabilities are ordered by expert id, and its head is its best entry).
+// Probabilities are >= 0, so their bit patterns order like the values; padding
+// (e >= E) has key (0, ~e). Round r takes the wave-wide largest head
+// probability m (one DPP reduction). When one lane holds m, its head is rank r.
+// When several do (equal probabilities are common: the logits are rounded to
+// the activation dtype), the next entry in rank order is the lowest expert id
+// among their heads -- every lane's lowest id of probability m is its head --
+// found by a second reduction over ~e; that branch is wave-uniform. Only the
+// chosen lane pops. The pop is split: the head is replaced at once (the next
+// reduction needs it); the rest of the shift is applied during the next
+// round's reduction, which does not depend on it.
 template <int EPL>
 HX_DEV void route_token_core(const float* lg, int E, int k, bool norm, int& out_e, float& out_w) {
   const int lane = lane_id();
@@ -123,25 +102,16 @@ HX_DEV void route_token_core(const float* lg, int E, int k, bool norm, int& out_
 #pragma unroll
   for (int j = 0; j < EPL; j++) s = s + v[j];
   s = wave_sum<64>(s);
-  uint32_t h[EPL], l[EPL], h0[EPL], l0[EPL];
+  uint32_t h[EPL], l[EPL];
 #pragma unroll
   for (int j = 0; j < EPL; j++) {
     h[j] = __float_as_uint(v[j] / s);   // padding: 0 / s = +0
     l[j] = ~(uint32_t)(lane + 64 * j);
   }
   sort_keys_desc<EPL>(h, l);
-#pragma unroll
-  for (int j = 0; j < EPL; j++) {
-    h0[j] = h[j];
-    l0[j] = l[j];
-  }
   float my_p = 0.0f, tot = 0.0f;
   int my_e = 0;
-  unsigned long long multi = 0;
-  // The pop of round r is split: the head h[0] is replaced at once (the next
-  // reduction needs it); the rest of the shift is applied during the next
-  // round's reduction, which does not depend on it.
-  uint32_t pend = 0u;   // all-ones in the lanes popped by the previous round
+  uint32_t pend = 0u;   // all-ones in the lane popped by the previous round
   for (int r = 0; r < k; r++) {
     uint32_t x = h[0];
     x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xf, 0xf, false));
@@ -157,22 +127,20 @@ HX_DEV void route_token_core(const float* lg, int E, int k, bool norm, int& out_
     x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false));
     x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false));
     const uint32_t m = (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
-    const bool hit = h[0] == m;
+    bool hit = h[0] == m;
+    unsigned long long hold = __ballot(hit);
+    if (hold & (hold - 1)) {   // several heads hold m: the lowest expert id goes first
+      const uint32_t lo = wave_max_u32(hit ? l[0] : 0u);
+      hit = hit && l[0] == lo;
+      hold = __ballot(hit);
+    }
     pend = hit ? 0xffffffffu : 0u;
-    h[0] = EPL > 1 ? ((h[0] & ~pend) | (h[1] & pend)) : (h[0] & ~pend);
-    const unsigned long long hold = __ballot(hit);
-    multi |= hold & (hold - 1);
     const int e = (int)~(uint32_t)__builtin_amdgcn_readlane((int)l[0], __ffsll((long long)hold) - 1);
+    h[0] = EPL > 1 ? ((h[0] & ~pend) | (h[1] & pend)) : (h[0] & ~pend);
     const float pm = __uint_as_float(m);
     tot = tot + pm;
     my_p = lane == r ? pm : my_p;
     my_e = lane == r ? e : my_e;
-  }
-  if (multi) {   // two lanes held an equal maximum: redo the selection exactly
-    my_p = 0.0f;
-    tot = 0.0f;
-    my_e = 0;
-    route_rounds_exact<EPL>(h0, l0, k, my_p, my_e, tot);
   }
   out_e = my_e;
   out_w = norm ? my_p / tot : my_p;
@@ -252,38 +220,43 @@ HX_DEV void route_small_lds(const float* logits, int E1, int E, int k, bool norm
   for (int t = wave; t < T; t += nw) route_token_lds(logits + (int64_t)t * E1, E, k, norm, want_sgw, t, sm);
   __syncthreads();
   if (F <= 64) {
-    // one wave, entry f in lane f: its position is the number of entries with
-    // a smaller (expert, f) key; it opens a slot when no earlier entry has its
-    // expert; its slot is the number of slot-opening entries with smaller experts
+    // entry f in lane f of wave 0. Stable sort by key (expert, f): position =
+    // number of smaller keys, counted from the keys in LDS (4 per read, all
+    // reads independent). Then, in sorted order, a position starts a slot when
+    // its expert differs from the previous one: the slot index is the number of
+    // starts at or before it (ballot + mbcnt) and the slot ends at the next start.
+    const int F4 = (F + 3) & ~3;
+    if (tid < F4) sm.perm[tid] = tid < F ? (sm.idx[tid] << 6) | tid : 0x7fffffff;   // experts < 1024
+    __syncthreads();
     if (wave == 0) {
       const int lane = lane_id();
-      const int e = lane < F ? sm.idx[lane] : 0x7fff;   // experts < 1024
-      const int key = (e << 6) | lane;
-      int pos = 0, before = 0;
-      for (int j = 0; j < F; j++) {
-        const int kj = __builtin_amdgcn_readlane(key, j);
-        pos += kj < key;
-        before += (kj >> 6) == e && j < lane;
+      const int key = lane < F ? sm.perm[lane] : 0x7fffffff;
+      int pos = 0;
+      for (int j = 0; j < F4; j += 4) {
+        const int4 q = *(const int4*)(sm.perm + j);
+        pos += (q.x < key) + (q.y < key) + (q.z < key) + (q.w < key);
       }
-      const bool first = lane < F && before == 0;
-      const unsigned long long fm = __ballot(first);
-      int slot = 0, count = 0;
-      for (int j = 0; j < F; j++) {
-        const int ej = __builtin_amdgcn_readlane(key, j) >> 6;
-        slot += (int)((fm >> j) & 1ull) & (ej < e);
-        count += ej == e;
-      }
+      __builtin_amdgcn_wave_barrier();   // every read above precedes the writes below
       if (lane < F) {
         sm.pos[lane] = pos;
         sm.perm[pos] = lane;
-        sm.first[lane] = first;
       }
-      if (first) {
+      __builtin_amdgcn_wave_barrier();
+      const int f = lane < F ? sm.perm[lane] : 0;
+      const int e = lane < F ? sm.idx[f] : -1;
+      const int eprev = __builtin_amdgcn_update_dpp(-1, e, 0x138, 0xf, 0xf, false);   // wave_shr:1, lane 0 gets -1
+      const bool start = lane < F && e != eprev;
+      const unsigned long long sb = __ballot(start);
+      if (lane < F) sm.first[f] = start;
+      if (start) {
+        const int slot = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(sb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sb, 0u));
+        const unsigned long long later = sb & ~((2ull << lane) - 1ull);
+        const int next = later ? __ffsll((long long)later) - 1 : F;
         sm.slots[3 * slot + 0] = e;
-        sm.slots[3 * slot + 1] = pos;
-        sm.slots[3 * slot + 2] = count;
+        sm.slots[3 * slot + 1] = lane;
+        sm.slots[3 * slot + 2] = next - lane;
       }
-      if (lane == 0) sm.nroute = __popcll(fm);
+      if (lane == 0) sm.nroute = __popcll(sb);
     }
     __syncthreads();
     return;

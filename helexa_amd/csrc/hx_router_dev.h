@@ -39,6 +39,53 @@ HX_DEV void load8(const void* base, int64_t row_elems, int64_t row, int h0, int 
   }
 }
 
+// The decoder RMSNorm on the bf16 token rows a wave holds in registers (group
+// g = lane + 64 i of token t in xr[t][i]): per token, an fmaf chain of squares
+// over the lane's groups in order, the 64-lane butterfly, inv = 1 / sqrt(ss / H
+// + eps), then x * inv * (1 + w) rounded to bf16 in place. Every wave of the
+// router does the same arithmetic, so all hold the same rows; wave 0 of
+// workgroup 0 writes them to xn_out.
+template <int TT, int NG>
+HX_DEV void rmsnorm_regs(const RouterArgs& a, uint32_t (&xr)[TT][NG][4], int t0) {
+  const int lane = lane_id(), H = a.H, G = H / 8;
+  float w[NG][8];
+#pragma unroll
+  for (int i = 0; i < NG; i++) {
+    const int g = min(lane + 64 * i, G - 1);
+    const float4 w0 = *(const float4*)(a.norm_w + 8 * g), w1 = *(const float4*)(a.norm_w + 8 * g + 4);
+    w[i][0] = w0.x; w[i][1] = w0.y; w[i][2] = w0.z; w[i][3] = w0.w;
+    w[i][4] = w1.x; w[i][5] = w1.y; w[i][6] = w1.z; w[i][7] = w1.w;
+  }
+  const bool writer = blockIdx.x == 0 && threadIdx.x < 64;
+#pragma unroll
+  for (int t = 0; t < TT; t++) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+      if (lane + 64 * i >= G) break;
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const float v = __uint_as_float(q & 1 ? xr[t][i][q / 2] & 0xffff0000u : xr[t][i][q / 2] << 16);
+        ss = __builtin_fmaf(v, v, ss);
+      }
+    }
+    ss = wave_sum<64>(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)H + a.eps);
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float lo = __uint_as_float(xr[t][i][q] << 16) * inv * (1.0f + w[i][2 * q]);
+        const float hi = __uint_as_float(xr[t][i][q] & 0xffff0000u) * inv * (1.0f + w[i][2 * q + 1]);
+        xr[t][i][q] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+      }
+      if (writer && t0 + t < a.T && lane + 64 * i < G)
+        *(uint4*)(a.xn_out + (int64_t)(t0 + t) * H + 8 * (lane + 64 * i)) =
+            make_uint4(xr[t][i][0], xr[t][i][1], xr[t][i][2], xr[t][i][3]);
+    }
+  }
+}
+
 // One wave: logits of tokens t0 .. t0+TT-1 for router rows e0 .. e0+TE-1, for
 // H % 8 == 0 and at most 64 * NG groups of 8. Every load of the wave is issued
 // before the first multiply-add (addresses are clamped into range and the
@@ -73,6 +120,9 @@ HX_DEV void router_rows_u(const RouterArgs& a, int e0, int t0) {
         xr[t][i][4 * q] = v.x; xr[t][i][4 * q + 1] = v.y; xr[t][i][4 * q + 2] = v.z; xr[t][i][4 * q + 3] = v.w;
       }
     }
+  }
+  if constexpr (XBF) {
+    if (a.norm_w) rmsnorm_regs<TT, NG>(a, xr, t0);
   }
   float acc[TT][TE];
 #pragma unroll
