@@ -58,7 +58,16 @@ HX_DEV void x_pairs_bf16(const uint16_t* p, uint32_t* out) {
   pairs_from_f16x8(h, out);
 }
 
-HX_DEV void x_pairs_f16(const uint16_t* p, uint32_t* out) { pairs_from_f16x8(*(const uint4*)p, out); }
+typedef const __attribute__((address_space(3))) uint16_t* lds_cu16;
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+HX_DEV uint4 ld16(const uint16_t* p) { return *(const uint4*)p; }
+HX_DEV uint4 ld16(lds_cu16 p) {
+  const u32x4v v = *(const __attribute__((address_space(3))) u32x4v*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+// 8 f16 at p (global or LDS) -> 4 pairs in weight-pair order
+template <class P>
+HX_DEV void x_pairs_f16(P p, uint32_t* out) { pairs_from_f16x8(ld16(p), out); }
 
 // 4 bytes b0..b3 (already offset to unsigned) -> f16 pairs (1024+b0, 1024+b2), (1024+b1, 1024+b3)
 HX_DEV uint32_t bytes02(uint32_t q) { return __builtin_amdgcn_perm(q, 0x64646464u, 0x00060004u); }
@@ -79,11 +88,11 @@ struct DChunk<HX_Q8_0> {
     Chunk<HX_Q8_0>::load(mat, R, K, row, c, r);
   }
   // activation positions: elements 32c .. 32c+31, pairs per 8
-  template <bool XF16>
-  HX_DEV static void load_x(const uint16_t* xrow, int c, uint32_t* xp, float* xs) {
+  template <bool XF16, class P = const uint16_t*>
+  HX_DEV static void load_x(P xrow, int c, uint32_t* xp, float* xs) {
 #pragma unroll
     for (int v = 0; v < 4; v++) {
-      if (XF16) x_pairs_f16(xrow + 32 * c + 8 * v, xp + 4 * v);
+      if constexpr (XF16) x_pairs_f16(xrow + 32 * c + 8 * v, xp + 4 * v);
       else x_pairs_bf16(xrow + 32 * c + 8 * v, xp + 4 * v);
     }
     float s = 0.f;
@@ -112,13 +121,13 @@ struct DChunk<HX_Q4_K> {
   HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
     Chunk<HX_Q4_K>::load(mat, R, K, row, c, r);
   }
-  template <bool XF16>
-  HX_DEV static void load_x(const uint16_t* xrow, int c, uint32_t* xp, float* xs) {
+  template <bool XF16, class P = const uint16_t*>
+  HX_DEV static void load_x(P xrow, int c, uint32_t* xp, float* xs) {
     const int sb = c >> 3, cc = c & 7, p = cc >> 1, h = cc & 1;
-    const uint16_t* lo = xrow + sb * 256 + 64 * p + 16 * h;
+    const auto lo = xrow + sb * 256 + 64 * p + 16 * h;
 #pragma unroll
     for (int v = 0; v < 2; v++) {
-      if (XF16) {
+      if constexpr (XF16) {
         x_pairs_f16(lo + 8 * v, xp + 4 * v);
         x_pairs_f16(lo + 32 + 8 * v, xp + 8 + 4 * v);
       } else {
@@ -163,13 +172,13 @@ struct DChunk<HX_Q6_K> {
   HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
     Chunk<HX_Q6_K>::load(mat, R, K, row, c, r);
   }
-  template <bool XF16>
-  HX_DEV static void load_x(const uint16_t* xrow, int c, uint32_t* xp, float* xs) {
+  template <bool XF16, class P = const uint16_t*>
+  HX_DEV static void load_x(P xrow, int c, uint32_t* xp, float* xs) {
     const int sb = c >> 3, cc = c & 7, n = cc >> 2, a = cc & 3;
-    const uint16_t* base = xrow + sb * 256 + 128 * n + 8 * a;
+    const auto base = xrow + sb * 256 + 128 * n + 8 * a;
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-      if (XF16) x_pairs_f16(base + 32 * s, xp + 4 * s);
+      if constexpr (XF16) x_pairs_f16(base + 32 * s, xp + 4 * s);
       else x_pairs_bf16(base + 32 * s, xp + 4 * s);
       float t = 0.f;
 #pragma unroll
@@ -234,7 +243,9 @@ HX_DEV void touch_sink(const ExpertArgs& a, Touch t) {
 }
 
 // NR (gate, up) row pairs of one expert for a list of tokens; h stored as f16
-template <int FMT, int LPR, int NR>
+// BATCH: tokens may come several at a time (the single-token kernel leaves the
+// batched path out, which keeps its register count and occupancy)
+template <int FMT, int LPR, int NR, bool BATCH = true>
 HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U, int rows, int row0, int count,
                          const int* tok, const int* hrow) {
   using D = DChunk<FMT>;
@@ -247,6 +258,38 @@ HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U
     if (row < rows) {
       D::load(G, rows, K, row, c, rgt[g]);
       D::load(U, rows, K, row, c, rup[g]);
+    }
+  }
+  if constexpr (BATCH && LPR == 64) {
+    if (count > 1) {
+      // tokens four at a time: every activation load of the batch first, then
+      // the 4 NR (gate, up) pairs of dot products, summed by one reduce-scatter
+      constexpr int TB = 4, M = TB * NR;
+      const int lane = lane_id();
+      for (int j0 = 0; j0 < count; j0 += TB) {
+        uint32_t xp[TB][D::NX];
+        float xs[TB][D::NS];
+#pragma unroll
+        for (int jj = 0; jj < TB; jj++) {
+          const int j = min(j0 + jj, count - 1);
+          D::template load_x<false>((const uint16_t*)a.x + (int64_t)tok[j] * K, c, xp[jj], xs[jj]);
+        }
+        float pg[M], pu[M];
+#pragma unroll
+        for (int jj = 0; jj < TB; jj++)
+#pragma unroll
+          for (int g = 0; g < NR; g++) {
+            const bool ok = row0 + g * RG < rows;
+            pg[jj * NR + g] = ok ? D::dot(rgt[g], xp[jj], xs[jj]) : 0.f;
+            pu[jj * NR + g] = ok ? D::dot(rup[g], xp[jj], xs[jj]) : 0.f;
+          }
+        rs_pairs64<M>(pg, pu);
+        constexpr int SH = M == 8 ? 3 : (M == 4 ? 4 : 5);
+        const int m = lane >> SH, jj = m / NR, g = m % NR, j = j0 + jj, row = row0 + g * RG;
+        if ((lane & ((1 << SH) - 1)) == 0 && j < count && row < rows)
+          ((_Float16*)a.hbf)[(int64_t)hrow[j] * a.hstride + row] = (_Float16)(siluf_(pg[0]) * pu[0]);
+      }
+      return;
     }
   }
   for (int j = 0; j < count; j++) {
@@ -322,7 +365,7 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
         tok[j] = j;
         hrow[j] = a.F + j;
       }
-      gate_up_rows<FMT, LPR, NR>(a, a.sgate.base, a.sup.base, a.Is, r0 + lane_id() / LPR, a.T, tok, hrow);
+      gate_up_rows<FMT, LPR, NR, false>(a, a.sgate.base, a.sup.base, a.Is, r0 + lane_id() / LPR, a.T, tok, hrow);
     }
   }
   if (publisher && blockIdx.x > 0) return;
@@ -341,7 +384,7 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
   }
   const int row0 = (blockIdx.x * 4 + wave) * (RG * NR) + lane_id() / LPR;
   if (row0 - lane_id() / LPR < a.I)
-    gate_up_rows<FMT, LPR, NR>(a, a.gate.mat(e), a.up.mat(e), a.I, row0, count, tok, hrow);
+    gate_up_rows<FMT, LPR, NR, false>(a, a.gate.mat(e), a.up.mat(e), a.I, row0, count, tok, hrow);
 }
 
 // ----------------------------------------------------------------------------
@@ -354,18 +397,21 @@ __global__ __launch_bounds__(256) void k_gate_up_plan(ExpertArgs a) {
   constexpr int RG = 64 / LPR;
   const int u = blockIdx.y;
   const int nslots = a.plan[0];
-  const int e = a.plan[4 + 4 * u], start = a.plan[4 + 4 * u + 1], count = a.plan[4 + 4 * u + 2];
+  const int4 sr = *(const int4*)(a.plan + 4 + 4 * u);   // expert, first row, rows, first row's token
+  const int e = sr.x, start = sr.y, count = sr.z;
   if (u >= nslots || e >= a.E) return;
   const int tok0 = 4 + 4 * a.max_slots;
   int tok[HX_DECODE_MAX_T], hrow[HX_DECODE_MAX_T];
-  for (int j = 0; j < count; j++) {
+  tok[0] = sr.w;
+  hrow[0] = start;
+  for (int j = 1; j < count; j++) {
     hrow[j] = start + j;
     tok[j] = a.plan[tok0 + start + j];
   }
   const int wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * 4 + wave) * (RG * NR) + lane_id() / LPR;
   if (row0 - lane_id() / LPR < a.I)
-    gate_up_rows<FMT, LPR, NR>(a, a.gate.mat(e), a.up.mat(e), a.I, row0, count, tok, hrow);
+    gate_up_rows<FMT, LPR, NR, false>(a, a.gate.mat(e), a.up.mat(e), a.I, row0, count, tok, hrow);
 }
 
 // ----------------------------------------------------------------------------
@@ -373,77 +419,114 @@ __global__ __launch_bounds__(256) void k_gate_up_plan(ExpertArgs a) {
 // contributions w * (row . h) go to LDS and are summed in slot order (experts
 // ascending, then the shared expert).
 // ----------------------------------------------------------------------------
-template <int FMT, int LPR, int SPW, int NW>
+// XLDS: the group's rows of h are staged in LDS first (many rows: each row of
+// h is read by every output-row block, and the activations then stay out of
+// the registers while the weight loads are in flight); otherwise (one token)
+// each wave loads its activations from global memory together with its weights,
+// which keeps the kernel to one memory round trip after the plan.
+template <int FMT, int LPR, int SPW, int NW, bool XLDS>
 __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
   using D = DChunk<FMT>;
   constexpr int RG = 64 / LPR;
-  extern __shared__ int32_t splan[];
-  load_plan(a, splan);
-  float* contrib = (float*)(splan + plan_ints(a.max_slots, a.F, a.T));
-  const int nslots = splan[0], T = a.T;
-  const int tok0 = 4 + 4 * a.max_slots, w0 = tok0 + a.F + a.T;
-  const int lane = lane_id(), wave = threadIdx.x >> 6, rg = lane / LPR, c = lane % LPR;
-  const int n0 = blockIdx.x * RG, row = n0 + rg;
-  for (int i = threadIdx.x; i < nslots * T * RG; i += 64 * NW) contrib[i] = 0.f;
-  __syncthreads();
-  for (int ub = wave; ub < nslots; ub += NW * SPW) {
-    // every load of the batch first: the SPW slots' weight chunks and the
-    // activations of each slot's first token
-    typename D::Raw raw[SPW];
-    uint32_t xp0[SPW][D::NX];
-    float xs0[SPW][D::NS];
-#pragma unroll
-    for (int s = 0; s < SPW; s++) {
-      const int u = ub + NW * s;
-      if (u < nslots) {
-        const int e = splan[4 + 4 * u], start = splan[4 + 4 * u + 1];
-        const bool sh = e == a.E;
-        const int K = sh ? a.Is : a.I;
-        if (row < a.H && c < K / 32) {
-          D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row, c, raw[s]);
-          D::template load_x<true>((const uint16_t*)a.hbf + (int64_t)start * a.hstride, c, xp0[s], xs0[s]);
-        }
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < SPW; s++) {
-      const int u = ub + NW * s;
-      if (u >= nslots) break;
-      const int e = splan[4 + 4 * u], start = splan[4 + 4 * u + 1], count = splan[4 + 4 * u + 2];
-      const bool sh = e == a.E;
-      const int K = sh ? a.Is : a.I;
-      for (int j = 0; j < count; j++) {
-        const int hrow = start + j, t = splan[tok0 + hrow];
-        const float wgt = __int_as_float(splan[w0 + hrow]);
-        float p = 0.f;
-        if (c < K / 32) {
-          if (j == 0) {
-            p = D::dot(raw[s], xp0[s], xs0[s]);
-          } else {
-            uint32_t xp[D::NX];
-            float xs[D::NS];
-            D::template load_x<true>((const uint16_t*)a.hbf + (int64_t)hrow * a.hstride, c, xp, xs);
-            p = D::dot(raw[s], xp, xs);
-          }
-        }
-        p = wave_sum<LPR>(p);
-        if (c == 0 && row < a.H) contrib[((int64_t)u * T + t) * RG + rg] = wgt * p;
+  static_assert(NW * SPW == HX_DOWN_ROWS, "one pass per wave over a group of rows of h");
+  // LDS: the group's rows of h (f16, Kmax each; XLDS only), then per row its
+  // token, weight and expert, then the contributions [HX_DOWN_ROWS][RG]
+  extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
+  const int Kmax = XLDS ? (a.I > a.Is ? a.I : a.Is) : 0;
+  int* stok = (int*)(xl + HX_DOWN_ROWS * Kmax);
+  float* swt = (float*)(stok + HX_DOWN_ROWS);
+  int* sexp = (int*)(swt + HX_DOWN_ROWS);
+  float* contrib = (float*)(sexp + HX_DOWN_ROWS);
+  const int T = a.T, NH = a.F + T;
+  const int nh_all = a.F + (a.Is > 0 ? T : 0);   // rows of h in use
+  const int h0 = blockIdx.y * HX_DOWN_ROWS;      // this workgroup's group of rows
+  const int nh = min(nh_all - h0, HX_DOWN_ROWS);
+  {
+    const int tok0 = 4 + 4 * a.max_slots + h0;
+    const int i = threadIdx.x;
+    if (i < nh) stok[i] = a.plan[tok0 + i];
+    else if (i >= 32 && i < 32 + nh) swt[i - 32] = __int_as_float(a.plan[tok0 + NH + i - 32]);
+    else if (i >= 64 && i < 64 + nh) sexp[i - 64] = a.plan[tok0 + 2 * NH + i - 64];
+    if constexpr (XLDS) {
+      // the group's rows of h, 16 bytes per thread and step
+      const int per_row = Kmax / 8, n16 = nh * per_row;
+      for (int q = threadIdx.x; q < n16; q += 64 * NW) {
+        const int r = q / per_row, o = q - r * per_row;
+        *(uint4*)(xl + r * Kmax + 8 * o) = *(const uint4*)(a.hbf + (int64_t)(h0 + r) * a.hstride + 8 * o);
       }
     }
   }
   __syncthreads();
+  const int lane = lane_id(), wave = threadIdx.x >> 6, rg = lane / LPR, c = lane % LPR;
+  const int n0 = blockIdx.x * RG, row = n0 + rg;
+  // every weight load of the wave first (SPW rows of h), then the dot products
+  // with the activations from LDS
+  typename D::Raw raw[SPW];
+  uint32_t xpg[XLDS ? 1 : SPW][D::NX];
+  float xsg[XLDS ? 1 : SPW][D::NS];
+#pragma unroll
+  for (int s = 0; s < SPW; s++) {
+    const int hr = wave + NW * s;
+    if (hr < nh) {
+      const int e = sexp[hr];
+      const bool sh = e == a.E;
+      const int K = sh ? a.Is : a.I;
+      if (row < a.H && c < K / 32) {
+        D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row, c, raw[s]);
+        if constexpr (!XLDS)
+          D::template load_x<true>((const uint16_t*)a.hbf + (int64_t)(h0 + hr) * a.hstride, c, xpg[s], xsg[s]);
+      }
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < SPW; s++) {
+    const int hr = wave + NW * s;
+    if (hr >= nh) break;
+    const int K = sexp[hr] == a.E ? a.Is : a.I;
+    float p = 0.f;
+    if (c < K / 32) {
+      if constexpr (XLDS) {
+        uint32_t xp[D::NX];
+        float xs[D::NS];
+        D::template load_x<true>((lds_cu16)(xl + hr * Kmax), c, xp, xs);
+        p = D::dot(raw[s], xp, xs);
+      } else {
+        p = D::dot(raw[s], xpg[s], xsg[s]);
+      }
+    }
+    p = wave_sum<LPR>(p);
+    if (c == 0 && row < a.H) contrib[hr * RG + rg] = swt[hr] * p;
+  }
+  __syncthreads();
+  // token t's output: its rows of h in order (slots by ascending expert, then
+  // the shared expert), as the reference's combine order; with several groups,
+  // the group's partial sum, which k_down_reduce adds up in group order
   for (int i = threadIdx.x; i < T * RG; i += 64 * NW) {
     const int t = i / RG, r = i % RG;
     if (n0 + r >= a.H) continue;
     float y = 0.f;
-    for (int u = 0; u < nslots; u++) y += contrib[((int64_t)u * T + t) * RG + r];
-    if (a.resid) {
+    for (int hr = 0; hr < nh; hr++)
+      if (stok[hr] == t) y += contrib[hr * RG + r];
+    if (gridDim.y > 1) {
+      a.dpart[((int64_t)blockIdx.y * T + t) * a.H + n0 + r] = y;
+    } else if (a.resid) {
       uint16_t* px = a.resid + (int64_t)t * a.H + n0 + r;
       *px = f32_to_bf16(bf16_to_f32(*px) + bf16_to_f32(f32_to_bf16(y)));
     } else {
       ((uint16_t*)a.y)[(int64_t)t * a.H + n0 + r] = f32_to_bf16(y);
     }
   }
+}
+
+// sum of the down kernel's per-group partials, in group order, for T tokens
+__global__ __launch_bounds__(256) void k_down_reduce(ExpertArgs a, int groups) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)a.T * a.H) return;
+  const int64_t TH = (int64_t)a.T * a.H;
+  float y = 0.f;
+  for (int g = 0; g < groups; g++) y += a.dpart[g * TH + i];
+  if (a.resid) a.resid[i] = f32_to_bf16(bf16_to_f32(a.resid[i]) + bf16_to_f32(f32_to_bf16(y)));
+  else ((uint16_t*)a.y)[i] = f32_to_bf16(y);
 }
 
 // ----------------------------------------------------------------------------
@@ -511,15 +594,21 @@ static hipError_t gate_up_plan_fmt(const ExpertArgs& a, hipStream_t s) {
 template <int FMT>
 static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
   const int nch = (a.I > a.Is ? a.I : a.Is) / 32;
+  const int groups = down_groups(a.F, a.Is > 0 ? a.T : 0);
+  const bool xlds = a.T > 1;   // one token: activations straight from global memory
 #define DD(LPR)                                                                                   \
   {                                                                                               \
     constexpr int RG = 64 / LPR;                                                                  \
-    size_t lds = sizeof(int32_t) * plan_ints(a.max_slots, a.F, a.T) +                              \
-                 (size_t)a.max_slots * a.T * RG * sizeof(float);                                  \
-    hipLaunchKernelGGL((k_down_dec<FMT, LPR, 3, 4>), dim3((a.H + RG - 1) / RG), dim3(256), lds, s, a); \
+    const int Kmax = xlds ? (a.I > a.Is ? a.I : a.Is) : 0;                                        \
+    size_t lds = (size_t)HX_DOWN_ROWS * Kmax * 2 + (size_t)HX_DOWN_ROWS * (3 + RG) * 4;           \
+    const dim3 grid((a.H + RG - 1) / RG, groups);                                                   \
+    if (xlds) hipLaunchKernelGGL((k_down_dec<FMT, LPR, 6, 4, true>), grid, dim3(256), lds, s, a);   \
+    else hipLaunchKernelGGL((k_down_dec<FMT, LPR, 6, 4, false>), grid, dim3(256), lds, s, a);       \
   }
   if (nch == 64) DD(64) else if (nch == 32) DD(32) else DD(16)
 #undef DD
+  if (groups > 1)
+    hipLaunchKernelGGL(k_down_reduce, dim3((unsigned)(((int64_t)a.T * a.H + 255) / 256)), dim3(256), 0, s, a, groups);
   return hipGetLastError();
 }
 

@@ -149,6 +149,75 @@ HX_DEV float wave_sum(float v) {
   return v;
 }
 
+// One step of the butterfly over lane ^ OFF (OFF a power of two <= 32).
+// rs_keep: a lane keeps the sum of lo (lane bit clear) or hi (bit set) with
+// its partner's copy of the same value; bf_add: v + partner's v. Exact xor
+// partners throughout (lane ^ 4 via row_ror:12 or :4 by bit 2).
+template <int OFF>
+HX_DEV float rs_keep(float lo, float hi) {
+  const int l = __lane_id();
+  if (OFF == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else if (OFF == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else if (OFF == 8) {
+    const float s1 = lo + dpp_f<0x128>(lo), s2 = hi + dpp_f<0x128>(hi);
+    return (l & 8) ? s2 : s1;
+  } else if (OFF == 4) {
+    const float s1 = lo + dpp_f<0x12C>(lo), s2 = hi + dpp_f<0x124>(hi);
+    return (l & 4) ? s2 : s1;
+  } else if (OFF == 2) {
+    const float s1 = lo + dpp_f<0x4E>(lo), s2 = hi + dpp_f<0x4E>(hi);
+    return (l & 2) ? s2 : s1;
+  } else {
+    const float s1 = lo + dpp_f<0xB1>(lo), s2 = hi + dpp_f<0xB1>(hi);
+    return (l & 1) ? s2 : s1;
+  }
+}
+template <int OFF>
+HX_DEV float bf_add(float v) {
+  const int l = __lane_id();
+  if (OFF == 32 || OFF == 16) {
+    const auto r = OFF == 32 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false)
+                             : __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else if (OFF == 8) {
+    return v + dpp_f<0x128>(v);
+  } else if (OFF == 4) {
+    // both reads with the whole wave active (a DPP read of a lane that is off
+    // in the current exec mask yields 0), then the select
+    const float a = dpp_f<0x124>(v), b = dpp_f<0x12C>(v);
+    return v + ((l & 4) ? a : b);
+  } else if (OFF == 2) {
+    return v + dpp_f<0x4E>(v);
+  } else {
+    return v + dpp_f<0xB1>(v);
+  }
+}
+
+// Wave-wide sums of M (gate, up) pairs (M a power of two <= 64): the first
+// log2 M steps of the butterfly are a reduce-scatter over the pairs, the rest
+// plain butterfly steps; lane l ends with the sums of pair l >> (6 - log2 M).
+template <int M, int STEP = 0>
+HX_DEV void rs_pairs64(float* g, float* u) {
+  if constexpr (STEP < 6) {
+    constexpr int OFF = 32 >> STEP, LIVE = M >> STEP;
+    if constexpr (LIVE >= 2) {
+#pragma unroll
+      for (int k = 0; k < LIVE / 2; k++) {
+        g[k] = rs_keep<OFF>(g[k], g[k + LIVE / 2]);
+        u[k] = rs_keep<OFF>(u[k], u[k + LIVE / 2]);
+      }
+    } else {
+      g[0] = bf_add<OFF>(g[0]);
+      u[0] = bf_add<OFF>(u[0]);
+    }
+    rs_pairs64<M, STEP + 1>(g, u);
+  }
+}
+
 // The butterfly of wave_sum<64> applied to 64 values at once, as a
 // reduce-scatter: at each step a lane adds its partner's copy of only the half
 // of its live values it keeps (the half selected by the lane's bit for that

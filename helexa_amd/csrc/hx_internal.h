@@ -47,7 +47,10 @@ __host__ __device__ inline int dispatch_blocks(int F) { return (F + HX_DISPATCH_
 //   [4 + 4u + {0,1,2}]          slot u: expert (E = shared), start position, count
 //   [4 + 4*max_slots + p]       token of permuted position p (p < F + T; shared: F + t)
 //   [4 + 4*max_slots + F+T + p] routing weight of position p (f32 bits)
-__host__ __device__ inline int plan_ints(int max_slots, int F, int T) { return 4 + 4 * max_slots + 2 * (F + T); }
+// decode plan: [0] slots used; [4 + 4u ..] slot u's (expert, first row, row count);
+// then per row of h (routed rows in dispatch order, then the shared expert's T
+// rows): token, weight bits, expert (E for the shared expert)
+__host__ __device__ inline int plan_ints(int max_slots, int F, int T) { return 4 + 4 * max_slots + 3 * (F + T); }
 
 struct RouterArgs {
   const void* x;       // [T, H] act dtype
@@ -105,7 +108,14 @@ struct ExpertArgs {
   // decoder residual folded into the decode down kernel: resid[t] becomes
   // bf16(resid[t] + bf16(y[t])) in place of writing y (bf16 activations)
   uint16_t* resid = nullptr;
+  // decode down partial sums [groups of HX_DOWN_ROWS rows of h][T][H] when the
+  // rows of h take more than one group
+  float* dpart = nullptr;
 };
+
+// rows of h one decode down workgroup takes (4 waves x 6 rows each)
+constexpr int HX_DOWN_ROWS = 24;
+__host__ __device__ inline int down_groups(int F, int T) { return (F + T + HX_DOWN_ROWS - 1) / HX_DOWN_ROWS; }
 
 void launch_router(const RouterArgs& a, bool xbf, bool rbf, hipStream_t s);
 void launch_route_small(const RouterArgs& a, hipStream_t s);   // T <= HX_DECODE_MAX_T, one workgroup

@@ -73,7 +73,8 @@ struct hx_moe {
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct WsLayout {
-  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, hist, hbuf, hbf, xh, obuf, xn, ym, total;
+  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, hist, hbuf, hbf, xh, obuf, xn, ym, dpart,
+      total;
   int hstride, max_slots, max_tiles;
 };
 
@@ -111,6 +112,7 @@ static WsLayout ws_layout(const hx_moe* m, int64_t T) {
   L.xh = decode ? 0 : take(sizeof(uint16_t) * T * H);
   L.xn = take(act * T * H);
   L.ym = take(act * T * H);
+  L.dpart = decode ? take(sizeof(float) * (size_t)down_groups((int)F, (int)T) * T * H) : 0;
   L.total = o;
   return L;
 }
@@ -387,6 +389,7 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
   a.max_slots = L.max_slots;
   a.max_tiles = L.max_tiles;
   a.plan = d.plan;
+  a.dpart = L.dpart ? (float*)(ws + L.dpart) : nullptr;
 }
 
 // event helpers for the optional per-kernel timing
