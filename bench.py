@@ -59,9 +59,12 @@ def gguf_bytes(fmt, rows, cols):
 def step_bytes(cfg, fmts, unique_experts, T):
     """Algorithmic HBM bytes of one decode forward (every touched weight byte once,
     the tokens in and out once), in total and per kernel of the decode path:
-      router  -- router rows + shared-expert gate row (bf16), the shared expert's
-                 gate/up projections, the tokens;
-      gate_up -- the routed experts' gate/up projections, the tokens;
+      router  -- router rows + shared-expert gate row (bf16), the tokens (and,
+                 for T > 1, the shared expert's gate/up projections, which that
+                 kernel computes);
+      gate_up -- the routed experts' gate/up projections (and, for T = 1, the
+                 shared expert's, which the single-token kernel computes while
+                 it routes), the tokens;
       down    -- the routed and shared down projections, the output rows.
     The SwiGLU activations passed between kernels are intermediates and are not
     counted."""
@@ -72,7 +75,9 @@ def step_bytes(cfg, fmts, unique_experts, T):
     routed_gu = unique_experts * (gguf_bytes(fmts["gate"], I, H) + gguf_bytes(fmts["up"], I, H))
     down_w = unique_experts * gguf_bytes(fmts["down"], H, I) + gguf_bytes(fmts["sdown"], H, Is)
     total = router_w + shared_gu + routed_gu + down_w + 2 * act
-    return total, {"router": router_w + shared_gu + act, "gate_up": routed_gu + act, "down": down_w + act}
+    sg_router, sg_gate_up = (0, shared_gu) if T == 1 else (shared_gu, 0)
+    return total, {"router": router_w + sg_router + act, "gate_up": routed_gu + sg_gate_up + act,
+                   "down": down_w + act}
 
 
 def build_layers(cfg, fmts, n_layers, seed, keep_host_copy_of_first=False):

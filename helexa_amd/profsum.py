@@ -3,6 +3,7 @@
     python -m helexa_amd.profsum stats  <kernel_stats.csv> <out.txt> <title> <command>
     python -m helexa_amd.profsum pmc    <fetch_counter_collection.csv> <write_counter_collection.csv>
                                         <out.txt> <title> <command-fetch> <command-write> <copy_bytes>
+                                        [<calibration fetch csv> <calibration write csv>]
 
 `stats` keeps the library's kernels (names starting with "hx::" or "void hx::")
 from a `--kernel-trace --stats` run: calls, average / min / max duration.
@@ -61,24 +62,34 @@ def _counter_values(path: str, counter: str):
     return vals
 
 
+def _rel(path: str) -> str:
+    return os.path.join(os.path.basename(os.path.dirname(path)), os.path.basename(path))
+
+
 def _means(vals):
     return {k: (sum(v) / len(v), len(v)) for k, v in vals.items()}
 
 
 def pmc(fetch_csv: str, write_csv: str, out_path: str, title: str, cmd_fetch: str, cmd_write: str,
-        copy_bytes: int) -> str:
+        copy_bytes: int, calib_fetch_csv: str = None, calib_write_csv: str = None) -> str:
+    """calib_*_csv: counter runs that hold the copy_bytes calibration copy when
+    the measured runs do not (default: the measured runs themselves)"""
     fv = _counter_values(fetch_csv, "FETCH_SIZE")
     wv = _counter_values(write_csv, "WRITE_SIZE")
     fe, wr = _means(fv), _means(wv)
+    cfv = _counter_values(calib_fetch_csv, "FETCH_SIZE") if calib_fetch_csv else fv
+    cwv = _counter_values(calib_write_csv, "WRITE_SIZE") if calib_write_csv else wv
     # the calibration copies are the largest copy-kernel dispatches of the run
-    cf = max((x for k, v in fv.items() if COPY_KERNEL in k for x in v), default=None)
-    cw = max((x for k, v in wv.items() if COPY_KERNEL in k for x in v), default=None)
+    cf = max((x for k, v in cfv.items() if COPY_KERNEL in k for x in v), default=None)
+    cw = max((x for k, v in cwv.items() if COPY_KERNEL in k for x in v), default=None)
     if not cf or not cw:
         raise RuntimeError("no copy-kernel dispatch in the counter runs")
     kf = copy_bytes / (cf * 1024.0)
     kw = copy_bytes / (cw * 1024.0)
     lines = [f"# {title}", "", f"command (fetch): {cmd_fetch}", f"command (write): {cmd_write}",
              "($REPO is the repository root)", "",
+             (f"calibration runs: {_rel(calib_fetch_csv)} and {_rel(calib_write_csv)} (the same two counters "
+              "over bench.py --probe, which runs the copy)" if calib_fetch_csv else "calibration: the same runs"),
              f"calibration: {COPY_KERNEL} copying {copy_bytes} bytes reads FETCH_SIZE {cf:.1f} KiB and "
              f"WRITE_SIZE {cw:.1f} KiB per dispatch -> factors fetch {kf:.4f}, write {kw:.4f} "
              f"(HBM bytes = counter KiB * 1024 * factor)", "",
@@ -116,6 +127,6 @@ if __name__ == "__main__":
     if sys.argv[1] == "stats":
         print(stats(*sys.argv[2:6]))
     elif sys.argv[1] == "pmc":
-        print(pmc(*sys.argv[2:8], int(sys.argv[8])))
+        print(pmc(*sys.argv[2:8], int(sys.argv[8]), *sys.argv[9:11]))
     else:
         raise SystemExit(__doc__)
