@@ -448,7 +448,8 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
     else if (i >= 32 && i < 32 + nh) swt[i - 32] = __int_as_float(a.plan[tok0 + NH + i - 32]);
     else if (i >= 64 && i < 64 + nh) sexp[i - 64] = a.plan[tok0 + 2 * NH + i - 64];
     if constexpr (XLDS) {
-      // the group's rows of h, 16 bytes per thread and step
+      // the group's rows of h, 16 bytes per thread and step (measured: batching
+      // these loads per thread raised the register count and slowed the kernel)
       const int per_row = Kmax / 8, n16 = nh * per_row;
       for (int q = threadIdx.x; q < n16; q += 64 * NW) {
         const int r = q / per_row, o = q - r * per_row;

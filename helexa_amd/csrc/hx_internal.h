@@ -35,6 +35,11 @@ struct DispatchArgs {
   int32_t* plan;       // decode plan (written by the decode routing tail), see plan_ints()
   int max_slots;
   int32_t* hist;       // [dispatch_blocks(F)][E] per-block expert counts (multi-block dispatch)
+  // prefill: routing weight by permuted position, wpos[p] = topk_w[perm[p]],
+  // and the shared expert's sigmoid gate at wpos[F + t]
+  const float* topk_w = nullptr;
+  const float* sgw = nullptr;
+  float* wpos = nullptr;
 };
 
 // Multi-block dispatch: entries per block and block count.
@@ -47,6 +52,7 @@ __host__ __device__ inline int dispatch_blocks(int F) { return (F + HX_DISPATCH_
 //   [4 + 4u + {0,1,2}]          slot u: expert (E = shared), start position, count
 //   [4 + 4*max_slots + p]       token of permuted position p (p < F + T; shared: F + t)
 //   [4 + 4*max_slots + F+T + p] routing weight of position p (f32 bits)
+//   [4 + 4*max_slots + 2(F+T) + p] expert of position p (E for the shared rows)
 // decode plan: [0] slots used; [4 + 4u ..] slot u's (expert, first row, row count);
 // then per row of h (routed rows in dispatch order, then the shared expert's T
 // rows): token, weight bits, expert (E for the shared expert)
@@ -108,6 +114,7 @@ struct ExpertArgs {
   // decoder residual folded into the decode down kernel: resid[t] becomes
   // bf16(resid[t] + bf16(y[t])) in place of writing y (bf16 activations)
   uint16_t* resid = nullptr;
+  const float* wpos = nullptr;   // prefill: routing weight by permuted position (see DispatchArgs)
   // decode down partial sums [groups of HX_DOWN_ROWS rows of h][T][H] when the
   // rows of h take more than one group
   float* dpart = nullptr;

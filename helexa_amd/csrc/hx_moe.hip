@@ -74,7 +74,7 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct WsLayout {
   size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, hist, hbuf, hbf, xh, obuf, xn, ym, dpart,
-      total;
+      wpos, total;
   int hstride, max_slots, max_tiles;
 };
 
@@ -113,6 +113,7 @@ static WsLayout ws_layout(const hx_moe* m, int64_t T) {
   L.xn = take(act * T * H);
   L.ym = take(act * T * H);
   L.dpart = decode ? take(sizeof(float) * (size_t)down_groups((int)F, (int)T) * T * H) : 0;
+  L.wpos = decode ? 0 : take(sizeof(float) * (F + T));
   L.total = o;
   return L;
 }
@@ -364,6 +365,9 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
   d.plan = (int32_t*)(ws + L.plan);
   d.max_slots = L.max_slots;
   d.hist = L.hist ? (int32_t*)(ws + L.hist) : nullptr;
+  d.topk_w = r.topk_w;
+  d.sgw = r.sgw;
+  d.wpos = L.wpos ? (float*)(ws + L.wpos) : nullptr;
   ExpertArgs& a = p.ea;
   a = ExpertArgs{};
   a.gate = m->gate; a.up = m->up; a.down = m->down;
@@ -390,6 +394,7 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
   a.max_tiles = L.max_tiles;
   a.plan = d.plan;
   a.dpart = L.dpart ? (float*)(ws + L.dpart) : nullptr;
+  a.wpos = d.wpos;
 }
 
 // event helpers for the optional per-kernel timing

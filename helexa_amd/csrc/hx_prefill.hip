@@ -471,17 +471,225 @@ __global__ __launch_bounds__(64 * NW, (Q4k<FPW, NW>::NST == 3 ? 2 : 1)) void k_g
     if (kc & 1) q4k_compute<Q, 1>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
     else q4k_compute<Q, 0>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
   }
+  // the 64 x COLS f16 tile of h goes through LDS (columns in the swizzled
+  // order, row pitch COLS + 8) and out as 16-byte pieces
+  __syncthreads();   // every wave is done with the ring
+  constexpr int OP = Q::COLS + 8;
+  _Float16* ot = (_Float16*)ring;
 #pragma unroll
   for (int j = 0; j < FPW; j++) {
-    const int col = swz(n0 + 16 * (FPW * wave + j) + l16);
+    const int col = swz(16 * (FPW * wave + j) + l16);
 #pragma unroll
     for (int mt = 0; mt < 4; mt++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int m = 16 * mt + 4 * kq + i;
-        if (m < rows)
-          ((_Float16*)a.hbf)[(int64_t)(p0 + m) * a.hstride + col] = (_Float16)(siluf_(accg[mt][j][i]) * accu[mt][j][i]);
+        ot[m * OP + col] = (_Float16)(siluf_(accg[mt][j][i]) * accu[mt][j][i]);
       }
+  }
+  __syncthreads();
+  constexpr int PER_ROW = Q::COLS / 8;
+  for (int q = threadIdx.x; q < PM * PER_ROW; q += Q::NT) {
+    const int m = q / PER_ROW, c8 = (q % PER_ROW) * 8;
+    if (m < rows) *(uint4*)(a.hbf + (int64_t)(p0 + m) * a.hstride + n0 + c8) = *(const uint4*)(ot + m * OP + c8);
+  }
+}
+
+// ---------------------------------------------------------------- Q6_K down, streamed
+// k_down_q6k: h . W_d^T for Q6_K down projections with K = I = 512, the
+// operands streamed into LDS by global_load_lds_{dwordx4,dword} through a
+// 3-stage ring, two chunks ahead (3 workgroups per CU: about 100 KB in flight
+// per CU). Tile: 64 rows of h (contiguous in the dispatch order, f16, K
+// swizzled as the gate/up epilogue wrote it) x 128 output columns; wave w owns
+// columns 32w .. 32w + 31 (two B fragments).
+// K chunk c (8 per row) = the quarters {p, p + 2} (p = c & 1) of half
+// n = (c >> 1) & 1 of superblock c >> 2: those two quarters share their ql
+// bytes (low and high nibbles) and the half's qh bytes, so a chunk needs per
+// weight row 32 ql + 32 qh bytes, with the half's 8 scales beside them.
+//   stage: A = 64 rows x 64 K (8 KB; the row's 8 16-byte pieces stored at
+//          slot piece ^ (row % 8)); B = 64 B per weight row; S = 8 B per row;
+//   once per tile: d of both superblocks of each weight row (4 B).
+// Dequantisation in registers: q = ql nibble | (qh bits << 4) under the 0x6400
+// f16 pattern (1024 + q, exact), (x - 1056) * (d * sc) with packed f16 ops.
+// Rows are scaled by their routing weight by position (the shared expert's
+// rows by its sigmoid gate) and written as bf16 to the per-assignment rows.
+constexpr int DQ_A = PM * 64 * 2;
+constexpr int DQ_BROW = 64;
+constexpr int DQ_B = 128 * DQ_BROW;
+constexpr int DQ_S = 128 * 8;
+constexpr int DQ_STAGE = DQ_A + DQ_B + DQ_S;
+constexpr int DQ_NST = 3;
+constexpr int DQ_K = 512;
+constexpr int DQ_NC = DQ_K / 64;
+
+HX_DEV void dma4(const void* g, uint32_t lds_base) {
+  uint32_t save;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(save) : "v"(g), "s"(lds_base) : "memory");
+}
+
+// first K column of chunk c: 256 (c >> 2) + 128 ((c >> 1) & 1) + 32 (c & 1)
+HX_DEV int dq_col(int c) { return 256 * (c >> 2) + 128 * ((c >> 1) & 1) + 32 * (c & 1); }
+
+// Per-thread DMA sources of chunk 0. Chunk c adds 2 dq_col(c) bytes to the A
+// sources, dq_col(c) / 2 (the ql offset 128 sb + 64 n + 32 p) to ql pieces,
+// 64 sb + 32 n to qh pieces and 16 sb + 8 n to the scales.
+// A piece q = 256 i + t: row q / 8, slot q % 8 holding segment
+// (q % 8) ^ (row % 8): segments 0..3 are K columns 8 s .. of quarter p, 4..7 of
+// quarter p + 2 (64 columns further). B piece q = 256 i + t: part q % 4 of
+// weight row q / 4 (ql bytes 16 part for parts 0, 1; qh bytes 16 (part - 2)).
+// Scale dword t: row t / 2, half t % 2.
+struct DqSrc {
+  const uint8_t* a[2];
+  const uint8_t* b[2];
+  const uint8_t* s;
+  uint32_t bqh;   // bit i: b[i] is a qh piece
+};
+
+HX_DEV DqSrc dq_sources(const uint16_t* hbf, int hstride, int p0, int rows, const uint8_t* W, int R, int n0) {
+  const int tid = threadIdx.x;
+  DqSrc src;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int q = i * 256 + tid, row = q >> 3, seg = (q & 7) ^ (row & 7);
+    const int r = min(row, rows - 1);   // padding rows repeat the last row
+    src.a[i] = (const uint8_t*)(hbf + (int64_t)(p0 + r) * hstride + 64 * (seg >> 2) + 8 * (seg & 3));
+  }
+  const uint8_t* ql = W;
+  const uint8_t* qh = W + (int64_t)R * (DQ_K / 2);
+  const uint8_t* sc = W + (int64_t)R * (DQ_K / 2 + DQ_K / 4);
+  src.bqh = 0;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int q = i * 256 + tid, row = q >> 2, part = q & 3;
+    src.b[i] = part < 2 ? ql + (int64_t)(n0 + row) * (DQ_K / 2) + 16 * part
+                        : qh + (int64_t)(n0 + row) * (DQ_K / 4) + 16 * (part - 2);
+    src.bqh |= (part >= 2 ? 1u : 0u) << i;
+  }
+  src.s = sc + (int64_t)(n0 + (tid >> 1)) * (DQ_K / 16) + 4 * (tid & 1);
+  return src;
+}
+
+// 5 DMA instructions per wave and chunk
+HX_DEV void dq_issue(uint32_t lds0, int st, const DqSrc& src, int c, int wave_u) {
+  const uint32_t sbase = lds0 + (uint32_t)(st * DQ_STAGE);
+  const int sb = c >> 2, n = (c >> 1) & 1;
+  const int aoff = 2 * dq_col(c), qloff = 128 * sb + 64 * n + 32 * (c & 1), qhoff = 64 * sb + 32 * n;
+#pragma unroll
+  for (int i = 0; i < 2; i++) dma16(src.a[i] + aoff, sbase + (uint32_t)(i * 4096 + wave_u * 1024));
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+    dma16(src.b[i] + ((src.bqh >> i) & 1 ? qhoff : qloff), sbase + (uint32_t)(DQ_A + i * 4096 + wave_u * 1024));
+  dma4(src.s + 16 * sb + 8 * n, sbase + (uint32_t)(DQ_A + DQ_B + wave_u * 256));
+}
+
+// (lo4 & 0x000F000F) | 0x64006400 | (hi2 & 0x00300030): two 6-bit codes as 1024 + q
+HX_DEV uint32_t q6_pair(uint32_t lo4, uint32_t hi2, uint32_t knib, uint32_t kmagic, uint32_t k30) {
+  return and_or(hi2, k30, and_or(lo4, knib, kmagic));
+}
+
+template <int P>   // chunk parity: quarters P and P + 2 of the half
+HX_DEV void dq_compute(const lds_u8* st, const uint16_t* dl, int sb, f32x4_t (*acc)[4], int wave, int l16, int kq,
+                       uint32_t knib, uint32_t kmagic, uint32_t k30) {
+  const h2_t off = h2s(-1056.0f);
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int brow = 32 * wave + 16 * j + l16;
+    const lds_u8* B = st + DQ_A + brow * DQ_BROW;
+    const uint2 ql = lds_ld8(B + 8 * kq), qh = lds_ld8(B + 32 + 8 * kq);
+    const uint2 sc = lds_ld8(st + DQ_A + DQ_B + brow * 8);
+    const float d = f16_to_f32(dl[2 * brow + sb]);
+    const int sh = 8 * (kq >> 1);
+#pragma unroll
+    for (int t = 0; t < 2; t++) {   // MFMA step t: quarter q = P + 2 t, ql nibble t
+      constexpr int Q0 = P;
+      const int q = Q0 + 2 * t;
+      const uint32_t sw = q < 2 ? sc.x : sc.y;   // scale 2 q + kq / 2 of the half
+      const h2_t a = h2s(d * (float)(int8_t)((sw >> (16 * (q & 1) + sh)) & 0xffu));
+      const uint32_t wx = ql.x >> (4 * t), wy = ql.y >> (4 * t);
+      const uint32_t hx_ = q < 3 ? qh.x << (4 - 2 * q) : qh.x >> 2, hy = q < 3 ? qh.y << (4 - 2 * q) : qh.y >> 2;
+      const f16x8_t bf = __builtin_bit_cast(
+          f16x8_t, make_uint4(u32((h2(q6_pair(wx, hx_, knib, kmagic, k30)) + off) * a),
+                              u32((h2(q6_pair(wx >> 8, hx_ >> 8, knib, kmagic, k30)) + off) * a),
+                              u32((h2(q6_pair(wy, hy, knib, kmagic, k30)) + off) * a),
+                              u32((h2(q6_pair(wy >> 8, hy >> 8, knib, kmagic, k30)) + off) * a)));
+#pragma unroll
+      for (int mt = 0; mt < 4; mt++) {
+        const int row = 16 * mt + l16, seg = 4 * t + kq;
+        const f16x8_t av = __builtin_bit_cast(
+            f16x8_t, *(const __attribute__((address_space(3))) u32x4_t*)(st + row * 128 + ((seg ^ (l16 & 7)) << 4)));
+        acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf, acc[j][mt], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// grid (H / 128, tiles rounded up to 8), mapped by xcd_tile
+__global__ __launch_bounds__(256, 3) void k_down_q6k(ExpertArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t ring[DQ_NST * DQ_STAGE + 128 * 4];
+  __shared__ float rws[PM];
+  int nt, tile;
+  xcd_tile(nt, tile);
+  if (tile >= a.counts[1]) return;
+  const int e = a.tiles[4 * tile + 1], p0 = a.tiles[4 * tile + 2], rows = a.tiles[4 * tile + 3];
+  const bool sh = e == a.E;
+  const int n0 = nt * 128;
+  const uint8_t* W = sh ? a.sdown.base : a.down.mat(e);
+  const int lane = lane_id(), wave = threadIdx.x >> 6, l16 = lane & 15, kq = lane >> 4;
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  // routing weights, loaded before the DMAs and first used after the last one
+  const float rw = threadIdx.x < PM ? a.wpos[p0 + min((int)threadIdx.x, rows - 1)] : 0.f;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)ring;
+  const uint16_t* dl = (const uint16_t*)(ring + DQ_NST * DQ_STAGE);
+  // d of both superblocks of the 128 weight rows (waves 0 and 1, one dword each)
+  if (wave_u < 2)
+    dma4(W + (int64_t)a.H * (DQ_K / 2 + DQ_K / 4 + DQ_K / 16) + (int64_t)(n0 + 64 * wave_u + lane) * 4,
+         lds0 + (uint32_t)(DQ_NST * DQ_STAGE + wave_u * 256));
+  const DqSrc src = dq_sources(a.hbf, a.hstride, p0, rows, W, a.H, n0);
+#pragma unroll
+  for (int c = 0; c < DQ_NST - 1; c++) dq_issue(lds0, c, src, c, wave_u);
+  const uint32_t knib = __builtin_amdgcn_readfirstlane(0x000F000Fu), k30 = __builtin_amdgcn_readfirstlane(0x00300030u);
+  uint32_t kmagic;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(kmagic));
+  f32x4_t acc[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int i = 0; i < 4; i++) acc[j][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < DQ_NC; c++) {
+    // chunk c (and, before chunk 0, the d dwords) has landed once at most the
+    // 5 DMAs of chunk c + 1 are outstanding
+    if (c + 1 < DQ_NC) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();   // chunk c is in LDS for every wave; stage (c - 1) % NST is free
+    if (c + DQ_NST - 1 < DQ_NC) dq_issue(lds0, (c + DQ_NST - 1) % DQ_NST, src, c + DQ_NST - 1, wave_u);
+    const lds_u8* st = (const lds_u8*)ring + (c % DQ_NST) * DQ_STAGE;
+    if (c & 1) dq_compute<1>(st, dl, c >> 2, acc, wave, l16, kq, knib, kmagic, k30);
+    else dq_compute<0>(st, dl, c >> 2, acc, wave, l16, kq, knib, kmagic, k30);
+  }
+  if (threadIdx.x < PM) rws[threadIdx.x] = rw;
+  __syncthreads();   // also: every wave is done with the ring
+  // the 64 x 128 bf16 output tile goes through LDS (row pitch 272 B, so the
+  // 16 lanes of a row group write different banks) and out as 16-byte pieces
+  constexpr int OP = 136;   // pitch in bf16
+  uint16_t* ot = (uint16_t*)ring;
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int col = 32 * wave + 16 * j + l16;
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int m = 16 * mt + 4 * kq + i;
+        ot[m * OP + col] = f32_to_bf16(rws[m] * acc[j][mt][i]);
+      }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int q = i * 256 + threadIdx.x, m = q >> 4, c8 = (q & 15) * 8;
+    if (m < rows)
+      *(uint4*)((uint16_t*)a.obuf + (int64_t)(p0 + m) * a.H + n0 + c8) = *(const uint4*)(ot + m * OP + c8);
   }
 }
 
@@ -674,7 +882,10 @@ hipError_t launch_down_mfma(const ExpertArgs& a, hipStream_t s) {
   switch (a.down.fmt) {
     case HX_Q4_K: hipLaunchKernelGGL(k_down_mfma<HX_Q4_K>, grid, dim3(256), 0, s, a); break;
     case HX_Q8_0: hipLaunchKernelGGL(k_down_mfma<HX_Q8_0>, grid, dim3(256), 0, s, a); break;
-    case HX_Q6_K: hipLaunchKernelGGL(k_down_mfma<HX_Q6_K>, grid, dim3(256), 0, s, a); break;
+    case HX_Q6_K:
+      if (a.I == DQ_K && a.wpos) hipLaunchKernelGGL(k_down_q6k, grid, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL(k_down_mfma<HX_Q6_K>, grid, dim3(256), 0, s, a);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();

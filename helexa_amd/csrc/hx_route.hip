@@ -142,6 +142,7 @@ HX_DEV void dispatch_block(const DispatchArgs& a, DispatchSmem& sm) {
       int pos = sm.cnt[e] + pre + rank;
       a.perm[pos] = f;
       if (a.inv) a.inv[f] = pos;
+      if (a.wpos) a.wpos[pos] = a.topk_w[f];
     }
     __syncthreads();
     if (leader) {
@@ -154,6 +155,8 @@ HX_DEV void dispatch_block(const DispatchArgs& a, DispatchSmem& sm) {
 
 __global__ __launch_bounds__(1024) void k_dispatch(DispatchArgs a) {
   __shared__ DispatchSmem sm;
+  if (a.wpos && a.has_shared)
+    for (int t = threadIdx.x; t < a.T; t += 1024) a.wpos[a.F + t] = a.sgw[t];
   dispatch_block<1024>(a, sm);
 }
 
@@ -268,6 +271,8 @@ __global__ __launch_bounds__(256) void k_disp_scatter(DispatchArgs a) {
   __shared__ int cnt[HX_MAX_EXPERTS];
   __shared__ uint8_t whist[4][HX_MAX_EXPERTS];
   const int b = blockIdx.x, E = a.E, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
+  if (b == 0 && a.wpos && a.has_shared)
+    for (int t = tid; t < a.T; t += 256) a.wpos[a.F + t] = a.sgw[t];
   for (int e = tid; e < E; e += 256) {
     cnt[e] = a.hist[(int64_t)b * E + e];
     whist[0][e] = whist[1][e] = whist[2][e] = whist[3][e] = 0;
@@ -296,6 +301,7 @@ __global__ __launch_bounds__(256) void k_disp_scatter(DispatchArgs a) {
       const int pos = cnt[e] + pre + rank;
       a.perm[pos] = f;
       if (a.inv) a.inv[f] = pos;
+      if (a.wpos) a.wpos[pos] = a.topk_w[f];
     }
     __syncthreads();
     if (leader) {
