@@ -388,6 +388,89 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
 }
 
 // ----------------------------------------------------------------------------
+// K2 for one token with H = 64 chunks of 32 and k = KR: a wave owns one row
+// of the gate or of the up projection (waves 2i and 2i + 1: row 2b + i of
+// workgroup b) for the KR routed experts and the shared expert. Every wave
+// routes the token itself (same arithmetic as route_token_core, so all waves
+// agree; no barrier) and issues the loads of its row of the rank-r expert right
+// after round r, so the weight stream overlaps the rest of the selection; the
+// shared expert's row is loaded before routing starts. The KR + 1 dot products
+// of a wave are summed by one reduce-scatter, and wave 2i combines them with
+// wave 2i + 1's into h = silu(gate) * up, stored at the row of h of the
+// expert's dispatch position. Workgroup 0 also publishes routing and plan.
+// ----------------------------------------------------------------------------
+template <int FMT, int EPL, int KR>
+__global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a) {
+  using D = DChunk<FMT>;
+  static_assert(KR < 16, "the rank-r sums and the shared one fit 16 values");
+  __shared__ RouteSmem sm;
+  __shared__ float sums[4][16];
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  const int mat = wave & 1;                       // 0: gate, 1: up
+  const int row = blockIdx.x * 2 + (wave >> 1);   // row of I (and of the shared expert's Is)
+  const int K = a.H;
+  uint32_t xp[D::NX];
+  float xs[D::NS];
+  D::template load_x<false>((const uint16_t*)a.x, lane, xp, xs);
+  const bool shrow = a.Is > 0 && row < a.Is, rrow = row < a.I;
+  // loads are unconditional (out-of-range rows read row 0 and are dropped at
+  // the end), and a scheduling barrier after each round's loads keeps the
+  // compiler from pulling the dot products' first instructions up to them,
+  // which would wait for every load on the spot
+  typename D::Raw rsh;
+  const bool hs = a.Is > 0;   // without a shared expert, read routed matrix 0
+  D::load(hs ? (mat ? a.sup.base : a.sgate.base) : (mat ? a.up.mat(0) : a.gate.mat(0)),
+          hs ? a.Is : a.I, K, shrow ? row : 0, lane, rsh);
+  __builtin_amdgcn_sched_barrier(0);
+  const float sg = r.has_shared ? r.logits[r.E] : 0.f;
+  typename D::Raw raw[KR];
+  int my_e;
+  float my_w;
+  route_token_core_hook<EPL, KR>(r.logits, r.E, r.norm, my_e, my_w, [&](int j, int e) {
+    D::load(mat ? a.up.mat(e) : a.gate.mat(e), a.I, K, rrow ? row : 0, lane, raw[j]);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  // dispatch position of rank `lane`: the k experts are distinct
+  int pos = 0;
+#pragma unroll
+  for (int j = 0; j < KR; j++) pos += __builtin_amdgcn_readlane(my_e, j) < my_e;
+  float v[16];
+#pragma unroll
+  for (int j = 0; j < KR; j++) v[j] = D::dot(raw[j], xp, xs);
+  const float vs = D::dot(rsh, xp, xs);
+  v[KR] = hs ? vs : 0.f;
+#pragma unroll
+  for (int j = KR + 1; j < 16; j++) v[j] = 0.f;
+  rs_vals64<16>(v);   // lane l: value l / 4
+  if ((lane & 3) == 0) sums[wave][lane >> 2] = v[0];
+  const bool publisher = blockIdx.x == 0;
+  if (publisher && wave == 0) {
+    if (lane < KR) {
+      sm.idx[lane] = my_e;
+      sm.w[lane] = my_w;
+      sm.pos[lane] = pos;
+      sm.perm[pos] = lane;
+      sm.first[lane] = 1;
+      sm.slots[3 * pos + 0] = my_e;
+      sm.slots[3 * pos + 1] = pos;
+      sm.slots[3 * pos + 2] = 1;
+    }
+    if (lane == 0) {
+      sm.sgw[0] = r.has_shared ? sigmoidf_(sg) : 0.0f;
+      sm.nroute = KR;
+    }
+  }
+  __syncthreads();
+  if (mat == 0 && lane <= KR) {
+    const float g = sums[wave][lane], u = sums[wave + 1][lane];
+    const _Float16 h = (_Float16)(siluf_(g) * u);
+    if (lane < KR && rrow) ((_Float16*)a.hbf)[(int64_t)pos * a.hstride + row] = h;
+    if (lane == KR && shrow) ((_Float16*)a.hbf)[(int64_t)a.F * a.hstride + row] = h;
+  }
+  if (publisher) publish_route(r.d, r.topk_w, r.sgw, sm);
+}
+
+// ----------------------------------------------------------------------------
 // K2 for T > 1: the routing and plan were published by one workgroup
 // (k_route_small); grid row u computes rows of slot u's expert from the plan.
 // The shared expert's slot (the last) was computed by the router kernel.
@@ -622,7 +705,23 @@ hipError_t launch_router_dec(const RouterArgs& r, const ExpertArgs& a, bool rbf,
   }
 }
 
+template <int FMT>
+static hipError_t gate_up_dec1_fmt(const RouterArgs& r, const ExpertArgs& a, hipStream_t s) {
+  const int rows = a.I > a.Is ? a.I : a.Is;
+  hipLaunchKernelGGL((k_gate_up_dec1<FMT, 8, 10>), dim3((rows + 1) / 2), dim3(256), 0, s, r, a);
+  return hipGetLastError();
+}
+
 hipError_t launch_gate_up_dec(const RouterArgs& r, const ExpertArgs& a, hipStream_t s) {
+  // one token, H = 2048, top-10 of 257..512 experts: the overlapped kernel
+  if (a.T == 1 && a.H == 64 * 32 && a.k == 10 && r.E > 256 && r.E <= 512) {
+    switch (a.gate.fmt) {
+      case HX_Q8_0: return gate_up_dec1_fmt<HX_Q8_0>(r, a, s);
+      case HX_Q4_K: return gate_up_dec1_fmt<HX_Q4_K>(r, a, s);
+      case HX_Q6_K: return gate_up_dec1_fmt<HX_Q6_K>(r, a, s);
+      default: break;
+    }
+  }
   switch (a.gate.fmt) {
     case HX_Q8_0: return gate_up_dec_fmt<HX_Q8_0>(r, a, s);
     case HX_Q4_K: return gate_up_dec_fmt<HX_Q4_K>(r, a, s);

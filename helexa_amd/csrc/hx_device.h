@@ -218,6 +218,22 @@ HX_DEV void rs_pairs64(float* g, float* u) {
   }
 }
 
+// Wave-wide sums of M values (M a power of two <= 64), as rs_pairs64 for
+// single values: lane l ends with the sum of value l >> (6 - log2 M) in v[0].
+template <int M, int STEP = 0>
+HX_DEV void rs_vals64(float* v) {
+  if constexpr (STEP < 6) {
+    constexpr int OFF = 32 >> STEP, LIVE = M >> STEP;
+    if constexpr (LIVE >= 2) {
+#pragma unroll
+      for (int k = 0; k < LIVE / 2; k++) v[k] = rs_keep<OFF>(v[k], v[k + LIVE / 2]);
+    } else {
+      v[0] = bf_add<OFF>(v[0]);
+    }
+    rs_vals64<M, STEP + 1>(v);
+  }
+}
+
 // The butterfly of wave_sum<64> applied to 64 values at once, as a
 // reduce-scatter: at each step a lane adds its partner's copy of only the half
 // of its live values it keeps (the half selected by the lane's bit for that

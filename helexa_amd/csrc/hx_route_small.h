@@ -64,6 +64,68 @@ HX_DEV void sort_keys_desc(uint32_t* h, uint32_t* l) {
       }
 }
 
+// softmax over the E logits of a token and this lane's keys, sorted
+template <int EPL>
+HX_DEV void route_keys(const float* lg, int E, uint32_t* h, uint32_t* l) {
+  const int lane = lane_id();
+  float v[EPL];
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < EPL; j++) {
+    const int e = lane + 64 * j;
+    const float x = lg[e < E ? e : E - 1];
+    v[j] = e < E ? x : -__builtin_inff();
+    mx = v[j] > mx ? v[j] : mx;
+  }
+  mx = wave_max_dpp(mx);
+#pragma unroll
+  for (int j = 0; j < EPL; j++) v[j] = v[j] - mx;
+  expf_route_n<EPL>(v);   // padding: exp(-inf) = 0
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < EPL; j++) s = s + v[j];
+  s = wave_sum<64>(s);
+#pragma unroll
+  for (int j = 0; j < EPL; j++) {
+    h[j] = __float_as_uint(v[j] / s);   // padding: 0 / s = +0
+    l[j] = ~(uint32_t)(lane + 64 * j);
+  }
+  sort_keys_desc<EPL>(h, l);
+}
+
+// One selection round: the wave-wide largest head probability m; when several
+// heads hold it, the lowest expert id among them. Returns that expert (wave-
+// uniform) and its probability bits in m; pops it. The rest of the previous
+// pop's shift (pend) is applied alongside the reduction.
+template <int EPL>
+HX_DEV int route_round(uint32_t* h, uint32_t* l, uint32_t& pend, uint32_t& m) {
+  uint32_t x = h[0];
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xf, 0xf, false));
+#pragma unroll
+  for (int j = 1; j + 1 < EPL; j++) h[j] = (h[j] & ~pend) | (h[j + 1] & pend);
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xf, 0xf, false));
+  if (EPL > 1) h[EPL - 1] &= ~pend;
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xf, 0xf, false));
+#pragma unroll
+  for (int j = 0; j + 1 < EPL; j++) l[j] = (l[j] & ~pend) | (l[j + 1] & pend);
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x140, 0xf, 0xf, false));
+  l[EPL - 1] &= ~pend;
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false));
+  x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false));
+  m = (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+  bool hit = h[0] == m;
+  unsigned long long hold = __ballot(hit);
+  if (hold & (hold - 1)) {   // several heads hold m: the lowest expert id goes first
+    const uint32_t lo = wave_max_u32(hit ? l[0] : 0u);
+    hit = hit && l[0] == lo;
+    hold = __ballot(hit);
+  }
+  pend = hit ? 0xffffffffu : 0u;
+  const int e = (int)~(uint32_t)__builtin_amdgcn_readlane((int)l[0], __ffsll((long long)hold) - 1);
+  h[0] = EPL > 1 ? ((h[0] & ~pend) | (h[1] & pend)) : (h[0] & ~pend);
+  return e;
+}
+
 // One wave routes one token: softmax over E with expf_route and the
 // lane-strided butterfly sum, then the k largest probabilities, ties to the
 // lowest expert id, and the sequential renormalisation in rank order. Lane
@@ -85,58 +147,39 @@ HX_DEV void sort_keys_desc(uint32_t* h, uint32_t* l) {
 template <int EPL>
 HX_DEV void route_token_core(const float* lg, int E, int k, bool norm, int& out_e, float& out_w) {
   const int lane = lane_id();
-  float v[EPL];
-  float mx = -__builtin_inff();
-#pragma unroll
-  for (int j = 0; j < EPL; j++) {
-    const int e = lane + 64 * j;
-    const float x = lg[e < E ? e : E - 1];
-    v[j] = e < E ? x : -__builtin_inff();
-    mx = v[j] > mx ? v[j] : mx;
-  }
-  mx = wave_max_dpp(mx);
-#pragma unroll
-  for (int j = 0; j < EPL; j++) v[j] = v[j] - mx;
-  expf_route_n<EPL>(v);   // padding: exp(-inf) = 0
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < EPL; j++) s = s + v[j];
-  s = wave_sum<64>(s);
   uint32_t h[EPL], l[EPL];
-#pragma unroll
-  for (int j = 0; j < EPL; j++) {
-    h[j] = __float_as_uint(v[j] / s);   // padding: 0 / s = +0
-    l[j] = ~(uint32_t)(lane + 64 * j);
-  }
-  sort_keys_desc<EPL>(h, l);
+  route_keys<EPL>(lg, E, h, l);
   float my_p = 0.0f, tot = 0.0f;
   int my_e = 0;
   uint32_t pend = 0u;   // all-ones in the lane popped by the previous round
   for (int r = 0; r < k; r++) {
-    uint32_t x = h[0];
-    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0xB1, 0xf, 0xf, false));
+    uint32_t m;
+    const int e = route_round<EPL>(h, l, pend, m);
+    const float pm = __uint_as_float(m);
+    tot = tot + pm;
+    my_p = lane == r ? pm : my_p;
+    my_e = lane == r ? e : my_e;
+  }
+  out_e = my_e;
+  out_w = norm ? my_p / tot : my_p;
+}
+
+// route_token_core with K rounds unrolled and hook(r, e) called right after
+// round r picks expert e (wave-uniform), so a caller can start loading that
+// expert's weights while the later rounds run
+template <int EPL, int K, class Hook>
+HX_DEV void route_token_core_hook(const float* lg, int E, bool norm, int& out_e, float& out_w, Hook&& hook) {
+  const int lane = lane_id();
+  uint32_t h[EPL], l[EPL];
+  route_keys<EPL>(lg, E, h, l);
+  float my_p = 0.0f, tot = 0.0f;
+  int my_e = 0;
+  uint32_t pend = 0u;
 #pragma unroll
-    for (int j = 1; j + 1 < EPL; j++) h[j] = (h[j] & ~pend) | (h[j + 1] & pend);
-    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x4E, 0xf, 0xf, false));
-    if (EPL > 1) h[EPL - 1] &= ~pend;
-    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x141, 0xf, 0xf, false));
-#pragma unroll
-    for (int j = 0; j + 1 < EPL; j++) l[j] = (l[j] & ~pend) | (l[j + 1] & pend);
-    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x140, 0xf, 0xf, false));
-    l[EPL - 1] &= ~pend;
-    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x142, 0xa, 0xf, false));
-    x = max(x, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x143, 0xc, 0xf, false));
-    const uint32_t m = (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
-    bool hit = h[0] == m;
-    unsigned long long hold = __ballot(hit);
-    if (hold & (hold - 1)) {   // several heads hold m: the lowest expert id goes first
-      const uint32_t lo = wave_max_u32(hit ? l[0] : 0u);
-      hit = hit && l[0] == lo;
-      hold = __ballot(hit);
-    }
-    pend = hit ? 0xffffffffu : 0u;
-    const int e = (int)~(uint32_t)__builtin_amdgcn_readlane((int)l[0], __ffsll((long long)hold) - 1);
-    h[0] = EPL > 1 ? ((h[0] & ~pend) | (h[1] & pend)) : (h[0] & ~pend);
+  for (int r = 0; r < K; r++) {
+    uint32_t m;
+    const int e = route_round<EPL>(h, l, pend, m);
+    hook(r, e);
     const float pm = __uint_as_float(m);
     tot = tot + pm;
     my_p = lane == r ? pm : my_p;
