@@ -228,11 +228,13 @@ HX_DEV f16x8_t frag(const uint16_t* base) { return __builtin_bit_cast(f16x8_t, *
 //          64 qs bytes of the chunk's half superblock, 80 B per row.
 // Each wave dequantises its own B fragments from the raw bytes in LDS, so the
 // activations are the only operand every wave reads in full.
-// LDS: FPW = 1 with 4 waves, 3 stages of 26 KB (2 workgroups per CU, about
-// 100 KB in flight per CU). Measured on MI355X for the A3B shapes, this beats
-// 8 waves over 128 + 128 columns (4 stages of 36 KB, one workgroup per CU)
-// and 4 waves with FPW = 2: fewer waves per SIMD hide less of the LDS and
-// dequantisation latency than the halved activation traffic saves.
+// LDS: FPW = 1 with 4 waves, 2 stages of 26 KB, so 3 workgroups per CU.
+// Measured on MI355X for the A3B shapes, this beats 3 stages with 2
+// workgroups per CU (the kernel waits more on its own LDS reads, dequantisation
+// and MFMA chains than on memory, so waves per SIMD matter more than a second
+// chunk of look-ahead), 4 waves with FPW = 2, and 8 waves over 128 + 128
+// columns: fewer waves per SIMD hide less of the LDS and dequantisation
+// latency than the halved activation traffic saves.
 // The DMA instructions are issued from inline assembly (M0 saved and restored
 // around them) because the compiler, not knowing which LDS bytes a DMA writes,
 // would otherwise wait for every outstanding one before each LDS read; the
@@ -268,7 +270,7 @@ struct Q4k {
   static constexpr int COLS = 16 * FPW * NW;             // gate (and up) columns of a tile
   static constexpr int BROWS = 2 * COLS;                 // gate + up weight rows
   static constexpr int STAGE = QA_BYTES + BROWS * QB_ROW;
-  static constexpr int NST = STAGE <= 27 * 1024 ? 3 : 4;
+  static constexpr int NST = 2;                          // ring stages
   static constexpr int NA = 1024 / NT;                   // A DMA rounds
   static constexpr int BPIECES = 5 * BROWS;              // 16-byte pieces of B per chunk
   static constexpr int NBI = (BPIECES + NT - 1) / NT;    // B DMA rounds
@@ -425,7 +427,8 @@ HX_DEV void q4k_wait(int ahead, int wave_u) {
 
 // grid (I / COLS, tiles rounded up to 8), mapped by xcd_tile
 template <int FPW, int NW>
-__global__ __launch_bounds__(64 * NW, (Q4k<FPW, NW>::NST == 3 ? 2 : 1)) void k_gate_up_q4k(ExpertArgs a) {
+// (the second bound is waves per SIMD: 3 workgroups of 4 waves per CU)
+__global__ __launch_bounds__(64 * NW, 3) void k_gate_up_q4k(ExpertArgs a) {
   using Q = Q4k<FPW, NW>;
   __shared__ __attribute__((aligned(16))) uint8_t ring[Q::NST * Q::STAGE];
   __shared__ int rowsrc[PM];
