@@ -87,18 +87,22 @@ struct DChunk<HX_Q8_0> {
   HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
     Chunk<HX_Q8_0>::load(mat, R, K, row, c, r);
   }
-  // activation positions: elements 32c .. 32c+31, pairs per 8
-  template <bool XF16, class P = const uint16_t*>
-  HX_DEV static void load_x(P xrow, int c, uint32_t* xp, float* xs) {
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-      if constexpr (XF16) x_pairs_f16(xrow + 32 * c + 8 * v, xp + 4 * v);
-      else x_pairs_bf16(xrow + 32 * c + 8 * v, xp + 4 * v);
-    }
+  // activation positions: elements 32c .. 32c+31; group g of 8 -> pairs xp[4g ..]
+  HX_DEV static int x_group_off(int c, int g) { return 32 * c + 8 * g; }
+  HX_DEV static void x_sums(const uint32_t* xp, float* xs) {
     float s = 0.f;
 #pragma unroll
     for (int i = 0; i < 16; i++) s += f16x2_sum(xp[i]);
     xs[0] = s;
+  }
+  template <bool XF16, class P = const uint16_t*>
+  HX_DEV static void load_x(P xrow, int c, uint32_t* xp, float* xs) {
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      if constexpr (XF16) x_pairs_f16(xrow + x_group_off(c, v), xp + 4 * v);
+      else x_pairs_bf16(xrow + x_group_off(c, v), xp + 4 * v);
+    }
+    x_sums(xp, xs);
   }
   HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs) {
     const uint32_t q[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
@@ -121,20 +125,12 @@ struct DChunk<HX_Q4_K> {
   HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
     Chunk<HX_Q4_K>::load(mat, R, K, row, c, r);
   }
-  template <bool XF16, class P = const uint16_t*>
-  HX_DEV static void load_x(P xrow, int c, uint32_t* xp, float* xs) {
+  // activation positions: the low run (groups 0, 1) and the high run (2, 3)
+  HX_DEV static int x_group_off(int c, int g) {
     const int sb = c >> 3, cc = c & 7, p = cc >> 1, h = cc & 1;
-    const auto lo = xrow + sb * 256 + 64 * p + 16 * h;
-#pragma unroll
-    for (int v = 0; v < 2; v++) {
-      if constexpr (XF16) {
-        x_pairs_f16(lo + 8 * v, xp + 4 * v);
-        x_pairs_f16(lo + 32 + 8 * v, xp + 8 + 4 * v);
-      } else {
-        x_pairs_bf16(lo + 8 * v, xp + 4 * v);
-        x_pairs_bf16(lo + 32 + 8 * v, xp + 8 + 4 * v);
-      }
-    }
+    return sb * 256 + 64 * p + 16 * h + 8 * (g & 1) + 32 * (g >> 1);
+  }
+  HX_DEV static void x_sums(const uint32_t* xp, float* xs) {
     float a = 0.f, b = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
@@ -143,6 +139,15 @@ struct DChunk<HX_Q4_K> {
     }
     xs[0] = a;
     xs[1] = b;
+  }
+  template <bool XF16, class P = const uint16_t*>
+  HX_DEV static void load_x(P xrow, int c, uint32_t* xp, float* xs) {
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      if constexpr (XF16) x_pairs_f16(xrow + x_group_off(c, g), xp + 4 * g);
+      else x_pairs_bf16(xrow + x_group_off(c, g), xp + 4 * g);
+    }
+    x_sums(xp, xs);
   }
   HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs) {
     const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
@@ -172,19 +177,28 @@ struct DChunk<HX_Q6_K> {
   HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
     Chunk<HX_Q6_K>::load(mat, R, K, row, c, r);
   }
-  template <bool XF16, class P = const uint16_t*>
-  HX_DEV static void load_x(P xrow, int c, uint32_t* xp, float* xs) {
+  // activation positions: quarter g of the chunk's half superblock
+  HX_DEV static int x_group_off(int c, int g) {
     const int sb = c >> 3, cc = c & 7, n = cc >> 2, a = cc & 3;
-    const auto base = xrow + sb * 256 + 128 * n + 8 * a;
+    return sb * 256 + 128 * n + 8 * a + 32 * g;
+  }
+  HX_DEV static void x_sums(const uint32_t* xp, float* xs) {
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-      if constexpr (XF16) x_pairs_f16(base + 32 * s, xp + 4 * s);
-      else x_pairs_bf16(base + 32 * s, xp + 4 * s);
       float t = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; i++) t += f16x2_sum(xp[4 * s + i]);
       xs[s] = t;
     }
+  }
+  template <bool XF16, class P = const uint16_t*>
+  HX_DEV static void load_x(P xrow, int c, uint32_t* xp, float* xs) {
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      if constexpr (XF16) x_pairs_f16(xrow + x_group_off(c, g), xp + 4 * g);
+      else x_pairs_bf16(xrow + x_group_off(c, g), xp + 4 * g);
+    }
+    x_sums(xp, xs);
   }
   HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs) {
     const uint32_t l0[2] = {r.l0.x, r.l0.y}, l1[2] = {r.l1.x, r.l1.y}, hh[2] = {r.h.x, r.h.y};
@@ -504,32 +518,43 @@ __global__ __launch_bounds__(256) void k_gate_up_plan(ExpertArgs a) {
 // ----------------------------------------------------------------------------
 // XLDS: the group's rows of h are staged in LDS first (many rows: each row of
 // h is read by every output-row block, and the activations then stay out of
-// the registers while the weight loads are in flight); otherwise (one token)
-// each wave loads its activations from global memory together with its weights,
-// which keeps the kernel to one memory round trip after the plan.
+// the registers while the weight loads are in flight). Otherwise (one token)
+// each wave loads its activations from global memory together with its
+// weights, every load unconditional (rows past the group's end, and chunks past
+// a shorter shared expert's K, read valid data whose result is dropped) and
+// all of them issued before any is used, so the kernel makes one memory round
+// trip after the plan.
 template <int FMT, int LPR, int SPW, int NW, bool XLDS>
 __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
   using D = DChunk<FMT>;
   constexpr int RG = 64 / LPR;
-  static_assert(NW * SPW == HX_DOWN_ROWS, "one pass per wave over a group of rows of h");
+  constexpr int ROWS = NW * SPW;   // rows of h per group (one pass per wave)
+  static_assert(ROWS <= HX_DOWN_ROWS, "groups of at most HX_DOWN_ROWS rows of h");
   // LDS: the group's rows of h (f16, Kmax each; XLDS only), then per row its
-  // token, weight and expert, then the contributions [HX_DOWN_ROWS][RG]
+  // token, weight and expert, then the contributions [ROWS][RG]
   extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
   const int Kmax = XLDS ? (a.I > a.Is ? a.I : a.Is) : 0;
-  int* stok = (int*)(xl + HX_DOWN_ROWS * Kmax);
-  float* swt = (float*)(stok + HX_DOWN_ROWS);
-  int* sexp = (int*)(swt + HX_DOWN_ROWS);
-  float* contrib = (float*)(sexp + HX_DOWN_ROWS);
+  int* stok = (int*)(xl + ROWS * Kmax);
+  float* swt = (float*)(stok + ROWS);
+  int* sexp = (int*)(swt + ROWS);
+  float* contrib = (float*)(sexp + ROWS);
   const int T = a.T, NH = a.F + T;
   const int nh_all = a.F + (a.Is > 0 ? T : 0);   // rows of h in use
-  const int h0 = blockIdx.y * HX_DOWN_ROWS;      // this workgroup's group of rows
-  const int nh = min(nh_all - h0, HX_DOWN_ROWS);
+  const int h0 = blockIdx.y * ROWS;              // this workgroup's group of rows
+  const int nh = min(nh_all - h0, ROWS);
   {
+    // thread 32 part + r < 96 loads row r's token (part 0), weight (1) or
+    // expert (2); one load each, clamped to a valid row, so one round trip.
+    // Rows r in [nh, ROWS) get token -1 (no token's row).
+    static_assert(ROWS <= 32, "a part of the plan per 32 threads");
     const int tok0 = 4 + 4 * a.max_slots + h0;
-    const int i = threadIdx.x;
-    if (i < nh) stok[i] = a.plan[tok0 + i];
-    else if (i >= 32 && i < 32 + nh) swt[i - 32] = __int_as_float(a.plan[tok0 + NH + i - 32]);
-    else if (i >= 64 && i < 64 + nh) sexp[i - 64] = a.plan[tok0 + 2 * NH + i - 64];
+    const int i = threadIdx.x, part = i >> 5, r = i & 31;
+    if (i < 96) {
+      const int v = a.plan[tok0 + part * NH + min(r, nh - 1)];
+      int* dst = part == 0 ? stok : part == 1 ? (int*)swt : sexp;
+      if (r < nh) dst[r] = v;
+      else if (part == 0 && r < ROWS) dst[r] = -1;
+    }
     if constexpr (XLDS) {
       // the group's rows of h, 16 bytes per thread and step (measured: batching
       // these loads per thread raised the register count and slowed the kernel)
@@ -543,40 +568,53 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
   __syncthreads();
   const int lane = lane_id(), wave = threadIdx.x >> 6, rg = lane / LPR, c = lane % LPR;
   const int n0 = blockIdx.x * RG, row = n0 + rg;
-  // every weight load of the wave first (SPW rows of h), then the dot products
-  // with the activations from LDS
+  // every weight (and, for one token, activation) load of the wave first,
+  // then the dot products
   typename D::Raw raw[SPW];
-  uint32_t xpg[XLDS ? 1 : SPW][D::NX];
-  float xsg[XLDS ? 1 : SPW][D::NS];
+  uint4 xr[XLDS ? 1 : SPW][4];
 #pragma unroll
   for (int s = 0; s < SPW; s++) {
     const int hr = wave + NW * s;
-    if (hr < nh) {
-      const int e = sexp[hr];
+    if constexpr (XLDS) {
+      if (hr < nh) {
+        const int e = sexp[hr];
+        const bool sh = e == a.E;
+        const int K = sh ? a.Is : a.I;
+        if (row < a.H && c < K / 32) D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row, c, raw[s]);
+      }
+    } else {
+      const int hq = hr < nh ? hr : 0;
+      const int e = sexp[hq];
       const bool sh = e == a.E;
       const int K = sh ? a.Is : a.I;
-      if (row < a.H && c < K / 32) {
-        D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row, c, raw[s]);
-        if constexpr (!XLDS)
-          D::template load_x<true>((const uint16_t*)a.hbf + (int64_t)(h0 + hr) * a.hstride, c, xpg[s], xsg[s]);
-      }
+      const int cc = c < K / 32 ? c : 0;
+      D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row < a.H ? row : 0, cc, raw[s]);
+      const uint16_t* xrow = (const uint16_t*)a.hbf + (int64_t)(h0 + hq) * a.hstride;
+#pragma unroll
+      for (int g = 0; g < 4; g++) xr[s][g] = *(const uint4*)(xrow + D::x_group_off(cc, g));
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int s = 0; s < SPW; s++) {
     const int hr = wave + NW * s;
-    if (hr >= nh) break;
+    if (hr >= nh) {   // every contribution slot is defined (zero past the group's rows)
+      if (c == 0 && row < a.H) contrib[hr * RG + rg] = 0.f;
+      continue;
+    }
     const int K = sexp[hr] == a.E ? a.Is : a.I;
     float p = 0.f;
     if (c < K / 32) {
+      uint32_t xp[D::NX];
+      float xs[D::NS];
       if constexpr (XLDS) {
-        uint32_t xp[D::NX];
-        float xs[D::NS];
         D::template load_x<true>((lds_cu16)(xl + hr * Kmax), c, xp, xs);
-        p = D::dot(raw[s], xp, xs);
       } else {
-        p = D::dot(raw[s], xpg[s], xsg[s]);
+#pragma unroll
+        for (int g = 0; g < 4; g++) pairs_from_f16x8(xr[s][g], xp + 4 * g);
+        D::x_sums(xp, xs);
       }
+      p = D::dot(raw[s], xp, xs);
     }
     p = wave_sum<LPR>(p);
     if (c == 0 && row < a.H) contrib[hr * RG + rg] = swt[hr] * p;
@@ -589,8 +627,10 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
     const int t = i / RG, r = i % RG;
     if (n0 + r >= a.H) continue;
     float y = 0.f;
-    for (int hr = 0; hr < nh; hr++)
-      if (stok[hr] == t) y += contrib[hr * RG + r];
+    // unrolled, and the row selection a multiplication by 1 or 0 (exact), so
+    // the LDS reads are unconditional and go out together
+#pragma unroll
+    for (int hr = 0; hr < ROWS; hr++) y += contrib[hr * RG + r] * (stok[hr] == t ? 1.f : 0.f);
     if (gridDim.y > 1) {
       a.dpart[((int64_t)blockIdx.y * T + t) * a.H + n0 + r] = y;
     } else if (a.resid) {
@@ -680,6 +720,8 @@ static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
   const int nch = (a.I > a.Is ? a.I : a.Is) / 32;
   const int groups = down_groups(a.F, a.Is > 0 ? a.T : 0);
   const bool xlds = a.T > 1;   // one token: activations straight from global memory
+  // one token with at most 12 rows of h (k <= 11): 3 rows per wave
+  const bool small = !xlds && a.F + (a.Is > 0 ? 1 : 0) <= 12;
 #define DD(LPR)                                                                                   \
   {                                                                                               \
     constexpr int RG = 64 / LPR;                                                                  \
@@ -687,6 +729,7 @@ static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
     size_t lds = (size_t)HX_DOWN_ROWS * Kmax * 2 + (size_t)HX_DOWN_ROWS * (3 + RG) * 4;           \
     const dim3 grid((a.H + RG - 1) / RG, groups);                                                   \
     if (xlds) hipLaunchKernelGGL((k_down_dec<FMT, LPR, 6, 4, true>), grid, dim3(256), lds, s, a);   \
+    else if (small) hipLaunchKernelGGL((k_down_dec<FMT, LPR, 3, 4, false>), grid, dim3(256), lds, s, a); \
     else hipLaunchKernelGGL((k_down_dec<FMT, LPR, 6, 4, false>), grid, dim3(256), lds, s, a);       \
   }
   if (nch == 64) DD(64) else if (nch == 32) DD(32) else DD(16)
