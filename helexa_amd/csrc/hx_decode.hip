@@ -47,9 +47,8 @@ HX_DEV void pairs_from_f16x8(uint4 v, uint32_t* out) {
   }
 }
 
-// x: 8 bf16 at p -> 4 f16 pairs in weight-pair order
-HX_DEV void x_pairs_bf16(const uint16_t* p, uint32_t* out) {
-  uint4 v = *(const uint4*)p;
+// x: 8 bf16 (loaded) -> 4 f16 pairs in weight-pair order
+HX_DEV void x_pairs_bf16v(uint4 v, uint32_t* out) {
   uint4 h;
   h.x = bf16x2_to_f16x2(v.x);
   h.y = bf16x2_to_f16x2(v.y);
@@ -57,6 +56,8 @@ HX_DEV void x_pairs_bf16(const uint16_t* p, uint32_t* out) {
   h.w = bf16x2_to_f16x2(v.w);
   pairs_from_f16x8(h, out);
 }
+// x: 8 bf16 at p -> 4 f16 pairs in weight-pair order
+HX_DEV void x_pairs_bf16(const uint16_t* p, uint32_t* out) { x_pairs_bf16v(*(const uint4*)p, out); }
 
 typedef const __attribute__((address_space(3))) uint16_t* lds_cu16;
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
@@ -267,12 +268,10 @@ HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U
   const int c = lane_id() % LPR, K = a.H;
   typename D::Raw rgt[NR], rup[NR];
 #pragma unroll
-  for (int g = 0; g < NR; g++) {
-    const int row = row0 + g * RG;
-    if (row < rows) {
-      D::load(G, rows, K, row, c, rgt[g]);
-      D::load(U, rows, K, row, c, rup[g]);
-    }
+  for (int g = 0; g < NR; g++) {   // rows past the end read the last row (dropped)
+    const int row = min(row0 + g * RG, rows - 1);
+    D::load(G, rows, K, row, c, rgt[g]);
+    D::load(U, rows, K, row, c, rup[g]);
   }
   if constexpr (BATCH && LPR == 64) {
     if (count > 1) {
@@ -306,10 +305,23 @@ HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U
       return;
     }
   }
+  // token j's activations are loaded as raw bf16 before token j - 1's dot
+  // products (token 0's together with the weights), so each load overlaps work
+  uint4 xr[4];
+#pragma unroll
+  for (int g = 0; g < 4; g++) xr[g] = *(const uint4*)((const uint16_t*)a.x + (int64_t)tok[0] * K + D::x_group_off(c, g));
+  __builtin_amdgcn_sched_barrier(0);   // no weight arithmetic above these loads
   for (int j = 0; j < count; j++) {
     uint32_t xp[D::NX];
     float xs[D::NS];
-    D::template load_x<false>((const uint16_t*)a.x + (int64_t)tok[j] * K, c, xp, xs);
+#pragma unroll
+    for (int g = 0; g < 4; g++) x_pairs_bf16v(xr[g], xp + 4 * g);
+    D::x_sums(xp, xs);
+    if (j + 1 < count) {
+#pragma unroll
+      for (int g = 0; g < 4; g++)
+        xr[g] = *(const uint4*)((const uint16_t*)a.x + (int64_t)tok[j + 1] * K + D::x_group_off(c, g));
+    }
 #pragma unroll
     for (int g = 0; g < NR; g++) {
       const int row = row0 + g * RG;
@@ -555,44 +567,45 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
       if (r < nh) dst[r] = v;
       else if (part == 0 && r < ROWS) dst[r] = -1;
     }
-    if constexpr (XLDS) {
-      // the group's rows of h, 16 bytes per thread and step (measured: batching
-      // these loads per thread raised the register count and slowed the kernel)
-      const int per_row = Kmax / 8, n16 = nh * per_row;
-      for (int q = threadIdx.x; q < n16; q += 64 * NW) {
-        const int r = q / per_row, o = q - r * per_row;
-        *(uint4*)(xl + r * Kmax + 8 * o) = *(const uint4*)(a.hbf + (int64_t)(h0 + r) * a.hstride + 8 * o);
-      }
-    }
   }
   __syncthreads();
   const int lane = lane_id(), wave = threadIdx.x >> 6, rg = lane / LPR, c = lane % LPR;
   const int n0 = blockIdx.x * RG, row = n0 + rg;
   // every weight (and, for one token, activation) load of the wave first,
-  // then the dot products
+  // then the dot products; all unconditional (rows past the group's end, and
+  // chunks past a shorter shared expert's K, read valid data that is dropped)
   typename D::Raw raw[SPW];
   uint4 xr[XLDS ? 1 : SPW][4];
 #pragma unroll
   for (int s = 0; s < SPW; s++) {
     const int hr = wave + NW * s;
-    if constexpr (XLDS) {
-      if (hr < nh) {
-        const int e = sexp[hr];
-        const bool sh = e == a.E;
-        const int K = sh ? a.Is : a.I;
-        if (row < a.H && c < K / 32) D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row, c, raw[s]);
-      }
-    } else {
-      const int hq = hr < nh ? hr : 0;
-      const int e = sexp[hq];
-      const bool sh = e == a.E;
-      const int K = sh ? a.Is : a.I;
-      const int cc = c < K / 32 ? c : 0;
-      D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row < a.H ? row : 0, cc, raw[s]);
+    const int hq = hr < nh ? hr : 0;
+    const int e = sexp[hq];
+    const bool sh = e == a.E;
+    const int K = sh ? a.Is : a.I;
+    const int cc = c < K / 32 ? c : 0;
+    D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row < a.H ? row : 0, cc, raw[s]);
+    if constexpr (!XLDS) {
       const uint16_t* xrow = (const uint16_t*)a.hbf + (int64_t)(h0 + hq) * a.hstride;
 #pragma unroll
       for (int g = 0; g < 4; g++) xr[s][g] = *(const uint4*)(xrow + D::x_group_off(cc, g));
     }
+  }
+  if constexpr (XLDS) {
+    // the group's rows of h into LDS by DMA, issued after the weight loads so
+    // that both arrive in one round trip. The rows are contiguous in memory
+    // (pitch hstride == Kmax) and in LDS (pitch Kmax): 16-byte piece q goes
+    // to LDS byte 16 q. A wave moves 64 pieces per instruction; ROWS Kmax / 8
+    // is a multiple of 64 (Kmax = 512, 1024, 2048), so the pieces past the
+    // group's rows land inside the staging area; their sources are clamped to
+    // the last piece.
+    const int n16 = nh * (Kmax / 8);
+    const uint16_t* src = a.hbf + (int64_t)h0 * a.hstride;
+    const uint32_t xbase = (uint32_t)(uintptr_t)(lds_u8*)xl;
+    for (int q0 = 64 * __builtin_amdgcn_readfirstlane(wave); q0 < n16; q0 += 64 * NW)
+      dma16(src + 8 * min(q0 + lane, n16 - 1), xbase + 16u * (uint32_t)q0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -720,6 +733,7 @@ static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
   const int nch = (a.I > a.Is ? a.I : a.Is) / 32;
   const int groups = down_groups(a.F, a.Is > 0 ? a.T : 0);
   const bool xlds = a.T > 1;   // one token: activations straight from global memory
+  if (xlds && a.hstride != (a.I > a.Is ? a.I : a.Is)) return hipErrorInvalidValue;   // rows of h contiguous
   // one token with at most 12 rows of h (k <= 11): 3 rows per wave
   const bool small = !xlds && a.F + (a.Is > 0 ? 1 : 0) <= 12;
 #define DD(LPR)                                                                                   \

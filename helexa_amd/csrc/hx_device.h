@@ -19,6 +19,18 @@
 
 namespace hx {
 
+typedef __attribute__((address_space(3))) uint8_t lds_u8;
+
+// global_load_lds_dwordx4: lane l's 16 bytes at g land at LDS byte lds_base +
+// 16 l, no registers involved; issued from inline assembly with M0 saved and
+// restored around it (the compiler does not know which LDS bytes it writes, so
+// the waits for it are placed by hand)
+HX_DEV void dma16(const void* g, uint32_t lds_base) {
+  uint32_t save;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(save) : "v"(g), "s"(lds_base) : "memory");
+}
+
 HX_DEV float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
 HX_DEV uint16_t f32_to_bf16(float f) {

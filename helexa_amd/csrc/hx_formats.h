@@ -182,13 +182,14 @@ struct Chunk<HX_Q6_K> {
     int sb = c >> 3, cc = c & 7, n = cc >> 2, a = cc & 3;
     const uint8_t* ql = mat + (int64_t)row * (K / 2) + sb * 128 + 64 * n + 8 * a;
     const uint8_t* qh = mat + (int64_t)R * (K / 2) + (int64_t)row * (K / 4) + sb * 64 + 32 * n + 8 * a;
-    const int8_t* sc = (const int8_t*)(mat + (int64_t)R * (K / 2 + K / 4) + (int64_t)row * (K / 16) + sb * 16 + 8 * n + (a >> 1));
+    // the half's 8 scales as one 8-byte load; the chunk's are bytes
+    // (a >> 1) + 0, 2, 4, 6 of it
+    const uint2 sc8 = *(const uint2*)(mat + (int64_t)R * (K / 2 + K / 4) + (int64_t)row * (K / 16) + sb * 16 + 8 * n);
     const uint16_t* d = (const uint16_t*)(mat + (int64_t)R * (K / 2 + K / 4 + K / 16)) + (int64_t)row * (K / 256) + sb;
     r.l0 = *(const uint2*)ql;
     r.l1 = *(const uint2*)(ql + 32);
     r.h = *(const uint2*)qh;
-    r.sc = (uint32_t)(uint8_t)sc[0] | ((uint32_t)(uint8_t)sc[2] << 8) | ((uint32_t)(uint8_t)sc[4] << 16) |
-           ((uint32_t)(uint8_t)sc[6] << 24);
+    r.sc = __builtin_amdgcn_perm(sc8.y, sc8.x, 0x06040200u + 0x01010101u * (uint32_t)(a >> 1));
     r.d = *d;
   }
   static constexpr int NSUM = 4;

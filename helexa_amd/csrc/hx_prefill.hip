@@ -240,7 +240,6 @@ HX_DEV f16x8_t frag(const uint16_t* base) { return __builtin_bit_cast(f16x8_t, *
 // would otherwise wait for every outstanding one before each LDS read; the
 // waits are placed by hand: before the barrier of chunk kc, a wave waits until
 // only its DMAs of the chunks after kc are outstanding.
-typedef __attribute__((address_space(3))) uint8_t lds_u8;
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 
@@ -251,12 +250,6 @@ HX_DEV uint4 lds_ld16(const lds_u8* p) {
 HX_DEV uint2 lds_ld8(const lds_u8* p) {
   const u32x2_t v = *(const __attribute__((address_space(3))) u32x2_t*)p;
   return make_uint2(v.x, v.y);
-}
-
-HX_DEV void dma16(const void* g, uint32_t lds_base) {
-  uint32_t save;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
-               : "=&s"(save) : "v"(g), "s"(lds_base) : "memory");
 }
 
 constexpr int QA_BYTES = PM * 128 * 2;   // A stage
