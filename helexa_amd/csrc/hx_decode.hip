@@ -150,23 +150,34 @@ struct DChunk<HX_Q4_K> {
     }
     x_sums(xp, xs);
   }
+  // low nibbles (the low run) as 1024 + u, high nibbles masked in place as
+  // 1024 + 16 u (exact in f16: < 2048), so no shift separates them; the 1/16
+  // goes into the high run's scale. Scales and mins of the two runs without
+  // branches (the lanes of a wave hold different sub-blocks).
   HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs) {
+    const uint32_t kmagic = vconst<0x64006400u>(), klo = vconst<0x000F000Fu>(), khi = vconst<0x00F000F0u>();
     const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
     float lo = 0.f, hi = 0.f;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      lo = dot2(nib02(q[j]), xp[2 * j], lo);
-      lo = dot2(nib02(q[j] >> 8), xp[2 * j + 1], lo);
-      hi = dot2(nib02(q[j] >> 4), xp[8 + 2 * j], hi);
-      hi = dot2(nib02(q[j] >> 12), xp[8 + 2 * j + 1], hi);
+      const uint32_t t = q[j] >> 8;
+      lo = dot2(and_or(q[j], klo, kmagic), xp[2 * j], lo);
+      lo = dot2(and_or(t, klo, kmagic), xp[2 * j + 1], lo);
+      hi = dot2(and_or(q[j], khi, kmagic), xp[8 + 2 * j], hi);
+      hi = dot2(and_or(t, khi, kmagic), xp[8 + 2 * j + 1], hi);
     }
     const float d = f16_to_f32((uint16_t)(r.hdr.x & 0xffffu)), dmin = f16_to_f32((uint16_t)(r.hdr.x >> 16));
-    int sc0, m0, sc1, m1;
+    // sub-blocks 2p, 2p + 1: bytes (2p) & 3, +1 of the 6-bit fields (p < 2), or
+    // of the split fields (p >= 2)
     const int p = r.cc >> 1;
-    Chunk<HX_Q4_K>::scale_min(r.hdr, 2 * p, sc0, m0);
-    Chunk<HX_Q4_K>::scale_min(r.hdr, 2 * p + 1, sc1, m1);
-    return d * ((float)sc0 * (lo - 1024.0f * xs[0]) + (float)sc1 * (hi - 1024.0f * xs[1])) -
-           dmin * ((float)m0 * xs[0] + (float)m1 * xs[1]);
+    const uint32_t sh = 16u * (uint32_t)(p & 1);
+    const uint32_t a0 = r.hdr.y >> sh, a1 = r.hdr.z >> sh, a2 = r.hdr.w >> sh;
+    const uint32_t scp = p < 2 ? a0 & 0x3F3Fu : (a2 & 0x0F0Fu) | ((a0 >> 2) & 0x3030u);
+    const uint32_t mp = p < 2 ? a1 & 0x3F3Fu : ((a2 >> 4) & 0x0F0Fu) | ((a1 >> 2) & 0x3030u);
+    const float sc0 = (float)(scp & 0xffu), sc1 = (float)((scp >> 8) & 0xffu);
+    const float m0 = (float)(mp & 0xffu), m1 = (float)((mp >> 8) & 0xffu);
+    return d * (sc0 * (lo - 1024.0f * xs[0]) + (sc1 * 0.0625f) * (hi - 1024.0f * xs[1])) -
+           dmin * (m0 * xs[0] + m1 * xs[1]);
   }
 };
 
@@ -201,7 +212,13 @@ struct DChunk<HX_Q6_K> {
     }
     x_sums(xp, xs);
   }
+  // quarters 0, 1: code = low nibble | qh bits << 4 as 1024 + code; quarters
+  // 2, 3: high nibble masked in place, qh bits placed above it, as
+  // 1024 + 16 code (exact in f16: < 2048), the 1/16 going into the scale.
+  // One v_and_or_b32 per merge.
   HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs) {
+    const uint32_t kmagic = vconst<0x64006400u>(), klo = vconst<0x000F000Fu>(), khi = vconst<0x00F000F0u>();
+    const uint32_t k30 = vconst<0x00300030u>(), k300 = vconst<0x03000300u>();
     const uint32_t l0[2] = {r.l0.x, r.l0.y}, l1[2] = {r.l1.x, r.l1.y}, hh[2] = {r.h.x, r.h.y};
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -210,21 +227,24 @@ struct DChunk<HX_Q6_K> {
       for (int par = 0; par < 2; par++) {   // byte pairs (0,2) then (1,3)
         const int sh = 8 * par;
         const uint32_t a0 = l0[w] >> sh, a1 = l1[w] >> sh, h = hh[w] >> sh;
-        const uint32_t q0 = nib02(a0) | ((h << 4) & 0x00300030u);
-        const uint32_t q1 = nib02(a1) | ((h << 2) & 0x00300030u);
-        const uint32_t q2 = nib02(a0 >> 4) | (h & 0x00300030u);
-        const uint32_t q3 = nib02(a1 >> 4) | ((h >> 2) & 0x00300030u);
+        const uint32_t h4 = h << 4, h2 = h << 2;
+        const uint32_t q0 = and_or(h4, k30, and_or(a0, klo, kmagic));
+        const uint32_t q1 = and_or(h2, k30, and_or(a1, klo, kmagic));
+        const uint32_t q2 = and_or(h4, k300, and_or(a0, khi, kmagic));
+        const uint32_t q3 = and_or(h2, k300, and_or(a1, khi, kmagic));
         acc[0] = dot2(q0, xp[0 + 2 * w + par], acc[0]);
         acc[1] = dot2(q1, xp[4 + 2 * w + par], acc[1]);
         acc[2] = dot2(q2, xp[8 + 2 * w + par], acc[2]);
         acc[3] = dot2(q3, xp[12 + 2 * w + par], acc[3]);
       }
     }
+    // sum((code - 32) x) = acc - 1056 sum(x) for quarters 0, 1 and
+    // (acc - 1536 sum(x)) / 16 for quarters 2, 3
     float s = 0.f;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const float sc = (float)(int8_t)((r.sc >> (8 * q)) & 0xffu);
-      s = __builtin_fmaf(sc, acc[q] - 1056.0f * xs[q], s);
+      s = q < 2 ? __builtin_fmaf(sc, acc[q] - 1056.0f * xs[q], s) : __builtin_fmaf(sc * 0.0625f, acc[q] - 1536.0f * xs[q], s);
     }
     return f16_to_f32((uint16_t)r.d) * s;
   }
@@ -655,6 +675,131 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
   }
 }
 
+// ----------------------------------------------------------------------------
+// down + combine for T > 1 and K = 512, pipelined: workgroup = RG output rows
+// over every row of h, taken in groups of 24 (24 / NW per wave; NW = 8 keeps
+// the registers under 128, so 4 waves share each SIMD). The weights of
+// group g + 1 (registers, two buffers) and its rows of h (registers, then LDS,
+// two buffers) are loaded while group g's dot products run, so memory and
+// arithmetic overlap; the contributions of all rows stay in LDS and each
+// token's output is their sum in row order (slots by ascending expert, then
+// the shared expert), written directly, with no partial sums to reduce.
+// ----------------------------------------------------------------------------
+constexpr int DP_K = 512;
+template <int FMT, int LPR, int NW>
+__global__ __launch_bounds__(64 * NW) void k_down_pipe(ExpertArgs a) {
+  using D = DChunk<FMT>;
+  using Raw = typename D::Raw;
+  constexpr int ROWS = 24, SPW = ROWS / NW, RG = 64 / LPR, PR = DP_K / 8;
+  static_assert(SPW * NW == ROWS, "the waves split a group's rows of h evenly");
+  constexpr int PPT = ROWS * PR / (64 * NW);   // 16-byte pieces of h per thread and group
+  static_assert(PPT * 64 * NW == ROWS * PR, "a group's rows of h split evenly over the threads");
+  // LDS: rows of h [2][ROWS][DP_K] (f16), then per row of h its token, weight
+  // and expert, then the contributions [rows of h][RG]
+  extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
+  const int T = a.T, NH = a.F + T;
+  const int nh_all = a.F + (a.Is > 0 ? T : 0);
+  const int ng = (nh_all + ROWS - 1) / ROWS;
+  int* stok = (int*)(xl + 2 * ROWS * DP_K);
+  float* swt = (float*)(stok + nh_all);
+  int* sexp = (int*)(swt + nh_all);
+  float* contrib = (float*)(sexp + nh_all);
+  {
+    // the plan's tokens, weights and experts of all rows: PL loads per
+    // thread (3 nh_all <= 512), all issued before any is stored
+    constexpr int PL = 512 / (64 * NW);
+    const int tok0 = 4 + 4 * a.max_slots, n3 = 3 * nh_all;
+    int v[PL];
+#pragma unroll
+    for (int b = 0; b < PL; b++) {
+      const int i = min(b * 64 * NW + (int)threadIdx.x, n3 - 1), part = i / nh_all, r = i - part * nh_all;
+      v[b] = a.plan[tok0 + part * NH + r];
+    }
+#pragma unroll
+    for (int b = 0; b < PL; b++) {
+      const int i = b * 64 * NW + (int)threadIdx.x, part = i / nh_all, r = i - part * nh_all;
+      if (i < n3) (part == 0 ? stok : part == 1 ? (int*)swt : sexp)[r] = v[b];
+    }
+  }
+  __syncthreads();
+  const int lane = lane_id(), wave = threadIdx.x >> 6, rg = lane / LPR, c = lane % LPR;
+  const int n0 = blockIdx.x * RG, row = n0 + rg;
+  Raw ra[SPW], rb[SPW];
+  u32x4v xv[PPT];   // a native vector type, so the array stays in registers across the loop
+  // loads of group g: the wave's SPW weight rows (rows past the end read
+  // row 0 of the group, dropped later) and this thread's pieces of h
+  auto issue = [&](int g, Raw(&raw)[SPW]) __attribute__((always_inline)) {
+    const int h0 = g * ROWS, nh = min(nh_all - h0, ROWS);
+#pragma unroll
+    for (int s = 0; s < SPW; s++) {
+      const int hr = wave + NW * s, hq = hr < nh ? hr : 0;
+      const int e = sexp[h0 + hq];
+      const bool sh = e == a.E;
+      const int K = sh ? a.Is : a.I;
+      D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row < a.H ? row : 0, c < K / 32 ? c : 0, raw[s]);
+    }
+    const int n16 = nh * PR;
+    const uint16_t* src = a.hbf + (int64_t)h0 * a.hstride;
+#pragma unroll
+    for (int b = 0; b < PPT; b++) xv[b] = *(const u32x4v*)(src + 8 * min(b * 64 * NW + (int)threadIdx.x, n16 - 1));
+  };
+  // pieces past the group's rows (copies of its last piece) land in rows of
+  // the buffer that are not read
+  auto stage = [&](int g) __attribute__((always_inline)) {
+    uint16_t* dst = xl + (g & 1) * ROWS * DP_K;
+#pragma unroll
+    for (int b = 0; b < PPT; b++) *(u32x4v*)(dst + 8 * (b * 64 * NW + (int)threadIdx.x)) = xv[b];
+  };
+  auto compute = [&](int g, const Raw(&raw)[SPW]) __attribute__((always_inline)) {
+    const int h0 = g * ROWS, nh = min(nh_all - h0, ROWS);
+    const uint16_t* xb = xl + (g & 1) * ROWS * DP_K;
+#pragma unroll
+    for (int s = 0; s < SPW; s++) {
+      const int hr = wave + NW * s;
+      if (hr >= nh) continue;
+      const int K = sexp[h0 + hr] == a.E ? a.Is : a.I;
+      float p = 0.f;
+      if (c < K / 32) {
+        uint32_t xp[D::NX];
+        float xs[D::NS];
+        D::template load_x<true>((lds_cu16)(xb + hr * DP_K), c, xp, xs);
+        p = D::dot(raw[s], xp, xs);
+      }
+      p = wave_sum<LPR>(p);
+      if (c == 0 && row < a.H) contrib[(h0 + hr) * RG + rg] = swt[h0 + hr] * p;
+    }
+  };
+  // group g's h goes to LDS buffer g & 1 once it has arrived; every wave has
+  // finished group g - 1 (the other user of that buffer) before any passes
+  // the barrier that precedes group g's dot products
+  issue(0, ra);
+  for (int g = 0; g < ng; g += 2) {
+    stage(g);
+    if (g + 1 < ng) issue(g + 1, rb);
+    __syncthreads();
+    compute(g, ra);
+    if (g + 1 >= ng) break;
+    stage(g + 1);
+    if (g + 2 < ng) issue(g + 2, ra);
+    __syncthreads();
+    compute(g + 1, rb);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < T * RG; i += 64 * NW) {
+    const int t = i / RG, r = i % RG;
+    if (n0 + r >= a.H) continue;
+    float y = 0.f;
+#pragma unroll 8
+    for (int hr = 0; hr < nh_all; hr++) y += contrib[hr * RG + r] * (stok[hr] == t ? 1.f : 0.f);
+    if (a.resid) {
+      uint16_t* px = a.resid + (int64_t)t * a.H + n0 + r;
+      *px = f32_to_bf16(bf16_to_f32(*px) + bf16_to_f32(f32_to_bf16(y)));
+    } else {
+      ((uint16_t*)a.y)[(int64_t)t * a.H + n0 + r] = f32_to_bf16(y);
+    }
+  }
+}
+
 // sum of the down kernel's per-group partials, in group order, for T tokens
 __global__ __launch_bounds__(256) void k_down_reduce(ExpertArgs a, int groups) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -734,6 +879,17 @@ static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
   const int groups = down_groups(a.F, a.Is > 0 ? a.T : 0);
   const bool xlds = a.T > 1;   // one token: activations straight from global memory
   if (xlds && a.hstride != (a.I > a.Is ? a.I : a.Is)) return hipErrorInvalidValue;   // rows of h contiguous
+  // every row of h in one workgroup per RG output rows, pipelined over groups,
+  // for at most two groups of rows (measured on MI355X: with more groups the
+  // grouped kernel's extra workgroups hide more latency than the pipeline and
+  // the saved partial-sum pass are worth)
+  if (xlds && nch == DP_K / 32 && a.F + (a.Is > 0 ? a.T : 0) <= 48) {
+    constexpr int LPR = DP_K / 32, RG = 64 / LPR;
+    const int nh_all = a.F + (a.Is > 0 ? a.T : 0);
+    const size_t lds = (size_t)2 * 24 * DP_K * 2 + (size_t)nh_all * (3 + RG) * 4;
+    hipLaunchKernelGGL((k_down_pipe<FMT, LPR, 8>), dim3((a.H + RG - 1) / RG), dim3(512), lds, s, a);
+    return hipGetLastError();
+  }
   // one token with at most 12 rows of h (k <= 11): 3 rows per wave
   const bool small = !xlds && a.F + (a.Is > 0 ? 1 : 0) <= 12;
 #define DD(LPR)                                                                                   \

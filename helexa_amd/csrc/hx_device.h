@@ -31,6 +31,23 @@ HX_DEV void dma16(const void* g, uint32_t lds_base) {
                : "=&s"(save) : "v"(g), "s"(lds_base) : "memory");
 }
 
+// v_and_or_b32 with its two constants in registers (a VOP3 instruction on this
+// target takes no literal operand; left to itself the compiler splits the
+// operation into an and and an or, each with a literal)
+HX_DEV uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(o));
+  return r;
+}
+// a register holding the constant C (not volatile: repeated uses merge and the
+// move leaves loops)
+template <uint32_t C>
+HX_DEV uint32_t vconst() {
+  uint32_t r;
+  asm("v_mov_b32 %0, %1" : "=v"(r) : "i"(C));
+  return r;
+}
+
 HX_DEV float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
 HX_DEV uint16_t f32_to_bf16(float f) {

@@ -318,15 +318,6 @@ HX_DEV void q4k_issue(uint32_t lds0, int st, const Q4kSrc<Q>& src, int kc, int w
   }
 }
 
-// v_and_or_b32 with its two constants in registers (a VOP3 instruction on this
-// target takes no literal operand; left to itself the compiler splits the
-// operation into an and and an or, each with a literal)
-HX_DEV uint32_t and_or(uint32_t x, uint32_t m, uint32_t o) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(o));
-  return r;
-}
-
 // f16 (a, nb) of sub-blocks 4 PAR .. 4 PAR + 3 of a Q4_K superblock header:
 // a = d sc, nb = -dmin m, each one f16 rounding of the exact product (as in
 // h2s(d * (float)sc)); the 6-bit sc and m of the four sub-blocks are
