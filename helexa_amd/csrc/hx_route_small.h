@@ -15,6 +15,7 @@ namespace hx {
 constexpr int HX_SMALL_F = HX_DECODE_MAX_T * HX_MAX_TOPK;
 
 struct alignas(16) RouteSmem {
+  unsigned long long ball[2];  // dispatch of up to 128 entries: each wave's slot starts
   int idx[HX_SMALL_F];       // expert of flat entry f = t*k + j
   float w[HX_SMALL_F];       // routing weight of entry f
   int pos[HX_SMALL_F];       // permuted position of entry f
@@ -262,44 +263,55 @@ HX_DEV void route_small_lds(const float* logits, int E1, int E, int k, bool norm
   if (tid == 0) sm.nroute = 0;
   for (int t = wave; t < T; t += nw) route_token_lds(logits + (int64_t)t * E1, E, k, norm, want_sgw, t, sm);
   __syncthreads();
-  if (F <= 64) {
-    // entry f in lane f of wave 0. Stable sort by key (expert, f): position =
-    // number of smaller keys, counted from the keys in LDS (4 per read, all
-    // reads independent). Then, in sorted order, a position starts a slot when
-    // its expert differs from the previous one: the slot index is the number of
-    // starts at or before it (ballot + mbcnt) and the slot ends at the next start.
+  if (F <= 128) {
+    // entry f in lane f % 64 of wave f / 64. Stable sort by key (expert, f):
+    // position = number of smaller keys, counted from the keys in LDS (4 per
+    // read, all reads independent). Then, in sorted order, a position starts a
+    // slot when its expert differs from the previous one: the slot index is the
+    // number of starts at or before it (ballot + mbcnt, plus wave 0's count for
+    // wave 1) and the slot ends at the next start.
     const int F4 = (F + 3) & ~3;
-    if (tid < F4) sm.perm[tid] = tid < F ? (sm.idx[tid] << 6) | tid : 0x7fffffff;   // experts < 1024
+    if (tid < F4) sm.perm[tid] = tid < F ? (sm.idx[tid] << 7) | tid : 0x7fffffff;   // experts < 2^24
     __syncthreads();
-    if (wave == 0) {
-      const int lane = lane_id();
-      const int key = lane < F ? sm.perm[lane] : 0x7fffffff;
-      int pos = 0;
+    const int lane = lane_id(), f0 = 64 * wave + lane;
+    const bool mine = wave < 2 && f0 < F;
+    int pos = 0;
+    if (wave < 2) {
+      const int key = mine ? sm.perm[f0] : 0x7fffffff;
       for (int j = 0; j < F4; j += 4) {
         const int4 q = *(const int4*)(sm.perm + j);
         pos += (q.x < key) + (q.y < key) + (q.z < key) + (q.w < key);
       }
-      __builtin_amdgcn_wave_barrier();   // every read above precedes the writes below
-      if (lane < F) {
-        sm.pos[lane] = pos;
-        sm.perm[pos] = lane;
-      }
-      __builtin_amdgcn_wave_barrier();
-      const int f = lane < F ? sm.perm[lane] : 0;
-      const int e = lane < F ? sm.idx[f] : -1;
-      const int eprev = __builtin_amdgcn_update_dpp(-1, e, 0x138, 0xf, 0xf, false);   // wave_shr:1, lane 0 gets -1
-      const bool start = lane < F && e != eprev;
-      const unsigned long long sb = __ballot(start);
-      if (lane < F) sm.first[f] = start;
+    }
+    __syncthreads();   // every read of the keys precedes the writes below
+    if (mine) {
+      sm.pos[f0] = pos;
+      sm.perm[pos] = f0;
+    }
+    __syncthreads();
+    int f = 0, e = -1;
+    bool start = false;
+    if (mine) {   // sorted position f0
+      f = sm.perm[f0];
+      e = sm.idx[f];
+      start = f0 == 0 || e != sm.idx[sm.perm[f0 - 1]];
+    }
+    const unsigned long long sb = __ballot(start);
+    if (wave < 2 && lane == 0) sm.ball[wave] = sb;
+    __syncthreads();
+    if (wave < 2) {
+      const unsigned long long b0 = sm.ball[0], b1 = F > 64 ? sm.ball[1] : 0ull;
+      if (mine) sm.first[f] = start;
       if (start) {
-        const int slot = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(sb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sb, 0u));
+        const int slot = (wave ? __popcll(b0) : 0) +
+                         (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(sb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sb, 0u));
         const unsigned long long later = sb & ~((2ull << lane) - 1ull);
-        const int next = later ? __ffsll((long long)later) - 1 : F;
+        const int next = later ? 64 * wave + __ffsll((long long)later) - 1 : (wave == 0 && b1 ? 64 + __ffsll((long long)b1) - 1 : F);
         sm.slots[3 * slot + 0] = e;
-        sm.slots[3 * slot + 1] = lane;
-        sm.slots[3 * slot + 2] = next - lane;
+        sm.slots[3 * slot + 1] = f0;
+        sm.slots[3 * slot + 2] = next - f0;
       }
-      if (lane == 0) sm.nroute = __popcll(sb);
+      if (tid == 0) sm.nroute = __popcll(b0) + __popcll(b1);
     }
     __syncthreads();
     return;

@@ -202,6 +202,23 @@ def test_forward_c2_decode_q8_0(c2, T):
     assert rel_err(got, ref) <= TOL_BF16
 
 
+@pytest.mark.parametrize("pattern", [[0] * 8, [0, 0, 0, 0, 0, 1, 1, 2], [0, 1, 0, 1, 0, 1, 0, 1]])
+def test_forward_c2_decode_repeated_tokens(c2, pattern):
+    """tokens that share experts: slots of several rows, which for T = 8 and
+    k = 10 (80 assignments) cross the 64-entry boundary of the dispatch"""
+    base = c2.x(3, seed=77)
+    x = base[torch.tensor(pattern, device=base.device)].contiguous()
+    r = c2.block.route(x)
+    _, _, ix, wt = c2.oracle.route(x_np(x))
+    assert np.array_equal(r["topk_idx"].cpu().numpy(), ix)
+    assert np.array_equal(r["topk_w"].cpu().numpy().view(np.uint32), wt.view(np.uint32))
+    perm, offs, inv = O.dispatch(ix, c2.cfg.num_experts)
+    assert np.array_equal(r["perm"].cpu().numpy(), perm)
+    assert np.array_equal(r["offsets"].cpu().numpy(), offs)
+    got = c2.block.forward(x).float().cpu().numpy()
+    assert rel_err(got, c2.oracle.forward(x_np(x))) <= TOL_BF16
+
+
 def test_forward_q4_k_m_prefill_sampled_tokens():
     hx, synth = _hx()
     c = Case(synth.A3B, synth.FMT_Q4_K_M, 11, O.BF16)
