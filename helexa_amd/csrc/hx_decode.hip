@@ -282,7 +282,7 @@ HX_DEV void touch_sink(const ExpertArgs& a, Touch t) {
 // batched path out, which keeps its register count and occupancy)
 template <int FMT, int LPR, int NR, bool BATCH = true>
 HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U, int rows, int row0, int count,
-                         const int* tok, const int* hrow) {
+                         const int* tok, const int* hrow, const uint32_t* xcv = nullptr) {
   using D = DChunk<FMT>;
   constexpr int RG = 64 / LPR;
   const int c = lane_id() % LPR, K = a.H;
@@ -325,23 +325,40 @@ HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U
       return;
     }
   }
-  // token j's activations are loaded as raw bf16 before token j - 1's dot
-  // products (token 0's together with the weights), so each load overlaps work
-  uint4 xr[4];
+  // token j's activations are loaded before token j - 1's dot products
+  // (token 0's together with the weights), so each load overlaps work: already
+  // converted (pairs + sums, written by the router kernel) when a.xcv is set,
+  // else raw bf16
+  const bool cv = xcv != nullptr;
+  u32x4v xr[5];
+  auto xload = [&](int t) __attribute__((always_inline)) {
+    if (cv) {
+      const u32x4v* q = (const u32x4v*)(xcv + ((int64_t)t * (K / 32) + c) * HX_XCV_WORDS);
 #pragma unroll
-  for (int g = 0; g < 4; g++) xr[g] = *(const uint4*)((const uint16_t*)a.x + (int64_t)tok[0] * K + D::x_group_off(c, g));
+      for (int g = 0; g < 5; g++) xr[g] = q[g];
+    } else {
+#pragma unroll
+      for (int g = 0; g < 4; g++) xr[g] = *(const u32x4v*)((const uint16_t*)a.x + (int64_t)t * K + D::x_group_off(c, g));
+    }
+  };
+  xload(tok[0]);
   __builtin_amdgcn_sched_barrier(0);   // no weight arithmetic above these loads
   for (int j = 0; j < count; j++) {
     uint32_t xp[D::NX];
     float xs[D::NS];
-#pragma unroll
-    for (int g = 0; g < 4; g++) x_pairs_bf16v(xr[g], xp + 4 * g);
-    D::x_sums(xp, xs);
-    if (j + 1 < count) {
+    if (cv) {
 #pragma unroll
       for (int g = 0; g < 4; g++)
-        xr[g] = *(const uint4*)((const uint16_t*)a.x + (int64_t)tok[j + 1] * K + D::x_group_off(c, g));
+#pragma unroll
+        for (int i = 0; i < 4; i++) xp[4 * g + i] = xr[g][i];
+#pragma unroll
+      for (int i = 0; i < D::NS; i++) xs[i] = __uint_as_float(xr[4][i]);
+    } else {
+#pragma unroll
+      for (int g = 0; g < 4; g++) x_pairs_bf16v(make_uint4(xr[g][0], xr[g][1], xr[g][2], xr[g][3]), xp + 4 * g);
+      D::x_sums(xp, xs);
     }
+    if (j + 1 < count) xload(tok[j + 1]);
 #pragma unroll
     for (int g = 0; g < NR; g++) {
       const int row = row0 + g * RG;
@@ -364,14 +381,34 @@ HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U
 // T == 1 the shared expert is computed inside K2 while it routes.
 // ----------------------------------------------------------------------------
 template <int FMT, int LPR, int NR, bool RBF, int TT>
-__global__ __launch_bounds__(256) void k_router_dec(RouterArgs r, ExpertArgs a, int nrb) {
+__global__ __launch_bounds__(256) void k_router_dec(RouterArgs r, ExpertArgs a, int nrb, int nsb) {
   const int wave = threadIdx.x >> 6;
   if ((int)blockIdx.x < nrb) {
     router_rows<true, RBF, TT, 1>(r, blockIdx.x * 4 + wave, 0);
     return;
   }
+  if ((int)blockIdx.x >= nrb + nsb) {
+    // token t = 4 (block - nrb - nsb) + wave: each 32-wide chunk converted once
+    // to the expert dot's f16 pairs and activation sums, for k_gate_up_plan
+    using D = DChunk<FMT>;
+    const int t = 4 * ((int)blockIdx.x - nrb - nsb) + wave, nc = a.H / 32;
+    if (t >= a.T) return;
+    for (int c = lane_id(); c < nc; c += 64) {
+      uint32_t xp[D::NX];
+      float xs[D::NS];
+      D::template load_x<false>((const uint16_t*)a.x + (int64_t)t * a.H, c, xp, xs);
+      u32x4v* q = (u32x4v*)(a.xcv + ((int64_t)t * nc + c) * HX_XCV_WORDS);
+#pragma unroll
+      for (int g = 0; g < 4; g++) q[g] = u32x4v{xp[4 * g], xp[4 * g + 1], xp[4 * g + 2], xp[4 * g + 3]};
+      u32x4v sv = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int i = 0; i < D::NS; i++) sv[i] = __float_as_uint(xs[i]);
+      q[4] = sv;
+    }
+    return;
+  }
   constexpr int RG = 64 / LPR;
-  const int sb = blockIdx.x - nrb, nsb = gridDim.x - nrb;
+  const int sb = blockIdx.x - nrb;
   const int64_t per = (a.sdown.mat_bytes + nsb - 1) / nsb;
   const int64_t lo = (int64_t)sb * per, n = lo + per < a.sdown.mat_bytes ? per : a.sdown.mat_bytes - lo;
   const Touch pf = n > 0 ? touch_lines(a.sdown.base + lo, n) : Touch{0u, 0u};
@@ -540,7 +577,7 @@ __global__ __launch_bounds__(256) void k_gate_up_plan(ExpertArgs a) {
   const int wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * 4 + wave) * (RG * NR) + lane_id() / LPR;
   if (row0 - lane_id() / LPR < a.I)
-    gate_up_rows<FMT, LPR, NR, false>(a, a.gate.mat(e), a.up.mat(e), a.I, row0, count, tok, hrow);
+    gate_up_rows<FMT, LPR, NR, false>(a, a.gate.mat(e), a.up.mat(e), a.I, row0, count, tok, hrow, a.xcv);
 }
 
 // ----------------------------------------------------------------------------
@@ -831,7 +868,8 @@ static hipError_t router_dec_fmt(const RouterArgs& r, const ExpertArgs& a, bool 
   {                                                                                         \
     constexpr int RG = 64 / LPR;                                                            \
     const int nsb = a.Is > 0 && a.T > 1 ? (a.Is + 4 * RG * NR - 1) / (4 * RG * NR) : 0;    \
-    hipLaunchKernelGGL((k_router_dec<FMT, LPR, NR, RB, TT>), dim3(nrb + nsb), dim3(256), 0, s, r, a, nrb); \
+    const int ncb = a.xcv && a.T > 1 ? (a.T + 3) / 4 : 0;                                   \
+    hipLaunchKernelGGL((k_router_dec<FMT, LPR, NR, RB, TT>), dim3(nrb + nsb + ncb), dim3(256), 0, s, r, a, nrb, nsb); \
   }
 #define RD_T(LPR, RB) { if (r.T <= 1) RD(LPR, RB, 1) else if (r.T <= 2) RD(LPR, RB, 2) else if (r.T <= 4) RD(LPR, RB, 4) else RD(LPR, RB, 8) }
 #define RD_R(LPR) { if (rbf) RD_T(LPR, true) else RD_T(LPR, false) }

@@ -104,6 +104,8 @@ struct ExpertArgs {
   int hstride;
   uint16_t* hbf;       // [(F+T), hstride] f16 copy (prefill: elements swizzled in groups of 4)
   uint16_t* xh;        // [T, H] f16 tokens in the swizzled order (prefill)
+  uint32_t* xcv;       // [T][H / 32][HX_XCV_WORDS] decode, T > 1: each 32-wide chunk of a token as
+                       // the expert dot's f16 pairs (16 words) + its activation sums (4 floats)
   void* obuf;          // [(F+T), H] weighted expert outputs (prefill): bf16 for bf16
                        // activations, f32 for f32 ones
   const int32_t* inv;
@@ -121,6 +123,7 @@ struct ExpertArgs {
 };
 
 // rows of h one decode down workgroup takes (4 waves x 6 rows each)
+constexpr int HX_XCV_WORDS = 20;
 constexpr int HX_DOWN_ROWS = 24;
 __host__ __device__ inline int down_groups(int F, int T) { return (F + T + HX_DOWN_ROWS - 1) / HX_DOWN_ROWS; }
 

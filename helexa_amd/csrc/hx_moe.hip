@@ -73,7 +73,7 @@ struct hx_moe {
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 struct WsLayout {
-  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, hist, hbuf, hbf, xh, obuf, xn, ym, dpart,
+  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, hist, hbuf, hbf, xh, xcv, obuf, xn, ym, dpart,
       wpos, total;
   int hstride, max_slots, max_tiles;
 };
@@ -110,6 +110,7 @@ static WsLayout ws_layout(const hx_moe* m, int64_t T) {
   const size_t act = m->cfg.act_dtype == HX_BF16 ? 2 : 4;
   L.obuf = decode ? 0 : take(act * (F + T) * H);
   L.xh = decode ? 0 : take(sizeof(uint16_t) * T * H);
+  L.xcv = decode && T > 1 ? take(sizeof(uint32_t) * (size_t)T * (H / 32) * HX_XCV_WORDS) : 0;
   L.xn = take(act * T * H);
   L.ym = take(act * T * H);
   L.dpart = decode ? take(sizeof(float) * (size_t)down_groups((int)F, (int)T) * T * H) : 0;
@@ -387,6 +388,7 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
   a.hbf = L.hbf ? (uint16_t*)(ws + L.hbf) : nullptr;
   a.obuf = L.obuf ? (void*)(ws + L.obuf) : nullptr;
   a.xh = L.xh ? (uint16_t*)(ws + L.xh) : nullptr;
+  a.xcv = L.xcv ? (uint32_t*)(ws + L.xcv) : nullptr;
   a.inv = d.inv;
   a.topk_idx = d.topk_idx;
   a.y = y;
