@@ -585,6 +585,35 @@ __global__ __launch_bounds__(256) void k_gate_up_plan(ExpertArgs a) {
 // contributions w * (row . h) go to LDS and are summed in slot order (experts
 // ascending, then the shared expert).
 // ----------------------------------------------------------------------------
+// The expert dot's form of one 32-wide chunk of activations: its f16 pairs
+// (16 words) and activation sums (up to 4 floats), HX_XCV_WORDS words in all.
+typedef __attribute__((address_space(3))) u32x4v lds_v4;
+template <class D>
+HX_DEV void chunk_record(const u32x4v (&g4)[4], lds_v4* dst) {
+  uint32_t xp[D::NX];
+  float xs[D::NS];
+#pragma unroll
+  for (int g = 0; g < 4; g++) pairs_from_f16x8(make_uint4(g4[g][0], g4[g][1], g4[g][2], g4[g][3]), xp + 4 * g);
+  D::x_sums(xp, xs);
+#pragma unroll
+  for (int g = 0; g < 4; g++) dst[g] = u32x4v{xp[4 * g], xp[4 * g + 1], xp[4 * g + 2], xp[4 * g + 3]};
+  u32x4v sv = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int i = 0; i < D::NS; i++) sv[i] = __float_as_uint(xs[i]);
+  dst[4] = sv;
+}
+template <class D>
+HX_DEV void chunk_from_record(const lds_v4* src, uint32_t* xp, float* xs) {
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    const u32x4v v = src[g];
+    xp[4 * g] = v[0]; xp[4 * g + 1] = v[1]; xp[4 * g + 2] = v[2]; xp[4 * g + 3] = v[3];
+  }
+  const u32x4v v = src[4];
+#pragma unroll
+  for (int i = 0; i < D::NS; i++) xs[i] = __uint_as_float(v[i]);
+}
+
 // XLDS: the group's rows of h are staged in LDS first (many rows: each row of
 // h is read by every output-row block, and the activations then stay out of
 // the registers while the weight loads are in flight). Otherwise (one token)
@@ -599,11 +628,16 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
   constexpr int RG = 64 / LPR;
   constexpr int ROWS = NW * SPW;   // rows of h per group (one pass per wave)
   static_assert(ROWS <= HX_DOWN_ROWS, "groups of at most HX_DOWN_ROWS rows of h");
-  // LDS: the group's rows of h (f16, Kmax each; XLDS only), then per row its
-  // token, weight and expert, then the contributions [ROWS][RG]
+  // CV (K = 512): the staged rows are converted once per workgroup, in place,
+  // into one chunk record per (row, chunk) (the RG lanes of a wave that share
+  // a chunk would otherwise each convert it)
+  constexpr bool CV = XLDS && LPR == 16;
+  // LDS: the group's rows of h (f16, Kmax each; XLDS only; with CV the larger
+  // chunk records), then per row its token, weight and expert, then the
+  // contributions [ROWS][RG]
   extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
   const int Kmax = XLDS ? (a.I > a.Is ? a.I : a.Is) : 0;
-  int* stok = (int*)(xl + ROWS * Kmax);
+  int* stok = (int*)((uint8_t*)xl + (CV ? ROWS * LPR * HX_XCV_WORDS * 4 : ROWS * Kmax * 2));
   float* swt = (float*)(stok + ROWS);
   int* sexp = (int*)(swt + ROWS);
   float* contrib = (float*)(sexp + ROWS);
@@ -663,6 +697,25 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
       dma16(src + 8 * min(q0 + lane, n16 - 1), xbase + 16u * (uint32_t)q0);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    if constexpr (CV) {
+      // item q = (row q / 16, chunk q % 16): every thread reads its items' raw
+      // groups, then (after the barrier) writes their records over the rows
+      constexpr int IPT = (ROWS * LPR + 64 * NW - 1) / (64 * NW);
+      u32x4v g4[IPT][4];
+#pragma unroll
+      for (int it = 0; it < IPT; it++) {
+        const int q = min(it * 64 * NW + (int)threadIdx.x, nh * LPR - 1), hr = q / LPR, cc = q % LPR;
+#pragma unroll
+        for (int g = 0; g < 4; g++) g4[it][g] = *(const lds_v4*)(xl + hr * Kmax + D::x_group_off(cc, g));
+      }
+      __syncthreads();
+#pragma unroll
+      for (int it = 0; it < IPT; it++) {
+        const int q = it * 64 * NW + (int)threadIdx.x;
+        if (q < nh * LPR) chunk_record<D>(g4[it], (lds_v4*)xl + q * (HX_XCV_WORDS / 4));
+      }
+      __syncthreads();
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -677,7 +730,9 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
     if (c < K / 32) {
       uint32_t xp[D::NX];
       float xs[D::NS];
-      if constexpr (XLDS) {
+      if constexpr (CV) {
+        chunk_from_record<D>((const lds_v4*)xl + (hr * LPR + c) * (HX_XCV_WORDS / 4), xp, xs);
+      } else if constexpr (XLDS) {
         D::template load_x<true>((lds_cu16)(xl + hr * Kmax), c, xp, xs);
       } else {
 #pragma unroll
@@ -727,17 +782,19 @@ template <int FMT, int LPR, int NW>
 __global__ __launch_bounds__(64 * NW) void k_down_pipe(ExpertArgs a) {
   using D = DChunk<FMT>;
   using Raw = typename D::Raw;
-  constexpr int ROWS = 24, SPW = ROWS / NW, RG = 64 / LPR, PR = DP_K / 8;
+  constexpr int ROWS = 24, SPW = ROWS / NW, RG = 64 / LPR, NC = DP_K / 32;
   static_assert(SPW * NW == ROWS, "the waves split a group's rows of h evenly");
-  constexpr int PPT = ROWS * PR / (64 * NW);   // 16-byte pieces of h per thread and group
-  static_assert(PPT * 64 * NW == ROWS * PR, "a group's rows of h split evenly over the threads");
-  // LDS: rows of h [2][ROWS][DP_K] (f16), then per row of h its token, weight
-  // and expert, then the contributions [rows of h][RG]
+  static_assert(ROWS * NC <= 64 * NW, "one chunk of a group's rows of h per thread");
+  constexpr int REC = HX_XCV_WORDS / 4;   // 16-byte words per chunk record
+  // LDS: chunk records of the rows of h [2][ROWS][NC] (pairs + sums, converted
+  // once per workgroup), then per row of h its token, weight and expert, then
+  // the contributions [rows of h][RG]
   extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
   const int T = a.T, NH = a.F + T;
   const int nh_all = a.F + (a.Is > 0 ? T : 0);
   const int ng = (nh_all + ROWS - 1) / ROWS;
-  int* stok = (int*)(xl + 2 * ROWS * DP_K);
+  lds_v4* const rec = (lds_v4*)xl;
+  int* stok = (int*)((uint8_t*)xl + 2 * ROWS * NC * HX_XCV_WORDS * 4);
   float* swt = (float*)(stok + nh_all);
   int* sexp = (int*)(swt + nh_all);
   float* contrib = (float*)(sexp + nh_all);
@@ -762,9 +819,10 @@ __global__ __launch_bounds__(64 * NW) void k_down_pipe(ExpertArgs a) {
   const int lane = lane_id(), wave = threadIdx.x >> 6, rg = lane / LPR, c = lane % LPR;
   const int n0 = blockIdx.x * RG, row = n0 + rg;
   Raw ra[SPW], rb[SPW];
-  u32x4v xv[PPT];   // a native vector type, so the array stays in registers across the loop
+  u32x4v xv[4];   // a native vector type, so the array stays in registers across the loop
   // loads of group g: the wave's SPW weight rows (rows past the end read
-  // row 0 of the group, dropped later) and this thread's pieces of h
+  // row 0 of the group, dropped later) and this thread's chunk of h (item
+  // q = thread: row q / NC, chunk q % NC; past the end, the group's last row)
   auto issue = [&](int g, Raw(&raw)[SPW]) __attribute__((always_inline)) {
     const int h0 = g * ROWS, nh = min(nh_all - h0, ROWS);
 #pragma unroll
@@ -775,21 +833,18 @@ __global__ __launch_bounds__(64 * NW) void k_down_pipe(ExpertArgs a) {
       const int K = sh ? a.Is : a.I;
       D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row < a.H ? row : 0, c < K / 32 ? c : 0, raw[s]);
     }
-    const int n16 = nh * PR;
-    const uint16_t* src = a.hbf + (int64_t)h0 * a.hstride;
+    const int q = min((int)threadIdx.x, nh * NC - 1), hr = q / NC, cc = q % NC;
+    const uint16_t* src = a.hbf + (int64_t)(h0 + hr) * a.hstride;
 #pragma unroll
-    for (int b = 0; b < PPT; b++) xv[b] = *(const u32x4v*)(src + 8 * min(b * 64 * NW + (int)threadIdx.x, n16 - 1));
+    for (int g = 0; g < 4; g++) xv[g] = *(const u32x4v*)(src + D::x_group_off(cc, g));
   };
-  // pieces past the group's rows (copies of its last piece) land in rows of
-  // the buffer that are not read
+  // records past the group's rows land in slots that are not read
   auto stage = [&](int g) __attribute__((always_inline)) {
-    uint16_t* dst = xl + (g & 1) * ROWS * DP_K;
-#pragma unroll
-    for (int b = 0; b < PPT; b++) *(u32x4v*)(dst + 8 * (b * 64 * NW + (int)threadIdx.x)) = xv[b];
+    if ((int)threadIdx.x < ROWS * NC) chunk_record<D>(xv, rec + ((g & 1) * ROWS * NC + (int)threadIdx.x) * REC);
   };
   auto compute = [&](int g, const Raw(&raw)[SPW]) __attribute__((always_inline)) {
     const int h0 = g * ROWS, nh = min(nh_all - h0, ROWS);
-    const uint16_t* xb = xl + (g & 1) * ROWS * DP_K;
+    const lds_v4* xb = rec + (g & 1) * ROWS * NC * REC;
 #pragma unroll
     for (int s = 0; s < SPW; s++) {
       const int hr = wave + NW * s;
@@ -799,7 +854,7 @@ __global__ __launch_bounds__(64 * NW) void k_down_pipe(ExpertArgs a) {
       if (c < K / 32) {
         uint32_t xp[D::NX];
         float xs[D::NS];
-        D::template load_x<true>((lds_cu16)(xb + hr * DP_K), c, xp, xs);
+        chunk_from_record<D>(xb + (hr * NC + c) * REC, xp, xs);
         p = D::dot(raw[s], xp, xs);
       }
       p = wave_sum<LPR>(p);
@@ -924,7 +979,7 @@ static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
   if (xlds && nch == DP_K / 32 && a.F + (a.Is > 0 ? a.T : 0) <= 48) {
     constexpr int LPR = DP_K / 32, RG = 64 / LPR;
     const int nh_all = a.F + (a.Is > 0 ? a.T : 0);
-    const size_t lds = (size_t)2 * 24 * DP_K * 2 + (size_t)nh_all * (3 + RG) * 4;
+    const size_t lds = (size_t)2 * 24 * (DP_K / 32) * HX_XCV_WORDS * 4 + (size_t)nh_all * (3 + RG) * 4;
     hipLaunchKernelGGL((k_down_pipe<FMT, LPR, 8>), dim3((a.H + RG - 1) / RG), dim3(512), lds, s, a);
     return hipGetLastError();
   }
@@ -934,7 +989,8 @@ static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
   {                                                                                               \
     constexpr int RG = 64 / LPR;                                                                  \
     const int Kmax = xlds ? (a.I > a.Is ? a.I : a.Is) : 0;                                        \
-    size_t lds = (size_t)HX_DOWN_ROWS * Kmax * 2 + (size_t)HX_DOWN_ROWS * (3 + RG) * 4;           \
+    size_t lds = (size_t)HX_DOWN_ROWS * (Kmax == 512 ? 16 * HX_XCV_WORDS * 4 : Kmax * 2) +         \
+                 (size_t)HX_DOWN_ROWS * (3 + RG) * 4;                                              \
     const dim3 grid((a.H + RG - 1) / RG, groups);                                                   \
     if (xlds) hipLaunchKernelGGL((k_down_dec<FMT, LPR, 6, 4, true>), grid, dim3(256), lds, s, a);   \
     else if (small) hipLaunchKernelGGL((k_down_dec<FMT, LPR, 3, 4, false>), grid, dim3(256), lds, s, a); \
