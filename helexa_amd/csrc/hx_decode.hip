@@ -972,11 +972,10 @@ static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
   const int groups = down_groups(a.F, a.Is > 0 ? a.T : 0);
   const bool xlds = a.T > 1;   // one token: activations straight from global memory
   if (xlds && a.hstride != (a.I > a.Is ? a.I : a.Is)) return hipErrorInvalidValue;   // rows of h contiguous
-  // every row of h in one workgroup per RG output rows, pipelined over groups,
-  // for at most two groups of rows (measured on MI355X: with more groups the
-  // grouped kernel's extra workgroups hide more latency than the pipeline and
-  // the saved partial-sum pass are worth)
-  if (xlds && nch == DP_K / 32 && a.F + (a.Is > 0 ? a.T : 0) <= 48) {
+  // every row of h in one workgroup per RG output rows, pipelined over groups
+  // (measured on MI355X at T = 4 and 8: faster than the grouped kernel + the
+  // partial-sum pass); the plan of all rows is read in one pass (3 rows <= 512)
+  if (xlds && nch == DP_K / 32 && 3 * (a.F + (a.Is > 0 ? a.T : 0)) <= 512) {
     constexpr int LPR = DP_K / 32, RG = 64 / LPR;
     const int nh_all = a.F + (a.Is > 0 ? a.T : 0);
     const size_t lds = (size_t)2 * 24 * (DP_K / 32) * HX_XCV_WORDS * 4 + (size_t)nh_all * (3 + RG) * 4;
