@@ -347,7 +347,8 @@ HX_DEV void q4k_scales(const uint4& hdr, uint32_t kbyte, uint32_t kmagic, h2_t* 
   nb[3] = __builtin_shufflevector(m13, m13, 1, 1);
 }
 
-template <class Q, int PAR>   // chunk parity: sub-blocks 4 PAR .. 4 PAR + 3 of the superblock
+// MT: 16-row M sub-tiles in use (the tile's rows rounded up to 16)
+template <class Q, int PAR, int MT>   // chunk parity: sub-blocks 4 PAR .. 4 PAR + 3 of the superblock
 HX_DEV void q4k_compute(const lds_u8* st, f32x4_t (*accg)[Q::FPW_], f32x4_t (*accu)[Q::FPW_], int wave, int l16, int kq,
                         uint32_t knib, uint32_t kbyte, uint32_t kmagic) {
   constexpr int NF = Q::FPW_;
@@ -379,7 +380,7 @@ HX_DEV void q4k_compute(const lds_u8* st, f32x4_t (*accg)[Q::FPW_], f32x4_t (*ac
                                                      fma_pair(and_or(w1 >> 8, knib, kmagic), a[f][s], nb[f][s], off)));
     }
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++) {
+    for (int mt = 0; mt < MT; mt++) {
       const int row = 16 * mt + l16, seg = 4 * s + kq;
       const f16x8_t av = __builtin_bit_cast(f16x8_t, *(const __attribute__((address_space(3))) u32x4_t*)(st + row * 256 + ((seg ^ l16) << 4)));
 #pragma unroll
@@ -409,9 +410,62 @@ HX_DEV void q4k_wait(int ahead, int wave_u) {
   }
 }
 
+// the K loop and epilogue of k_gate_up_q4k for tiles of at most 16 MT rows:
+// MFMAs and activation-fragment reads only for the sub-tiles in use (the DMAs
+// still move all 64 rows, so every wave's DMA count, which the waits rely on,
+// does not depend on the tile)
+template <class Q, int MT>
+HX_DEV void q4k_main(const ExpertArgs& a, uint8_t* ring, const Q4kSrc<Q>& src, int nk, int rows, int p0, int n0,
+                     int wave, int wave_u, int l16, int kq, uint32_t knib, uint32_t kbyte, uint32_t kmagic) {
+  constexpr int FPW = Q::FPW_;
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)ring;
+  f32x4_t accg[MT][FPW], accu[MT][FPW];
+#pragma unroll
+  for (int i = 0; i < MT; i++)
+#pragma unroll
+    for (int j = 0; j < FPW; j++) {
+      accg[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      accu[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+  for (int c = 0; c < Q::NST - 1; c++)
+    if (c < nk) q4k_issue<Q>(lds0, c, src, c, wave_u);
+  for (int kc = 0; kc < nk; kc++) {
+    const int ahead = min(Q::NST - 2, nk - 1 - kc);
+    q4k_wait<Q>(ahead, wave_u);
+    __syncthreads();   // chunk kc is in LDS for every wave; stage (kc - 1) % NST is free
+    if (kc + Q::NST - 1 < nk) q4k_issue<Q>(lds0, (kc + Q::NST - 1) % Q::NST, src, kc + Q::NST - 1, wave_u);
+    const lds_u8* st = (const lds_u8*)ring + (kc % Q::NST) * Q::STAGE;
+    if (kc & 1) q4k_compute<Q, 1, MT>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
+    else q4k_compute<Q, 0, MT>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
+  }
+  // the 16 MT x COLS f16 rows of h go through LDS (columns in the swizzled
+  // order, row pitch COLS + 8) and out as 16-byte pieces
+  __syncthreads();   // every wave is done with the ring
+  constexpr int OP = Q::COLS + 8;
+  _Float16* ot = (_Float16*)ring;
+#pragma unroll
+  for (int j = 0; j < FPW; j++) {
+    const int col = swz(16 * (FPW * wave + j) + l16);
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int m = 16 * mt + 4 * kq + i;
+        ot[m * OP + col] = (_Float16)(siluf_(accg[mt][j][i]) * accu[mt][j][i]);
+      }
+  }
+  __syncthreads();
+  constexpr int PER_ROW = Q::COLS / 8;
+  for (int q = threadIdx.x; q < 16 * MT * PER_ROW; q += Q::NT) {
+    const int m = q / PER_ROW, c8 = (q % PER_ROW) * 8;
+    if (m < rows) *(uint4*)(a.hbf + (int64_t)(p0 + m) * a.hstride + n0 + c8) = *(const uint4*)(ot + m * OP + c8);
+  }
+}
+
 // grid (I / COLS, tiles rounded up to 8), mapped by xcd_tile
-template <int FPW, int NW>
 // (the second bound is waves per SIMD: 3 workgroups of 4 waves per CU)
+template <int FPW, int NW>
 __global__ __launch_bounds__(64 * NW, 3) void k_gate_up_q4k(ExpertArgs a) {
   using Q = Q4k<FPW, NW>;
   __shared__ __attribute__((aligned(16))) uint8_t ring[Q::NST * Q::STAGE];
@@ -432,53 +486,16 @@ __global__ __launch_bounds__(64 * NW, 3) void k_gate_up_q4k(ExpertArgs a) {
   __syncthreads();
   const int lane = lane_id(), wave = threadIdx.x >> 6, l16 = lane & 15, kq = lane >> 4;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)ring;
-  f32x4_t accg[4][FPW], accu[4][FPW];
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < FPW; j++) {
-      accg[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      accu[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    }
   const Q4kSrc<Q> src = q4k_sources<Q>(a.xh, a.H, rowsrc, G, U, n0, K);
   // dequantisation constants, kept in registers for v_and_or_b32
   const uint32_t knib = __builtin_amdgcn_readfirstlane(0x000F000Fu), kbyte = __builtin_amdgcn_readfirstlane(0x00FF00FFu);
   uint32_t kmagic;
   asm("v_mov_b32 %0, 0x64006400" : "=v"(kmagic));
-#pragma unroll
-  for (int c = 0; c < Q::NST - 1; c++)
-    if (c < nk) q4k_issue<Q>(lds0, c, src, c, wave_u);
-  for (int kc = 0; kc < nk; kc++) {
-    const int ahead = min(Q::NST - 2, nk - 1 - kc);
-    q4k_wait<Q>(ahead, wave_u);
-    __syncthreads();   // chunk kc is in LDS for every wave; stage (kc - 1) % NST is free
-    if (kc + Q::NST - 1 < nk) q4k_issue<Q>(lds0, (kc + Q::NST - 1) % Q::NST, src, kc + Q::NST - 1, wave_u);
-    const lds_u8* st = (const lds_u8*)ring + (kc % Q::NST) * Q::STAGE;
-    if (kc & 1) q4k_compute<Q, 1>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
-    else q4k_compute<Q, 0>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
-  }
-  // the 64 x COLS f16 tile of h goes through LDS (columns in the swizzled
-  // order, row pitch COLS + 8) and out as 16-byte pieces
-  __syncthreads();   // every wave is done with the ring
-  constexpr int OP = Q::COLS + 8;
-  _Float16* ot = (_Float16*)ring;
-#pragma unroll
-  for (int j = 0; j < FPW; j++) {
-    const int col = swz(16 * (FPW * wave + j) + l16);
-#pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int m = 16 * mt + 4 * kq + i;
-        ot[m * OP + col] = (_Float16)(siluf_(accg[mt][j][i]) * accu[mt][j][i]);
-      }
-  }
-  __syncthreads();
-  constexpr int PER_ROW = Q::COLS / 8;
-  for (int q = threadIdx.x; q < PM * PER_ROW; q += Q::NT) {
-    const int m = q / PER_ROW, c8 = (q % PER_ROW) * 8;
-    if (m < rows) *(uint4*)(a.hbf + (int64_t)(p0 + m) * a.hstride + n0 + c8) = *(const uint4*)(ot + m * OP + c8);
+  switch ((rows + 15) >> 4) {   // uniform over the workgroup
+    case 1: q4k_main<Q, 1>(a, ring, src, nk, rows, p0, n0, wave, wave_u, l16, kq, knib, kbyte, kmagic); break;
+    case 2: q4k_main<Q, 2>(a, ring, src, nk, rows, p0, n0, wave, wave_u, l16, kq, knib, kbyte, kmagic); break;
+    case 3: q4k_main<Q, 3>(a, ring, src, nk, rows, p0, n0, wave, wave_u, l16, kq, knib, kbyte, kmagic); break;
+    default: q4k_main<Q, 4>(a, ring, src, nk, rows, p0, n0, wave, wave_u, l16, kq, knib, kbyte, kmagic); break;
   }
 }
 
@@ -575,7 +592,8 @@ HX_DEV uint32_t q6_pair(uint32_t lo4, uint32_t hi2, uint32_t knib, uint32_t kmag
   return and_or(hi2, k30, and_or(lo4, knib, kmagic));
 }
 
-template <int P>   // chunk parity: quarters P and P + 2 of the half
+// MT: 16-row M sub-tiles in use
+template <int P, int MT>   // chunk parity: quarters P and P + 2 of the half
 HX_DEV void dq_compute(const lds_u8* st, const uint16_t* dl, int sb, f32x4_t (*acc)[4], int wave, int l16, int kq,
                        uint32_t knib, uint32_t kmagic, uint32_t k30) {
   const h2_t off = h2s(-1056.0f);
@@ -601,7 +619,7 @@ HX_DEV void dq_compute(const lds_u8* st, const uint16_t* dl, int sb, f32x4_t (*a
                               u32((h2(q6_pair(wy, hy, knib, kmagic, k30)) + off) * a),
                               u32((h2(q6_pair(wy >> 8, hy >> 8, knib, kmagic, k30)) + off) * a)));
 #pragma unroll
-      for (int mt = 0; mt < 4; mt++) {
+      for (int mt = 0; mt < MT; mt++) {
         const int row = 16 * mt + l16, seg = 4 * t + kq;
         const f16x8_t av = __builtin_bit_cast(
             f16x8_t, *(const __attribute__((address_space(3))) u32x4_t*)(st + row * 128 + ((seg ^ (l16 & 7)) << 4)));
@@ -612,6 +630,60 @@ HX_DEV void dq_compute(const lds_u8* st, const uint16_t* dl, int sb, f32x4_t (*a
 }
 
 // grid (H / 128, tiles rounded up to 8), mapped by xcd_tile
+// the K loop and epilogue of k_down_q6k for tiles of at most 16 MT rows (MFMAs
+// and activation-fragment reads for the sub-tiles in use; DMAs unchanged)
+template <int MT>
+HX_DEV void dq_main(const ExpertArgs& a, uint8_t* ring, float* rws, const DqSrc& src, float rw, int rows, int p0,
+                    int n0, int wave, int wave_u, int l16, int kq) {
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)ring;
+  const uint16_t* dl = (const uint16_t*)(ring + DQ_NST * DQ_STAGE);
+#pragma unroll
+  for (int c = 0; c < DQ_NST - 1; c++) dq_issue(lds0, c, src, c, wave_u);
+  const uint32_t knib = __builtin_amdgcn_readfirstlane(0x000F000Fu), k30 = __builtin_amdgcn_readfirstlane(0x00300030u);
+  uint32_t kmagic;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(kmagic));
+  f32x4_t acc[2][4];
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int i = 0; i < MT; i++) acc[j][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < DQ_NC; c++) {
+    // chunk c (and, before chunk 0, the d dwords) has landed once at most the
+    // 5 DMAs of chunk c + 1 are outstanding
+    if (c + 1 < DQ_NC) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();   // chunk c is in LDS for every wave; stage (c - 1) % NST is free
+    if (c + DQ_NST - 1 < DQ_NC) dq_issue(lds0, (c + DQ_NST - 1) % DQ_NST, src, c + DQ_NST - 1, wave_u);
+    const lds_u8* st = (const lds_u8*)ring + (c % DQ_NST) * DQ_STAGE;
+    if (c & 1) dq_compute<1, MT>(st, dl, c >> 2, acc, wave, l16, kq, knib, kmagic, k30);
+    else dq_compute<0, MT>(st, dl, c >> 2, acc, wave, l16, kq, knib, kmagic, k30);
+  }
+  if (threadIdx.x < PM) rws[threadIdx.x] = rw;
+  __syncthreads();   // also: every wave is done with the ring
+  // the 16 MT x 128 bf16 output rows go through LDS (row pitch 272 B, so the
+  // 16 lanes of a row group write different banks) and out as 16-byte pieces
+  constexpr int OP = 136;   // pitch in bf16
+  uint16_t* ot = (uint16_t*)ring;
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int col = 32 * wave + 16 * j + l16;
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int m = 16 * mt + 4 * kq + i;
+        ot[m * OP + col] = f32_to_bf16(rws[m] * acc[j][mt][i]);
+      }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < MT; i++) {
+    const int q = i * 256 + threadIdx.x, m = q >> 4, c8 = (q & 15) * 8;
+    if (m < rows)
+      *(uint4*)((uint16_t*)a.obuf + (int64_t)(p0 + m) * a.H + n0 + c8) = *(const uint4*)(ot + m * OP + c8);
+  }
+}
+
 __global__ __launch_bounds__(256, 3) void k_down_q6k(ExpertArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[DQ_NST * DQ_STAGE + 128 * 4];
   __shared__ float rws[PM];
@@ -627,56 +699,16 @@ __global__ __launch_bounds__(256, 3) void k_down_q6k(ExpertArgs a) {
   // routing weights, loaded before the DMAs and first used after the last one
   const float rw = threadIdx.x < PM ? a.wpos[p0 + min((int)threadIdx.x, rows - 1)] : 0.f;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)ring;
-  const uint16_t* dl = (const uint16_t*)(ring + DQ_NST * DQ_STAGE);
   // d of both superblocks of the 128 weight rows (waves 0 and 1, one dword each)
   if (wave_u < 2)
     dma4(W + (int64_t)a.H * (DQ_K / 2 + DQ_K / 4 + DQ_K / 16) + (int64_t)(n0 + 64 * wave_u + lane) * 4,
          lds0 + (uint32_t)(DQ_NST * DQ_STAGE + wave_u * 256));
   const DqSrc src = dq_sources(a.hbf, a.hstride, p0, rows, W, a.H, n0);
-#pragma unroll
-  for (int c = 0; c < DQ_NST - 1; c++) dq_issue(lds0, c, src, c, wave_u);
-  const uint32_t knib = __builtin_amdgcn_readfirstlane(0x000F000Fu), k30 = __builtin_amdgcn_readfirstlane(0x00300030u);
-  uint32_t kmagic;
-  asm("v_mov_b32 %0, 0x64006400" : "=v"(kmagic));
-  f32x4_t acc[2][4];
-#pragma unroll
-  for (int j = 0; j < 2; j++)
-#pragma unroll
-    for (int i = 0; i < 4; i++) acc[j][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < DQ_NC; c++) {
-    // chunk c (and, before chunk 0, the d dwords) has landed once at most the
-    // 5 DMAs of chunk c + 1 are outstanding
-    if (c + 1 < DQ_NC) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();   // chunk c is in LDS for every wave; stage (c - 1) % NST is free
-    if (c + DQ_NST - 1 < DQ_NC) dq_issue(lds0, (c + DQ_NST - 1) % DQ_NST, src, c + DQ_NST - 1, wave_u);
-    const lds_u8* st = (const lds_u8*)ring + (c % DQ_NST) * DQ_STAGE;
-    if (c & 1) dq_compute<1>(st, dl, c >> 2, acc, wave, l16, kq, knib, kmagic, k30);
-    else dq_compute<0>(st, dl, c >> 2, acc, wave, l16, kq, knib, kmagic, k30);
-  }
-  if (threadIdx.x < PM) rws[threadIdx.x] = rw;
-  __syncthreads();   // also: every wave is done with the ring
-  // the 64 x 128 bf16 output tile goes through LDS (row pitch 272 B, so the
-  // 16 lanes of a row group write different banks) and out as 16-byte pieces
-  constexpr int OP = 136;   // pitch in bf16
-  uint16_t* ot = (uint16_t*)ring;
-#pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int col = 32 * wave + 16 * j + l16;
-#pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int m = 16 * mt + 4 * kq + i;
-        ot[m * OP + col] = f32_to_bf16(rws[m] * acc[j][mt][i]);
-      }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int q = i * 256 + threadIdx.x, m = q >> 4, c8 = (q & 15) * 8;
-    if (m < rows)
-      *(uint4*)((uint16_t*)a.obuf + (int64_t)(p0 + m) * a.H + n0 + c8) = *(const uint4*)(ot + m * OP + c8);
+  switch ((rows + 15) >> 4) {   // uniform over the workgroup
+    case 1: dq_main<1>(a, ring, rws, src, rw, rows, p0, n0, wave, wave_u, l16, kq); break;
+    case 2: dq_main<2>(a, ring, rws, src, rw, rows, p0, n0, wave, wave_u, l16, kq); break;
+    case 3: dq_main<3>(a, ring, rws, src, rw, rows, p0, n0, wave, wave_u, l16, kq); break;
+    default: dq_main<4>(a, ring, rws, src, rw, rows, p0, n0, wave, wave_u, l16, kq); break;
   }
 }
 
