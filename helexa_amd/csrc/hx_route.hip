@@ -213,10 +213,18 @@ __global__ __launch_bounds__(1024) void k_disp_scan(DispatchArgs a) {
   const int e = threadIdx.x, E = a.E, nb = dispatch_blocks(a.F);
   int count = 0;
   if (e < E) {
-    for (int b = 0; b < nb; b++) {
-      const int h = a.hist[(int64_t)b * E + e];
-      a.hist[(int64_t)b * E + e] = count;
-      count += h;
+    // the expert's per-block counts, PB at a time: all loads of a batch
+    // issued before the first is used (one memory round trip per batch)
+    constexpr int PB = 16;
+    for (int b0 = 0; b0 < nb; b0 += PB) {
+      int h[PB];
+#pragma unroll
+      for (int i = 0; i < PB; i++) h[i] = b0 + i < nb ? a.hist[(int64_t)(b0 + i) * E + e] : 0;
+#pragma unroll
+      for (int i = 0; i < PB; i++) {
+        if (b0 + i < nb) a.hist[(int64_t)(b0 + i) * E + e] = count;
+        count += h[i];
+      }
     }
   }
   int tot;
@@ -267,23 +275,42 @@ __global__ __launch_bounds__(1024) void k_disp_scan(DispatchArgs a) {
   }
 }
 
+// wave w places the entries [f0 + 512 w, f0 + 512 w + 512) of block b's
+// chunk: its per-expert base = the block's base + the counts of waves 0..w-1
+// (from a per-wave histogram), then 64 entries at a time in order, the rank of
+// an entry among the equal experts of its 64 from bitwise ballots. Each wave
+// keeps its own running bases, so the waves never wait for each other after
+// the bases are set.
 __global__ __launch_bounds__(256) void k_disp_scatter(DispatchArgs a) {
-  __shared__ int cnt[HX_MAX_EXPERTS];
-  __shared__ uint8_t whist[4][HX_MAX_EXPERTS];
+  constexpr int NWV = 4, SUB = HX_DISPATCH_CHUNK / NWV;
+  __shared__ int wbase[NWV][HX_MAX_EXPERTS];
   const int b = blockIdx.x, E = a.E, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   if (b == 0 && a.wpos && a.has_shared)
     for (int t = tid; t < a.T; t += 256) a.wpos[a.F + t] = a.sgw[t];
-  for (int e = tid; e < E; e += 256) {
-    cnt[e] = a.hist[(int64_t)b * E + e];
-    whist[0][e] = whist[1][e] = whist[2][e] = whist[3][e] = 0;
-  }
+  for (int e = tid; e < E; e += 256)
+#pragma unroll
+    for (int w = 0; w < NWV; w++) wbase[w][e] = 0;
   __syncthreads();
   const int f0 = b * HX_DISPATCH_CHUNK, f1 = min(a.F, f0 + HX_DISPATCH_CHUNK);
+  const int s0 = min(f1, f0 + SUB * wave), s1 = min(f1, s0 + SUB);
+  for (int f = s0 + lane; f < s1; f += 64) atomicAdd(&wbase[wave][a.topk_idx[f]], 1);
+  __syncthreads();
+  for (int e = tid; e < E; e += 256) {
+    int run = a.hist[(int64_t)b * E + e];
+#pragma unroll
+    for (int w = 0; w < NWV; w++) {
+      const int c = wbase[w][e];
+      wbase[w][e] = run;
+      run += c;
+    }
+  }
+  __syncthreads();
   const int nbits = 32 - __clz(E);
   const unsigned long long lt = (1ull << lane) - 1ull;
-  for (int base = f0; base < f1; base += 256) {
-    const int f = base + tid;
-    const bool valid = f < f1;
+  int* base = wbase[wave];
+  for (int g = s0; g < s1; g += 64) {
+    const int f = g + lane;
+    const bool valid = f < s1;
     const int e = valid ? a.topk_idx[f] : 0;
     unsigned long long mask = __ballot(valid);
     for (int bit = 0; bit < nbits; bit++) {
@@ -291,24 +318,16 @@ __global__ __launch_bounds__(256) void k_disp_scatter(DispatchArgs a) {
       const unsigned long long m = __ballot(v);
       mask &= v ? m : ~m;
     }
-    const int rank = __popcll(mask & lt), wcount = __popcll(mask);
-    const bool leader = valid && rank == 0;
-    if (leader) whist[wave][e] = (uint8_t)wcount;
-    __syncthreads();
+    const int rank = __popcll(mask & lt), cnt = __popcll(mask);
     if (valid) {
-      int pre = 0;
-      for (int w = 0; w < wave; w++) pre += whist[w][e];
-      const int pos = cnt[e] + pre + rank;
+      const int pos = base[e] + rank;
       a.perm[pos] = f;
       if (a.inv) a.inv[f] = pos;
       if (a.wpos) a.wpos[pos] = a.topk_w[f];
     }
-    __syncthreads();
-    if (leader) {
-      atomicAdd(&cnt[e], wcount);
-      whist[wave][e] = 0;
-    }
-    __syncthreads();
+    __builtin_amdgcn_wave_barrier();   // every lane has read base[] before the leaders move it
+    if (valid && rank == 0) base[e] += cnt;
+    __builtin_amdgcn_wave_barrier();
   }
 }
 
