@@ -219,6 +219,30 @@ def test_forward_c2_decode_repeated_tokens(c2, pattern):
     assert rel_err(got, c2.oracle.forward(x_np(x))) <= TOL_BF16
 
 
+@pytest.fixture(scope="module")
+def q4km():
+    _, synth = _hx()
+    return Case(synth.A3B, synth.FMT_Q4_K_M, 13, O.BF16)
+
+
+@pytest.mark.parametrize("T", [2, 3, 5, 7])
+def test_forward_q4_k_m_decode_batches(q4km, T):
+    """decode for T > 1 at every group count of the pipelined down kernel (rows
+    of h = T (k + 1) in groups of 24: one to four groups)"""
+    x = q4km.x(T, seed=T)
+    got = q4km.block.forward(x).float().cpu().numpy()
+    assert rel_err(got, q4km.oracle.forward(x_np(x))) <= TOL_BF16
+
+
+@pytest.mark.parametrize("T", [9, 24, 40])
+def test_forward_q4_k_m_prefill_small_tiles(q4km, T):
+    """prefill tiles with 1, 2 and 3 sixteen-row sub-tiles in use (routed tiles of
+    a row or two; the shared expert's tile holds all T rows)"""
+    x = q4km.x(T, seed=100 + T)
+    got = q4km.block.forward(x).float().cpu().numpy()
+    assert rel_err(got, q4km.oracle.forward(x_np(x))) <= TOL_BF16
+
+
 def test_forward_q4_k_m_prefill_sampled_tokens():
     hx, synth = _hx()
     c = Case(synth.A3B, synth.FMT_Q4_K_M, 11, O.BF16)
