@@ -152,8 +152,9 @@ def bench_decode(args):
     us_per_layer = dt / steps * 1e6
 
     # per-kernel durations: the same steps launched eagerly with the library's HIP
-    # events around each kernel, queued behind a ~30 ms sleep kernel so that the
-    # GPU runs them back to back (no host launch gaps inside an event pair)
+    # events, queued behind a ~30 ms sleep kernel so that the GPU runs them back
+    # to back; for one token each kernel's event pair is recorded by its own
+    # dispatch (hipExtLaunchKernel), the interval a kernel trace reports
     kern = {}
     n_t = min(G, 256)
     for _ in range(max(1, min(reps, 4))):

@@ -924,7 +924,7 @@ static hipError_t router_dec_fmt(const RouterArgs& r, const ExpertArgs& a, bool 
     constexpr int RG = 64 / LPR;                                                            \
     const int nsb = a.Is > 0 && a.T > 1 ? (a.Is + 4 * RG * NR - 1) / (4 * RG * NR) : 0;    \
     const int ncb = a.xcv && a.T > 1 ? (a.T + 3) / 4 : 0;                                   \
-    hipLaunchKernelGGL((k_router_dec<FMT, LPR, NR, RB, TT>), dim3(nrb + nsb + ncb), dim3(256), 0, s, r, a, nrb, nsb); \
+    hx_launch(k_router_dec<FMT, LPR, NR, RB, TT>, dim3(nrb + nsb + ncb), dim3(256), 0, s, r, a, nrb, nsb); \
   }
 #define RD_T(LPR, RB) { if (r.T <= 1) RD(LPR, RB, 1) else if (r.T <= 2) RD(LPR, RB, 2) else if (r.T <= 4) RD(LPR, RB, 4) else RD(LPR, RB, 8) }
 #define RD_R(LPR) { if (rbf) RD_T(LPR, true) else RD_T(LPR, false) }
@@ -992,7 +992,7 @@ static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
                  (size_t)HX_DOWN_ROWS * (3 + RG) * 4;                                              \
     const dim3 grid((a.H + RG - 1) / RG, groups);                                                   \
     if (xlds) hipLaunchKernelGGL((k_down_dec<FMT, LPR, 6, 4, true>), grid, dim3(256), lds, s, a);   \
-    else if (small) hipLaunchKernelGGL((k_down_dec<FMT, LPR, 3, 4, false>), grid, dim3(256), lds, s, a); \
+    else if (small) hx_launch(k_down_dec<FMT, LPR, 3, 4, false>, grid, dim3(256), (uint32_t)lds, s, a); \
     else hipLaunchKernelGGL((k_down_dec<FMT, LPR, 6, 4, false>), grid, dim3(256), lds, s, a);       \
   }
   if (nch == 64) DD(64) else if (nch == 32) DD(32) else DD(16)
@@ -1014,7 +1014,7 @@ hipError_t launch_router_dec(const RouterArgs& r, const ExpertArgs& a, bool rbf,
 template <int FMT>
 static hipError_t gate_up_dec1_fmt(const RouterArgs& r, const ExpertArgs& a, hipStream_t s) {
   const int rows = a.I > a.Is ? a.I : a.Is;
-  hipLaunchKernelGGL((k_gate_up_dec1<FMT, 8, 10>), dim3((rows + 1) / 2), dim3(256), 0, s, r, a);
+  hx_launch(k_gate_up_dec1<FMT, 8, 10>, dim3((rows + 1) / 2), dim3(256), 0, s, r, a);
   return hipGetLastError();
 }
 

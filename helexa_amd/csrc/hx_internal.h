@@ -2,6 +2,7 @@
 // handle. Not part of the C ABI.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 
 #include <string>
@@ -162,5 +163,25 @@ hipError_t launch_residual_add(void* x, const void* y, bool bf, int64_t n, hipSt
 
 int64_t gguf_block_elems(int fmt);
 int64_t gguf_block_bytes(int fmt);
+
+// Per-kernel timing (hx_moe_timing_*): when start is set, the next launch
+// through hx_launch has the runtime record the two events at that kernel's own
+// dispatch start and end (hipExtLaunchKernel) -- the interval a kernel trace
+// reports -- and clears them.
+struct ExtTiming {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+extern thread_local ExtTiming g_ext_timing;
+template <typename K, typename... Args>
+inline void hx_launch(K kernel, dim3 grid, dim3 block, uint32_t shm, hipStream_t s, Args... args) {
+  ExtTiming& t = g_ext_timing;
+  if (t.start) {
+    const hipEvent_t a = t.start, b = t.stop;
+    t.start = t.stop = nullptr;
+    hipExtLaunchKernelGGL(kernel, grid, block, shm, s, a, b, 0u, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, shm, s, args...);
+  }
+}
 
 }  // namespace hx

@@ -399,6 +399,10 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
   a.wpos = d.wpos;
 }
 
+namespace hx {
+thread_local ExtTiming g_ext_timing;
+}
+
 // event helpers for the optional per-kernel timing
 static void tm_mark(hx_moe* m, int slot, int which, hipStream_t s) {
   Timing& t = m->tm;
@@ -409,6 +413,30 @@ static void tm_mark(hx_moe* m, int slot, int which, hipStream_t s) {
   // timing events are not recorded into graphs under capture
   if (st == hipStreamCaptureStatusNone) (void)hipEventRecord(ev, s);
   if (which == 1) t.used[(size_t)t.calls * N_SLOTS + slot] = 1;
+}
+
+// timing of a slot launched as one kernel through hx_launch: the events are
+// recorded by that kernel's dispatch itself (tm_ext before the launch,
+// tm_ext_done after; a launcher that did not consume them leaves the slot
+// untimed for this call)
+static void tm_ext(hx_moe* m, int slot, hipStream_t s) {
+  Timing& t = m->tm;
+  if (!t.on || t.calls >= t.max_calls) return;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  (void)hipStreamIsCapturing(s, &st);
+  if (st != hipStreamCaptureStatusNone) return;
+  const size_t k = ((size_t)t.calls * N_SLOTS + slot) * 2;
+  g_ext_timing.start = t.ev[k];
+  g_ext_timing.stop = t.ev[k + 1];
+}
+static void tm_ext_done(hx_moe* m, int slot) {
+  Timing& t = m->tm;
+  if (!t.on || t.calls >= t.max_calls) return;
+  if (g_ext_timing.start) {
+    g_ext_timing.start = g_ext_timing.stop = nullptr;
+    return;
+  }
+  t.used[(size_t)t.calls * N_SLOTS + slot] = 1;
 }
 
 static int run_routing(hx_moe* m, Plan& p, hipStream_t s) {
@@ -469,13 +497,16 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
   if (fast) {
     // router + shared gate/up; routed gate/up (one token: routing in its
     // prologue; more: routed once by one workgroup, then the plan); down + combine
-    tm_mark(m, SLOT_ROUTER, 0, s);
+    // one token: each slot is one kernel, timed by its own dispatch
+    if (T == 1) tm_ext(m, SLOT_ROUTER, s);
+    else tm_mark(m, SLOT_ROUTER, 0, s);
     HX_HIP(launch_router_dec(p.ra, p.ea, m->rdt == HX_BF16, s));
-    tm_mark(m, SLOT_ROUTER, 1, s);
+    if (T == 1) tm_ext_done(m, SLOT_ROUTER);
+    else tm_mark(m, SLOT_ROUTER, 1, s);
     if (T == 1) {
-      tm_mark(m, SLOT_GATE_UP, 0, s);
+      tm_ext(m, SLOT_GATE_UP, s);
       HX_HIP(launch_gate_up_dec(p.ra, p.ea, s));
-      tm_mark(m, SLOT_GATE_UP, 1, s);
+      tm_ext_done(m, SLOT_GATE_UP);
     } else {
       tm_mark(m, SLOT_ROUTE_TOKENS, 0, s);
       launch_route_small(p.ra, s);
@@ -485,9 +516,11 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
       HX_HIP(launch_gate_up_plan(p.ea, s));
       tm_mark(m, SLOT_GATE_UP, 1, s);
     }
-    tm_mark(m, SLOT_DOWN, 0, s);
+    if (T == 1) tm_ext(m, SLOT_DOWN, s);
+    else tm_mark(m, SLOT_DOWN, 0, s);
     HX_HIP(launch_down_dec(p.ea, s));
-    tm_mark(m, SLOT_DOWN, 1, s);
+    if (T == 1) tm_ext_done(m, SLOT_DOWN);
+    else tm_mark(m, SLOT_DOWN, 1, s);
   } else if (decode) {
     if ((rc = run_routing(m, p, s))) return rc;
     tm_mark(m, SLOT_GATE_UP, 0, s);
