@@ -492,6 +492,10 @@ __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a
   const int mat = wave & 1;                       // 0: gate, 1: up
   const int row = blockIdx.x * 2 + (wave >> 1);   // row of I (and of the shared expert's Is)
   const int K = a.H;
+  // the logits first: a wait for them then leaves the later loads in flight
+  float lv[EPL];
+  route_logits_load<EPL>(r.logits, r.E, lv);
+  const float sg = r.has_shared ? r.logits[r.E] : 0.f;
   uint32_t xp[D::NX];
   float xs[D::NS];
   D::template load_x<false>((const uint16_t*)a.x, lane, xp, xs);
@@ -505,12 +509,20 @@ __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a
   D::load(hs ? (mat ? a.sup.base : a.sgate.base) : (mat ? a.up.mat(0) : a.gate.mat(0)),
           hs ? a.Is : a.I, K, shrow ? row : 0, lane, rsh);
   __builtin_amdgcn_sched_barrier(0);
-  const float sg = r.has_shared ? r.logits[r.E] : 0.f;
   typename D::Raw raw[KR];
   int my_e;
   float my_w;
-  route_token_core_hook<EPL, KR>(r.logits, r.E, r.norm, my_e, my_w, [&](int j, int e) {
-    D::load(mat ? a.up.mat(e) : a.gate.mat(e), a.I, K, rrow ? row : 0, lane, raw[j]);
+  // round -1: the lowest id of the maximum logit, almost always rank 0: its
+  // row is loaded before the softmax and sort, and reloaded only if round 0
+  // selects another expert
+  int es = -1;
+  route_token_core_hook<EPL, KR>(lv, r.E, r.norm, my_e, my_w, [&](int j, int e) {
+    if (j < 0) {
+      es = e;
+      D::load(mat ? a.up.mat(e >= 0 ? e : 0) : a.gate.mat(e >= 0 ? e : 0), a.I, K, rrow ? row : 0, lane, raw[0]);
+    } else if (j > 0 || e != es) {
+      D::load(mat ? a.up.mat(e) : a.gate.mat(e), a.I, K, rrow ? row : 0, lane, raw[j]);
+    }
     __builtin_amdgcn_sched_barrier(0);
   });
   // dispatch position of rank `lane`: the k experts are distinct

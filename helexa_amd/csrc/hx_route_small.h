@@ -65,20 +65,48 @@ HX_DEV void sort_keys_desc(uint32_t* h, uint32_t* l) {
       }
 }
 
-// softmax over the E logits of a token and this lane's keys, sorted
+// this lane's logits (expert lane + 64 j; padding -inf)
 template <int EPL>
-HX_DEV void route_keys(const float* lg, int E, uint32_t* h, uint32_t* l) {
+HX_DEV void route_logits_load(const float* lg, int E, float* v) {
   const int lane = lane_id();
-  float v[EPL];
-  float mx = -__builtin_inff();
 #pragma unroll
   for (int j = 0; j < EPL; j++) {
     const int e = lane + 64 * j;
     const float x = lg[e < E ? e : E - 1];
     v[j] = e < E ? x : -__builtin_inff();
-    mx = v[j] > mx ? v[j] : mx;
   }
-  mx = wave_max_dpp(mx);
+}
+// the wave-wide max of the loaded logits
+template <int EPL>
+HX_DEV float route_logits_max(const float* v) {
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < EPL; j++) mx = v[j] > mx ? v[j] : mx;
+  return wave_max_dpp(mx);
+}
+template <int EPL>
+HX_DEV float route_logits(const float* lg, int E, float* v) {
+  route_logits_load<EPL>(lg, E, v);
+  return route_logits_max<EPL>(v);
+}
+
+// the lowest expert id whose logit is the maximum (wave-uniform; -1 if none):
+// rank 0 of the routing unless rounding gives a smaller logit the same
+// probability, so a caller may start work on it before the softmax
+template <int EPL>
+HX_DEV int route_argmax(const float* v, float mx, int E) {
+  const int lane = lane_id();
+  uint32_t cand = 0u;   // ~id of this lane's lowest id holding mx
+#pragma unroll
+  for (int j = EPL - 1; j >= 0; j--)
+    cand = v[j] == mx && lane + 64 * j < E ? ~(uint32_t)(lane + 64 * j) : cand;
+  return (int)~wave_max_u32(cand);
+}
+
+// softmax over the E logits of a token and this lane's keys, sorted
+template <int EPL>
+HX_DEV void route_keys_from(float* v, float mx, uint32_t* h, uint32_t* l) {
+  const int lane = lane_id();
 #pragma unroll
   for (int j = 0; j < EPL; j++) v[j] = v[j] - mx;
   expf_route_n<EPL>(v);   // padding: exp(-inf) = 0
@@ -92,6 +120,12 @@ HX_DEV void route_keys(const float* lg, int E, uint32_t* h, uint32_t* l) {
     l[j] = ~(uint32_t)(lane + 64 * j);
   }
   sort_keys_desc<EPL>(h, l);
+}
+template <int EPL>
+HX_DEV void route_keys(const float* lg, int E, uint32_t* h, uint32_t* l) {
+  float v[EPL];
+  const float mx = route_logits<EPL>(lg, E, v);
+  route_keys_from<EPL>(v, mx, h, l);
 }
 
 // One selection round: the wave-wide largest head probability m; when several
@@ -169,10 +203,17 @@ HX_DEV void route_token_core(const float* lg, int E, int k, bool norm, int& out_
 // round r picks expert e (wave-uniform), so a caller can start loading that
 // expert's weights while the later rounds run
 template <int EPL, int K, class Hook>
-HX_DEV void route_token_core_hook(const float* lg, int E, bool norm, int& out_e, float& out_w, Hook&& hook) {
+// v: this lane's logits from route_logits_load (the caller issues those loads
+// first, so that waiting for them does not wait for its other loads)
+HX_DEV void route_token_core_hook(float* v, int E, bool norm, int& out_e, float& out_w, Hook&& hook) {
   const int lane = lane_id();
   uint32_t h[EPL], l[EPL];
-  route_keys<EPL>(lg, E, h, l);
+  {
+    // hook(-1, e): the likely rank-0 expert, as soon as the logits are in
+    const float mx = route_logits_max<EPL>(v);
+    hook(-1, route_argmax<EPL>(v, mx, E));
+    route_keys_from<EPL>(v, mx, h, l);
+  }
   float my_p = 0.0f, tot = 0.0f;
   int my_e = 0;
   uint32_t pend = 0u;
