@@ -512,15 +512,19 @@ __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a
   typename D::Raw raw[KR];
   int my_e;
   float my_w;
-  // round -1: the lowest id of the maximum logit, almost always rank 0: its
-  // row is loaded before the softmax and sort, and reloaded only if round 0
-  // selects another expert
-  int es = -1;
-  route_token_core_hook<EPL, KR>(lv, r.E, r.norm, my_e, my_w, [&](int j, int e) {
+  // rounds -1 .. -SPEC: the experts of the SPEC largest logits (lowest id
+  // first), almost always ranks 0 .. SPEC - 1: their rows are loaded before the
+  // softmax and sort, and reloaded only if the round of that rank selects
+  // another expert (measured on MI355X: SPEC = 1 is fastest; each further
+  // guess delays the softmax by one more pair of wave reductions)
+  constexpr int SPEC = 1;
+  int es[SPEC];
+  route_token_core_hook<EPL, KR, SPEC>(lv, r.E, r.norm, my_e, my_w, [&](int j, int e) {
     if (j < 0) {
-      es = e;
-      D::load(mat ? a.up.mat(e >= 0 ? e : 0) : a.gate.mat(e >= 0 ? e : 0), a.I, K, rrow ? row : 0, lane, raw[0]);
-    } else if (j > 0 || e != es) {
+      const int sp = -1 - j;
+      es[sp] = e;
+      D::load(mat ? a.up.mat(e >= 0 ? e : 0) : a.gate.mat(e >= 0 ? e : 0), a.I, K, rrow ? row : 0, lane, raw[sp]);
+    } else if (j >= SPEC || e != es[j]) {
       D::load(mat ? a.up.mat(e) : a.gate.mat(e), a.I, K, rrow ? row : 0, lane, raw[j]);
     }
     __builtin_amdgcn_sched_barrier(0);

@@ -201,17 +201,32 @@ HX_DEV void route_token_core(const float* lg, int E, int k, bool norm, int& out_
 
 // route_token_core with K rounds unrolled and hook(r, e) called right after
 // round r picks expert e (wave-uniform), so a caller can start loading that
-// expert's weights while the later rounds run
-template <int EPL, int K, class Hook>
-// v: this lane's logits from route_logits_load (the caller issues those loads
-// first, so that waiting for them does not wait for its other loads)
+// expert's weights while the later rounds run; before the softmax, hook(-1 - s,
+// e) for s < SPEC with the expert of the s-th largest logit. v: this lane's
+// logits from route_logits_load (the caller issues those loads first, so that
+// waiting for them does not wait for its other loads).
+template <int EPL, int K, int SPEC, class Hook>
 HX_DEV void route_token_core_hook(float* v, int E, bool norm, int& out_e, float& out_w, Hook&& hook) {
   const int lane = lane_id();
   uint32_t h[EPL], l[EPL];
   {
-    // hook(-1, e): the likely rank-0 expert, as soon as the logits are in
+    // hook(-1 - s, e), s < SPEC: the likely rank-s expert (the s-th largest
+    // logit, lowest id first), as soon as the logits are in
     const float mx = route_logits_max<EPL>(v);
-    hook(-1, route_argmax<EPL>(v, mx, E));
+    int e = route_argmax<EPL>(v, mx, E);
+    hook(-1, e);
+    if constexpr (SPEC > 1) {
+      float w[EPL];
+#pragma unroll
+      for (int j = 0; j < EPL; j++) w[j] = v[j];
+#pragma unroll
+      for (int sp = 1; sp < SPEC; sp++) {
+#pragma unroll
+        for (int j = 0; j < EPL; j++) w[j] = lane + 64 * j == e ? -__builtin_inff() : w[j];
+        e = route_argmax<EPL>(w, route_logits_max<EPL>(w), E);
+        hook(-1 - sp, e);
+      }
+    }
     route_keys_from<EPL>(v, mx, h, l);
   }
   float my_p = 0.0f, tot = 0.0f;
