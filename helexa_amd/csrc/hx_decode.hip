@@ -934,10 +934,11 @@ bool decode_fast_ok(const ExpertArgs& a) {
 template <int FMT>
 static hipError_t router_dec_fmt(const RouterArgs& r, const ExpertArgs& a, bool rbf, hipStream_t s) {
   const int nch = a.H / 32, nrb = (r.E1 + 3) / 4;
-  constexpr int NR = 2;
+  // NR: shared-expert rows per wave (T > 1): one for up to 4 tokens, two for
+  // more (measured on MI355X: more workgroups win while the tokens are few)
 #define RD(LPR, RB, TT)                                                                     \
   {                                                                                         \
-    constexpr int RG = 64 / LPR;                                                            \
+    constexpr int RG = 64 / LPR, NR = TT <= 4 ? 1 : 2;                                      \
     const int nsb = a.Is > 0 && a.T > 1 ? (a.Is + 4 * RG * NR - 1) / (4 * RG * NR) : 0;    \
     const int ncb = a.xcv && a.T > 1 ? (a.T + 3) / 4 : 0;                                   \
     hx_launch(k_router_dec<FMT, LPR, NR, RB, TT>, dim3(nrb + nsb + ncb), dim3(256), 0, s, r, a, nrb, nsb); \
