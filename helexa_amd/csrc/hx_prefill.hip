@@ -366,18 +366,24 @@ HX_DEV void q4k_compute(const lds_u8* st, f32x4_t (*accg)[Q::FPW_], f32x4_t (*ac
   h2_t a[NB][4], nb[NB][4];
 #pragma unroll
   for (int f = 0; f < NB; f++) q4k_scales<PAR>(hdr[f], kbyte, kmagic, a[f], nb[f]);
-  const h2_t off = h2s(-1024.0f);
+  // low nibbles under the pattern 0x6400 (1024 + u), high nibbles masked in
+  // place under 0x5400 (64.0, mantissa step 1/16 there: 64 + u), both exact;
+  // no shift separates the two nibbles of a byte
+  const h2_t off_lo = h2s(-1024.0f), off_hi = h2s(-64.0f);
+  const uint32_t khi = vconst<0x00F000F0u>(), kmagic_hi = vconst<0x54005400u>();
 #pragma unroll
   for (int s = 0; s < 4; s++) {
     const int g = s >> 1, hi = s & 1;
+    const uint32_t km = hi ? khi : knib, kg = hi ? kmagic_hi : kmagic;
+    const h2_t off = hi ? off_hi : off_lo;
     f16x8_t bf[NB];
 #pragma unroll
     for (int f = 0; f < NB; f++) {
-      const uint32_t w0 = qs[f][g].x >> (4 * hi), w1 = qs[f][g].y >> (4 * hi);
-      bf[f] = __builtin_bit_cast(f16x8_t, make_uint4(fma_pair(and_or(w0, knib, kmagic), a[f][s], nb[f][s], off),
-                                                     fma_pair(and_or(w0 >> 8, knib, kmagic), a[f][s], nb[f][s], off),
-                                                     fma_pair(and_or(w1, knib, kmagic), a[f][s], nb[f][s], off),
-                                                     fma_pair(and_or(w1 >> 8, knib, kmagic), a[f][s], nb[f][s], off)));
+      const uint32_t w0 = qs[f][g].x, w1 = qs[f][g].y;
+      bf[f] = __builtin_bit_cast(f16x8_t, make_uint4(fma_pair(and_or(w0, km, kg), a[f][s], nb[f][s], off),
+                                                     fma_pair(and_or(w0 >> 8, km, kg), a[f][s], nb[f][s], off),
+                                                     fma_pair(and_or(w1, km, kg), a[f][s], nb[f][s], off),
+                                                     fma_pair(and_or(w1 >> 8, km, kg), a[f][s], nb[f][s], off)));
     }
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
