@@ -35,6 +35,9 @@ struct DispatchArgs {
   int32_t* counts;     // [2]: number of slots, number of tiles
   int32_t* plan;       // decode plan (written by the decode routing tail), see plan_ints()
   int max_slots;
+  // the decode routing tail writes the plan only (a forward reads nothing else;
+  // topk_idx, perm, inv, offsets, slots and counts are left as they were)
+  bool plan_only = false;
   int32_t* hist;       // [dispatch_blocks(F)][E] per-block expert counts (multi-block dispatch)
   // prefill: routing weight by permuted position, wpos[p] = topk_w[perm[p]],
   // and the shared expert's sigmoid gate at wpos[F + t]

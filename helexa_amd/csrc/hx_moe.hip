@@ -479,6 +479,7 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
   make_plan(m, x, T, y, (uint8_t*)ws, L, bias, p);
   const bool decode = T <= HX_DECODE_MAX_T;
   const bool fast = decode && decode_fast_ok(p.ea);
+  p.ra.d.plan_only = fast;   // the fast kernels read the plan only
   const bool bf = m->cfg.act_dtype == HX_BF16;
   const int H = m->cfg.hidden_size;
   uint16_t* xn = (uint16_t*)((uint8_t*)ws + L.xn);

@@ -441,59 +441,70 @@ HX_DEV void route_small_lds(const float* logits, int E1, int E, int k, bool norm
   __syncthreads();
 }
 
-// write the routing (and the decode plan) of RouteSmem to global memory
+// write the routing (and the decode plan) of RouteSmem to global memory; with
+// d.plan_only the decode plan and nothing else
 HX_DEV void publish_route(const DispatchArgs& d, float* topk_w, float* sgw, const RouteSmem& sm) {
   const int tid = threadIdx.x, nt = blockDim.x, F = d.F, T = d.T, E = d.E;
+  const bool all = !d.plan_only;
   const int ns = sm.nroute + (d.has_shared ? 1 : 0);
   const int tok0 = 4 + 4 * d.max_slots, w0 = tok0 + F + T, e0 = w0 + F + T;
   for (int f = tid; f < F; f += nt) {
     const int p = sm.pos[f];
-    d.topk_idx[f] = sm.idx[f];
-    topk_w[f] = sm.w[f];
-    d.perm[p] = f;
-    if (d.inv) d.inv[f] = p;
+    if (all) {
+      d.topk_idx[f] = sm.idx[f];
+      topk_w[f] = sm.w[f];
+      d.perm[p] = f;
+      if (d.inv) d.inv[f] = p;
+    }
     d.plan[tok0 + p] = f / d.k;
     d.plan[w0 + p] = __float_as_int(sm.w[f]);
     d.plan[e0 + p] = sm.idx[f];
   }
   for (int t = tid; t < T; t += nt) {
-    sgw[t] = sm.sgw[t];
+    if (all) sgw[t] = sm.sgw[t];
     d.plan[tok0 + F + t] = t;
     d.plan[w0 + F + t] = __float_as_int(sm.sgw[t]);
     d.plan[e0 + F + t] = E;
   }
   for (int u = tid; u < sm.nroute; u += nt) {
+#pragma unroll
     for (int q = 0; q < 3; q++) {
-      d.slots[3 * u + q] = sm.slots[3 * u + q];
+      if (all) d.slots[3 * u + q] = sm.slots[3 * u + q];
       d.plan[4 + 4 * u + q] = sm.slots[3 * u + q];
     }
     d.plan[4 + 4 * u + 3] = sm.perm[sm.slots[3 * u + 1]] / d.k;   // token of the slot's first row
   }
-  // offsets[e] = number of entries routed to experts below e = start of the
-  // first slot whose expert is >= e (F if none): binary search of the slots,
-  // which are in ascending expert order
-  for (int e = tid; e <= E; e += nt) {
-    int lo = 0, hi = sm.nroute;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (sm.slots[3 * mid] < e) lo = mid + 1;
-      else hi = mid;
+  if (all) {
+    // offsets[e] = number of entries routed to experts below e = start of the
+    // first slot whose expert is >= e (F if none): binary search of the slots,
+    // which are in ascending expert order
+    for (int e = tid; e <= E; e += nt) {
+      int lo = 0, hi = sm.nroute;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (sm.slots[3 * mid] < e) lo = mid + 1;
+        else hi = mid;
+      }
+      d.offsets[e] = lo < sm.nroute ? sm.slots[3 * lo + 1] : F;
     }
-    d.offsets[e] = lo < sm.nroute ? sm.slots[3 * lo + 1] : F;
   }
   if (tid == 0) {
     if (d.has_shared) {
       const int u = sm.nroute;
-      d.slots[3 * u + 0] = E;
-      d.slots[3 * u + 1] = F;
-      d.slots[3 * u + 2] = T;
+      if (all) {
+        d.slots[3 * u + 0] = E;
+        d.slots[3 * u + 1] = F;
+        d.slots[3 * u + 2] = T;
+      }
       d.plan[4 + 4 * u + 0] = E;
       d.plan[4 + 4 * u + 1] = F;
       d.plan[4 + 4 * u + 2] = T;
       d.plan[4 + 4 * u + 3] = 0;
     }
-    d.counts[0] = ns;
-    d.counts[1] = 0;
+    if (all) {
+      d.counts[0] = ns;
+      d.counts[1] = 0;
+    }
     d.plan[0] = ns;
   }
 }
