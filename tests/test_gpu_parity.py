@@ -219,6 +219,23 @@ def test_forward_c2_decode_repeated_tokens(c2, pattern):
     assert rel_err(got, c2.oracle.forward(x_np(x))) <= TOL_BF16
 
 
+@pytest.mark.parametrize("T", [1, 4])
+def test_route_after_forward_publishes_everything(c2, T):
+    """a decode forward writes only its plan into the handle's workspace; a
+    route() on the same workspace right after must still publish the whole
+    routing (ids, weights, permutation, offsets), bit-exact"""
+    x = c2.x(T, seed=90 + T)
+    c2.block.forward(x)
+    r = c2.block.route(x)
+    _, _, ix, wt = c2.oracle.route(x_np(x))
+    assert np.array_equal(r["topk_idx"].cpu().numpy(), ix)
+    assert np.array_equal(r["topk_w"].cpu().numpy().view(np.uint32), wt.view(np.uint32))
+    perm, offs, inv = O.dispatch(ix, c2.cfg.num_experts)
+    assert np.array_equal(r["perm"].cpu().numpy(), perm)
+    assert np.array_equal(r["offsets"].cpu().numpy(), offs)
+    assert np.array_equal(r["inv"].cpu().numpy(), inv)
+
+
 @pytest.fixture(scope="module")
 def q4km():
     _, synth = _hx()
