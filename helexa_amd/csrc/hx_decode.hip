@@ -384,7 +384,8 @@ template <int FMT, int LPR, int NR, bool RBF, int TT>
 __global__ __launch_bounds__(256) void k_router_dec(RouterArgs r, ExpertArgs a, int nrb, int nsb) {
   const int wave = threadIdx.x >> 6;
   if ((int)blockIdx.x < nrb) {
-    router_rows<true, RBF, TT, 1>(r, blockIdx.x * 4 + wave, 0);
+    constexpr int RTE = TT > 4 ? 2 : 1;   // router rows per wave
+    router_rows<true, RBF, TT, RTE>(r, (blockIdx.x * 4 + wave) * RTE, 0);
     return;
   }
   if ((int)blockIdx.x >= nrb + nsb) {
@@ -407,19 +408,23 @@ __global__ __launch_bounds__(256) void k_router_dec(RouterArgs r, ExpertArgs a, 
     }
     return;
   }
-  constexpr int RG = 64 / LPR;
-  const int sb = blockIdx.x - nrb;
+  // shared-expert block b: rows of group b / TS for the tokens of part b % TS
+  // (above 4 tokens the tokens are split in two, so each wave's serial token
+  // loop is half as long)
+  constexpr int RG = 64 / LPR, TS = TT > 4 ? 2 : 1;
+  const int b = blockIdx.x - nrb, sb = b / TS, ts = b % TS;
   const int64_t per = (a.sdown.mat_bytes + nsb - 1) / nsb;
-  const int64_t lo = (int64_t)sb * per, n = lo + per < a.sdown.mat_bytes ? per : a.sdown.mat_bytes - lo;
+  const int64_t lo = (int64_t)b * per, n = lo + per < a.sdown.mat_bytes ? per : a.sdown.mat_bytes - lo;
   const Touch pf = n > 0 ? touch_lines(a.sdown.base + lo, n) : Touch{0u, 0u};
+  const int tpp = (a.T + TS - 1) / TS, t0 = ts * tpp, t1 = min(a.T, t0 + tpp);
   int tok[HX_DECODE_MAX_T], hrow[HX_DECODE_MAX_T];
-  for (int j = 0; j < a.T; j++) {
-    tok[j] = j;
-    hrow[j] = a.F + j;
+  for (int j = 0; j < t1 - t0; j++) {
+    tok[j] = t0 + j;
+    hrow[j] = a.F + t0 + j;
   }
   const int row0 = (sb * 4 + wave) * (RG * NR) + lane_id() / LPR;
-  if (row0 - lane_id() / LPR < a.Is)
-    gate_up_rows<FMT, LPR, NR>(a, a.sgate.base, a.sup.base, a.Is, row0, a.T, tok, hrow);
+  if (row0 - lane_id() / LPR < a.Is && t1 > t0)
+    gate_up_rows<FMT, LPR, NR>(a, a.sgate.base, a.sup.base, a.Is, row0, t1 - t0, tok, hrow);
   touch_sink(a, pf);
 }
 
@@ -933,13 +938,20 @@ bool decode_fast_ok(const ExpertArgs& a) {
 
 template <int FMT>
 static hipError_t router_dec_fmt(const RouterArgs& r, const ExpertArgs& a, bool rbf, hipStream_t s) {
-  const int nch = a.H / 32, nrb = (r.E1 + 3) / 4;
+  const int nch = a.H / 32;
   // NR: shared-expert rows per wave (T > 1): one for up to 4 tokens, two for
-  // more (measured on MI355X: more workgroups win while the tokens are few)
+  // more (measured on MI355X: more workgroups win while the tokens are few).
+  // Above 4 tokens (about 300 registers: one workgroup per CU) each wave takes
+  // two router rows and the shared-expert tokens are split over two
+  // workgroups, so the grid (65 + 128 + xcv blocks) fits the 256 CUs at once
+  // and the shared part, which ends the kernel, is half as long per wave
+  // (measured on MI355X at T = 8: 10.1 -> 8.4 us; at T = 4 two rows per wave
+  // were slower)
 #define RD(LPR, RB, TT)                                                                     \
   {                                                                                         \
-    constexpr int RG = 64 / LPR, NR = TT <= 4 ? 1 : 2;                                      \
-    const int nsb = a.Is > 0 && a.T > 1 ? (a.Is + 4 * RG * NR - 1) / (4 * RG * NR) : 0;    \
+    constexpr int RG = 64 / LPR, NR = TT <= 4 ? 1 : 2, RTE = TT > 4 ? 2 : 1, TS = TT > 4 ? 2 : 1; \
+    const int nrb = (r.E1 + 4 * RTE - 1) / (4 * RTE);                                        \
+    const int nsb = a.Is > 0 && a.T > 1 ? TS * ((a.Is + 4 * RG * NR - 1) / (4 * RG * NR)) : 0; \
     const int ncb = a.xcv && a.T > 1 ? (a.T + 3) / 4 : 0;                                   \
     hx_launch(k_router_dec<FMT, LPR, NR, RB, TT>, dim3(nrb + nsb + ncb), dim3(256), 0, s, r, a, nrb, nsb); \
   }
