@@ -236,6 +236,39 @@ def test_route_after_forward_publishes_everything(c2, T):
     assert np.array_equal(r["inv"].cpu().numpy(), inv)
 
 
+@pytest.mark.parametrize("T", [1, 4])
+def test_forward_decode_with_router_bias(q4km, T):
+    """decode with the router-bias hook: the logits are no longer bf16 values
+    (bias added after the rounding); routing through the fast decode kernels
+    against the oracle with the same bias, and the routing itself bit-exact"""
+    _, synth = _hx()
+    bias = synth.zipf_bias(q4km.cfg.num_experts, 1.1, 2.0, 11)
+    x = q4km.x(T, seed=40 + T)
+    r = q4km.block.route(x, router_bias=bias)
+    _, _, ix, wt = q4km.oracle.route(x_np(x), bias=bias.cpu().numpy())
+    assert np.array_equal(r["topk_idx"].cpu().numpy(), ix)
+    assert np.array_equal(r["topk_w"].cpu().numpy().view(np.uint32), wt.view(np.uint32))
+    got = q4km.block.forward(x, router_bias=bias).float().cpu().numpy()
+    assert rel_err(got, q4km.oracle.forward(x_np(x), bias=bias.cpu().numpy())) <= TOL_BF16
+
+
+@pytest.fixture(scope="module")
+def q4km_raw():
+    """the A3B shape with norm_topk_prob = false (raw softmax weights)"""
+    hx, synth = _hx()
+    cfg = hx.TextConfig(hidden_size=2048, num_experts=512, num_experts_per_tok=10, moe_intermediate_size=512,
+                        shared_expert_intermediate_size=512, norm_topk_prob=False)
+    return Case(cfg, synth.FMT_Q4_K_M, 17, O.BF16)
+
+
+@pytest.mark.parametrize("T", [1, 4, 8])
+def test_forward_decode_without_renormalisation(q4km_raw, T):
+    """norm_topk_prob = false through the fast decode kernels, Q4_K_M"""
+    x = q4km_raw.x(T, seed=60 + T)
+    got = q4km_raw.block.forward(x).float().cpu().numpy()
+    assert rel_err(got, q4km_raw.oracle.forward(x_np(x))) <= TOL_BF16
+
+
 @pytest.fixture(scope="module")
 def q4km():
     _, synth = _hx()
