@@ -175,8 +175,9 @@ def bench_decode(args):
     d_us = kern_us.get(dominant, float("nan"))
     achieved = kbytes[dominant] / (d_us * 1e-6) / 1e9
     layer_gbs = total_bytes / (us_per_layer * 1e-6) / 1e9
-    from helexa_amd.profsum import read_pmc
+    from helexa_amd.profsum import read_pmc, read_stats_avg
     traffic = read_pmc(os.path.join(ROOT, "profiles", "c2_decode_pmc.txt"), KERNEL_NAMES[dominant])
+    trace_us = read_stats_avg(os.path.join(ROOT, "profiles", "c2_decode_kernels.txt"), KERNEL_NAMES[dominant])
 
     # the graph's last write of ys[0] came from layer 0 on xs[0]: it must equal an
     # eager forward bit for bit
@@ -200,7 +201,10 @@ def bench_decode(args):
                      "traffic": int(traffic) if traffic else None,
                      "traffic_source": "profiles/c2_decode_pmc.txt (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)"
                      if traffic else None,
-                     "algorithmic_bytes_per_launch": int(kbytes[dominant]), "avg_launch_us": round(d_us, 3)},
+                     "algorithmic_bytes_per_launch": int(kbytes[dominant]), "avg_launch_us": round(d_us, 3),
+                     # the same kernel's average in the committed rocprofv3 trace (a separate,
+                     # profiled run of this command; the events above cannot be read under it)
+                     "trace_avg_us": trace_us, "trace_source": "profiles/c2_decode_kernels.txt" if trace_us else None},
         "layer": {"algorithmic_bytes": int(total_bytes), "achieved_GBs": round(layer_gbs, 1),
                   "hbm_frac": round(layer_gbs / HBM_PEAK_GBS, 4),
                   "kernel_us": {k: round(v, 3) for k, v in kern_us.items()}},

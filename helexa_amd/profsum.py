@@ -123,6 +123,22 @@ def read_pmc(path: str, kernel_substr: str):
     return None
 
 
+def read_stats_avg(path: str, kernel_substr: str):
+    """average duration (us) of the first kernel whose name contains
+    kernel_substr, from a file written by stats(); None if absent"""
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            parts = line.rsplit(None, 5)   # kernel name (may hold spaces), then five numbers
+            if len(parts) == 6 and kernel_substr in parts[0]:
+                try:
+                    return float(parts[2])
+                except ValueError:
+                    continue
+    return None
+
+
 if __name__ == "__main__":
     if sys.argv[1] == "stats":
         print(stats(*sys.argv[2:6]))
