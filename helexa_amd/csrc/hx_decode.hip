@@ -431,7 +431,8 @@ __global__ __launch_bounds__(256) void k_router_dec(RouterArgs r, ExpertArgs a, 
 // ----------------------------------------------------------------------------
 // K2 (T == 1): routed gate/up + SwiGLU. Every workgroup routes the token from
 // the logits in LDS (wave 0) while its other waves compute shared-expert rows.
-// The last grid row's workgroup 0 only publishes routing and plan; workgroup
+// The last grid row's workgroup 0 only publishes the plan (and the routing
+// unless the forward asks for the plan only); workgroup
 // (x, u < last row) computes rows of slot u's expert. (Pulling the expert's
 // down projection into the caches here as well was measured to cost more in
 // this kernel than it saved in the next.)
@@ -485,7 +486,8 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
 // shared expert's row is loaded before routing starts. The KR + 1 dot products
 // of a wave are summed by one reduce-scatter, and wave 2i combines them with
 // wave 2i + 1's into h = silu(gate) * up, stored at the row of h of the
-// expert's dispatch position. Workgroup 0 also publishes routing and plan.
+// expert's dispatch position. Workgroup 0 also publishes the plan (and, unless
+// the forward asks for the plan only, the routing).
 // ----------------------------------------------------------------------------
 template <int FMT, int EPL, int KR>
 __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a) {
