@@ -54,3 +54,19 @@ def test_text_config_from_config_json_and_layer_uses_moe():
     nested = TextConfig.from_config_json('{"model_type": "qwen3_5_moe", "text_config": {"hidden_size": 64, '
                                          '"num_experts": 8, "num_experts_per_tok": 2}}')
     assert nested.num_experts == 8 and nested.hidden_size == 64
+
+
+def test_committed_profile_summaries_parse():
+    """bench.py reads the dominant decode kernel's HBM bytes and traced average
+    back from the committed rocprofv3 summaries: both must parse, and the
+    traffic must be within 5 % of the kernel's algorithmic bytes (11 expert
+    slots x 2 x 1,114,112 B + the token)"""
+    from helexa_amd.profsum import read_pmc, read_stats_avg
+    traffic = read_pmc(os.path.join(ROOT, "profiles", "c2_decode_pmc.txt"), "k_gate_up_dec")
+    avg_us = read_stats_avg(os.path.join(ROOT, "profiles", "c2_decode_kernels.txt"), "k_gate_up_dec")
+    assert traffic is not None and avg_us is not None
+    algorithmic = 11 * 2 * 1114112 + 2 * 2048
+    assert abs(traffic / algorithmic - 1.0) < 0.05
+    assert 1.0 < avg_us < 100.0
+    assert read_stats_avg(os.path.join(ROOT, "profiles", "c3_prefill_kernels.txt"), "k_gate_up_q4k") is not None
+    assert read_pmc(os.path.join(ROOT, "profiles", "c3_prefill_pmc.txt"), "k_gate_up_q4k") is not None
