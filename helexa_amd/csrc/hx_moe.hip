@@ -15,6 +15,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "hx_moe.h"
 #include "hx_internal.h"
 
@@ -28,6 +30,39 @@ static int fail(int code, const char* fmt, ...) {
   vsnprintf(g_err, sizeof g_err, fmt, ap);
   va_end(ap);
   return code;
+}
+
+// ----------------------------------------------------------------------------
+// scratch of hx_moe_forward_noalloc
+// ----------------------------------------------------------------------------
+// The workspace of the no-allocation forward: one copy per device, created with
+// the code object and held until the process ends. On the host `scratch` names
+// only a stand-in, not device memory: host code uses the address
+// hipGetSymbolAddress returns for the current device, taken once per device by
+// scratch_init (from hx_moe_create) and kept in g_scratch_ptr.
+#define HX_SCRATCH_MAX_DEVICES 64
+static __device__ __align__(256) uint8_t scratch[HX_NOALLOC_SCRATCH_BYTES];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[HX_SCRATCH_MAX_DEVICES];
+
+// device must be current
+static int scratch_init(int device) {
+  if (device < 0 || device >= HX_SCRATCH_MAX_DEVICES)
+    return fail(HX_ERR_UNSUPPORTED, "device %d: at most %d devices", device, HX_SCRATCH_MAX_DEVICES);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[device]) return HX_OK;
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p)
+    return fail(HX_ERR_DEVICE, "hipGetSymbolAddress(scratch) on device %d failed: %s", device, hipGetErrorString(e));
+  g_scratch_ptr[device] = p;
+  return HX_OK;
+}
+
+static void* scratch_ptr(int device) {
+  if (device < 0 || device >= HX_SCRATCH_MAX_DEVICES) return nullptr;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  return g_scratch_ptr[device];
 }
 
 #define HX_HIP(call)                                                                               \
@@ -271,6 +306,7 @@ extern "C" int hx_moe_create(const hx_moe_config* cfg, const hx_moe_weights* w, 
       return fail(HX_ERR_UNSUPPORTED, "intermediate size too large");
   }
   if (hipSetDevice(device) != hipSuccess) return fail(HX_ERR_DEVICE, "hipSetDevice(%d) failed", device);
+  if ((rc = scratch_init(device))) return rc;
   hx_moe* m = new hx_moe();
   m->cfg = c;
   m->device = device;
@@ -555,6 +591,22 @@ extern "C" int hx_moe_forward(hx_moe* m, const void* x, int64_t n_tokens, void* 
   if (n_tokens > (int64_t)1 << 24) return fail(HX_ERR_UNSUPPORTED, "too many tokens in one call");
   HX_HIP(hipSetDevice(m->device));
   return forward_impl(m, x, n_tokens, y, workspace, workspace_bytes, router_bias, (hipStream_t)stream);
+}
+
+extern "C" int hx_moe_forward_noalloc(hx_moe* m, const void* x, int64_t n_tokens, void* y,
+                                      const float* router_bias, void* stream) {
+  if (!m || n_tokens < 0 || (n_tokens > 0 && (!x || !y))) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
+  if (n_tokens == 0) return HX_OK;
+  if (n_tokens > (int64_t)1 << 24) return fail(HX_ERR_UNSUPPORTED, "too many tokens in one call");
+  const size_t need = ws_layout(m, n_tokens).total;
+  if (need > HX_NOALLOC_SCRATCH_BYTES)
+    return fail(HX_ERR_WORKSPACE_TOO_SMALL,
+                "hx_moe_forward_noalloc: %lld tokens need %zu bytes of workspace, the scratch holds %zu",
+                (long long)n_tokens, need, (size_t)HX_NOALLOC_SCRATCH_BYTES);
+  void* ws = scratch_ptr(m->device);
+  if (!ws) return fail(HX_ERR_DEVICE, "no scratch on device %d", m->device);
+  HX_HIP(hipSetDevice(m->device));
+  return forward_impl(m, x, n_tokens, y, ws, HX_NOALLOC_SCRATCH_BYTES, router_bias, (hipStream_t)stream);
 }
 
 extern "C" int hx_moe_forward_host(hx_moe* m, const void* x_host, int64_t n_tokens, void* y_host,

@@ -33,7 +33,8 @@ STATUS = {0: "HX_OK", 1: "HX_ERR_INVALID_ARGUMENT", 2: "HX_ERR_UNSUPPORTED", 3: 
           4: "HX_ERR_WORKSPACE_TOO_SMALL", 5: "HX_ERR_OUT_OF_MEMORY"}
 
 # every entry point include/hx_moe.h declares
-EXPORTS = ("hx_moe_create", "hx_moe_destroy", "hx_moe_workspace_size", "hx_moe_forward", "hx_moe_forward_host",
+EXPORTS = ("hx_moe_create", "hx_moe_destroy", "hx_moe_workspace_size", "hx_moe_forward", "hx_moe_forward_noalloc",
+           "hx_moe_forward_host",
            "hx_moe_route", "hx_moe_router_logits", "hx_moe_decoder_mlp", "hx_quantize", "hx_dequantize",
            "hx_row_bytes", "hx_moe_timing_begin", "hx_moe_timing_read", "hx_moe_timing_end", "hx_moe_timing_name", "hx_last_error")
 
@@ -78,6 +79,7 @@ def lib() -> C.CDLL:
             "hx_moe_destroy": (i32, [vp]),
             "hx_moe_workspace_size": (i32, [vp, i64, C.POINTER(C.c_size_t)]),
             "hx_moe_forward": (i32, [vp, vp, i64, vp, vp, C.c_size_t, vp, vp]),
+            "hx_moe_forward_noalloc": (i32, [vp, vp, i64, vp, vp, vp]),
             "hx_moe_forward_host": (i32, [vp, vp, i64, vp, vp]),
             "hx_moe_route": (i32, [vp, vp, i64, vp, vp, vp, vp, vp, vp, vp, C.c_size_t, vp]),
             "hx_moe_router_logits": (i32, [vp, vp, i64, vp, vp, vp]),
@@ -248,6 +250,23 @@ class Qwen3_5MoeBlock:
         check(lib().hx_moe_forward(self._h, _ptr(x), T, _ptr(y), ws_ptr, ws_n, _ptr(router_bias), _stream(stream)),
               "hx_moe_forward")
         return y
+
+    def forward_noalloc(self, xs, out, router_bias=None, stream=None):
+        """forward() through hx_moe_forward_noalloc: no workspace argument and no
+        allocation inside the library (its per-GPU scratch is the workspace). `out`
+        is required, a contiguous tensor of xs's shape and dtype."""
+        if xs.shape[-1] != self.cfg.hidden_size:
+            raise ValueError(f"last dim {xs.shape[-1]} != hidden {self.cfg.hidden_size}")
+        if _act_dtype(xs.dtype) != self.act_dtype:
+            raise TypeError("activation dtype differs from the block's")
+        if not xs.is_contiguous():
+            raise ValueError("xs must be contiguous (no copy is made here)")
+        if out.shape != xs.shape or out.dtype != xs.dtype or not out.is_contiguous():
+            raise ValueError("out must be contiguous with the input's shape and dtype")
+        T = xs.numel() // self.cfg.hidden_size
+        check(lib().hx_moe_forward_noalloc(self._h, _ptr(xs), T, _ptr(out), _ptr(router_bias), _stream(stream)),
+              "hx_moe_forward_noalloc")
+        return out
 
     def route(self, xs, router_bias=None, stream=None):
         """-> dict(topk_idx [T,k] i32, topk_w [T,k] f32, perm [T*k], offsets [E+1], inv [T*k])"""

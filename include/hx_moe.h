@@ -104,6 +104,22 @@ int hx_moe_workspace_size(const hx_moe* m, int64_t n_tokens, size_t* bytes);
 int hx_moe_forward(hx_moe* m, const void* x, int64_t n_tokens, void* y,
                    void* workspace, size_t workspace_bytes, const float* router_bias, void* stream);
 
+/* No counterpart in the reference: hx_moe_forward for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same arguments and results as
+ * hx_moe_forward with a NULL workspace, but the workspace is a fixed scratch
+ * array of HX_NOALLOC_SCRATCH_BYTES in the library's own device memory (one
+ * copy per GPU, set up by hx_moe_create and held until the process ends), so
+ * the call performs no allocation of any kind. n_tokens whose workspace
+ * (hx_moe_workspace_size) exceeds HX_NOALLOC_SCRATCH_BYTES are rejected with
+ * HX_ERR_WORKSPACE_TOO_SMALL; at the 80B-A3B shape the limit holds every
+ * decode batch and prefill chunks of up to 700 tokens. Every call on one GPU
+ * shares that GPU's scratch: calls that overlap on one GPU (other streams,
+ * other threads, other handles) race and must be serialised by the caller. */
+#define HX_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int hx_moe_forward_noalloc(hx_moe* m, const void* x, int64_t n_tokens, void* y, const float* router_bias,
+                           void* stream);
+
 /* Same, for host buffers (what a candle CPU-tensor wrapper calls): copies x in,
  * runs hx_moe_forward on the default stream, copies y out, synchronises. */
 int hx_moe_forward_host(hx_moe* m, const void* x_host, int64_t n_tokens, void* y_host,
