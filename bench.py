@@ -13,16 +13,24 @@ Method
   * The steps are captured into one HIP graph (the library launches three
     kernels per decode step on the capturing stream) and the graph is replayed;
     the timed region is bracketed by torch.cuda.synchronize() on both sides.
-  * Kernel durations for the roofline come from HIP events the library records
-    around each of its kernels (hx_moe_timing_*) on the stream it launches on,
-    over the same steps launched eagerly behind a sleep kernel (so the GPU runs
-    them back to back).
+  * Kernel durations for the roofline come from HIP events the library has
+    recorded by each kernel's own dispatch (hx_moe_timing_*, hipExtLaunchKernel)
+    on the stream it launches on, over 4 x 256 steps launched eagerly behind a
+    0.4 s sleep kernel. `roofline.trace_avg_us` is the same dispatches' average
+    in the committed rocprofv3 trace of this command (the `timed_avg_us` column
+    of profiles/c2_decode_kernels.txt); the two agree to within a few tenths of
+    a percent.
+  * --steps K times exactly K steps (a graph of G steps, G the largest divisor
+    of K up to 256, replayed K / G times).
   * Algorithmic bytes per step are computed from the actual routing (unique
     experts touched) and the GGUF sizes of what must be read once.
   * cpu_baseline: the CPU restatement of the reference's candle path (oracle/)
     on the host cores, on a bounded sample of the same workload.
   * `prefill` (secondary): C3, 2048 tokens of the same layer in Q4_K_M (gate/up
-    Q4_K, down Q6_K), tokens/s with its MFMA and HBM fractions.
+    Q4_K, down Q6_K), tokens/s with its MFMA and HBM fractions, and a roofline
+    object for the gate/up MFMA kernel (event-timed; traced average, HBM traffic
+    and MFMA counters from profiles/). `prefill_512`: the same at the
+    reference's production prefill chunk of 512 tokens.
   * `c5_skew` (secondary): C5, 4096 tokens with a Zipf(1.1) router bias
     calibrated so the top 8 experts take ~40% of the assignments.
   * `c4_stack` (secondary): C4, the 48-layer Q4_K_M stack with RMSNorm and
@@ -137,30 +145,39 @@ def bench_decode(args):
     U = float(np.mean(uniq))
     total_bytes, kbytes = step_bytes(cfg, fmts, U, 1)
 
-    G = 256                                     # steps per graph
+    # exactly args.steps timed steps: a graph of G steps (the largest divisor of
+    # the step count up to 256) replayed steps / G times
+    steps = max(1, args.steps)
+    G = max(d for d in range(1, min(256, steps) + 1) if steps % d == 0)
     g = capture(blocks, xs, ys, wss, G)
-    for _ in range(max(1, args.warmup // G)):
+    for _ in range(max(1, -(-args.warmup // G))):
         g.replay()
     torch.cuda.synchronize()
-    reps = max(1, args.steps // G)
+    reps = steps // G
     t0 = time.perf_counter()
     for _ in range(reps):
         g.replay()
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
-    steps = reps * G
     us_per_layer = dt / steps * 1e6
 
-    # per-kernel durations: the same steps launched eagerly with the library's HIP
-    # events, queued behind a ~30 ms sleep kernel so that the GPU runs them back
-    # to back; for one token each kernel's event pair is recorded by its own
-    # dispatch (hipExtLaunchKernel), the interval a kernel trace reports
+    # the graph's last write of ys[(G - 1) % 64] came from layer (G - 1) % L on
+    # xs[(G - 1) % 64]: it must equal an eager forward bit for bit
+    last = G - 1
+    graph_ok = bool(torch.equal(blocks[last % len(blocks)].forward(xs[last % n_x]), ys[last % n_x]))
+
+    # per-kernel durations: 256 steps launched eagerly with the library's HIP
+    # events, queued behind a 0.4 s sleep kernel (long enough that every launch is
+    # queued before the GPU reaches them, also under a profiler's slower host
+    # side), so the GPU runs them back to back; for one token each kernel's event
+    # pair is recorded by its own dispatch (hipExtLaunchKernel), the interval a
+    # kernel trace reports for the same dispatches
     kern = {}
-    n_t = min(G, 256)
-    for _ in range(max(1, min(reps, 4))):
+    n_t = 256
+    for _ in range(4):
         for b in blocks:
             b.timing_begin((n_t + len(blocks) - 1) // len(blocks))
-        torch.cuda._sleep(int(2.4e9 * 0.03))
+        torch.cuda._sleep(int(2.4e9 * 0.4))
         for i in range(n_t):
             blocks[i % len(blocks)].forward(xs[i % len(xs)], workspace=wss[i % len(blocks)], out=ys[i % len(ys)])
         torch.cuda.synchronize()
@@ -178,10 +195,6 @@ def bench_decode(args):
     from helexa_amd.profsum import read_pmc, read_stats_avg
     traffic = read_pmc(os.path.join(ROOT, "profiles", "c2_decode_pmc.txt"), KERNEL_NAMES[dominant])
     trace_us = read_stats_avg(os.path.join(ROOT, "profiles", "c2_decode_kernels.txt"), KERNEL_NAMES[dominant])
-
-    # the graph's last write of ys[0] came from layer 0 on xs[0]: it must equal an
-    # eager forward bit for bit
-    graph_ok = bool(torch.equal(blocks[0].forward(xs[0]), ys[0]))
 
     out = {
         "metric": METRIC, "value": round(us_per_layer, 3), "unit": "us/layer (C2 decode)",
@@ -233,43 +246,102 @@ def cpu_baseline(cfg, fmts, host0, x0, budget_s):
                       f"oracle/hx_oracle.c scatter loop, {threads} OpenMP threads"}
 
 
-def bench_prefill(T=2048, reps=5):
-    import numpy as np
+PREFILL_KERNELS = {"gate_up": "k_gate_up_q4k", "down": "k_down_q6k", "router": "k_router88"}
+
+
+def prefill_work(cfg, fmts, T, U):
+    """Algorithmic flops and HBM bytes of one prefill forward, in total and for
+    the two MFMA kernels (each needed weight byte once; tokens in/out once; the
+    kernels' own inputs and outputs: f16 tokens, f16 SwiGLU rows h, weighted
+    bf16 rows)."""
+    H, I, Is, E, k = cfg.hidden_size, cfg.moe_intermediate_size, cfg.shared_expert_intermediate_size, \
+        cfg.num_experts, cfg.num_experts_per_tok
+    F = T * k
+    gu_w = U * 2 * gguf_bytes(fmts["gate"], I, H) + 2 * gguf_bytes(fmts["sgate"], Is, H)
+    dn_w = U * gguf_bytes(fmts["down"], H, I) + gguf_bytes(fmts["sdown"], H, Is)
+    flops = {"gate_up": 2 * (F * 2 * H * I + T * 2 * H * Is), "down": 2 * (F * H * I + T * H * Is),
+             "router": 2 * T * H * (E + 1)}
+    kbytes = {"gate_up": gu_w + T * H * 2 + (F + T) * I * 2, "down": dn_w + (F + T) * I * 2 + (F + T) * H * 2,
+              "router": (E + 1) * H * 2 + T * H * 2}
+    total_flops = 2 * T * k * 3 * H * I + 2 * T * 3 * H * Is + 2 * T * H * E
+    total_bytes = gu_w + dn_w + (E + 1) * H * 2 + 2 * T * H * 2
+    return total_flops, total_bytes, flops, kbytes
+
+
+def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=5, bias=None, pmc_file=None, mfma_file=None,
+                trace_file=None):
+    """One prefill line: wall-clock time of `reps` forwards, then the same forwards
+    again with every kernel timed by its own dispatch's HIP events, queued behind
+    a sleep kernel; roofline of the gate/up MFMA kernel (the largest)."""
     import torch
     import helexa_amd as hx
     from helexa_amd import synth
-    cfg, fmts = synth.A3B, synth.FMT_Q4_K_M
-    w = synth.make_weights(cfg, fmts, 4242)
+    from helexa_amd.profsum import read_pmc, read_stats_avg, read_mfma
+    w = synth.make_weights(cfg, fmts, w_seed)
     blk = hx.Qwen3_5MoeBlock.load(cfg, w, act_dtype=hx.BF16)
     del w
-    x = synth.make_x(cfg, T, 77)
+    x = synth.make_x(cfg, T, x_seed)
     ws = torch.empty(blk.workspace_size(T), dtype=torch.uint8, device="cuda")
     y = torch.empty_like(x)
-    idx = blk.route(x)["topk_idx"]
-    U = int(torch.unique(idx).numel())
+    r = blk.route(x, router_bias=bias)
+    U = int(torch.unique(r["topk_idx"]).numel())
+    counts = torch.diff(r["offsets"]).cpu()
     for _ in range(2):
-        blk.forward(x, workspace=ws, out=y)
+        blk.forward(x, router_bias=bias, workspace=ws, out=y)
     torch.cuda.synchronize()
-    blk.timing_begin(reps)
     t0 = time.perf_counter()
     for _ in range(reps):
-        blk.forward(x, workspace=ws, out=y)
+        blk.forward(x, router_bias=bias, workspace=ws, out=y)
     torch.cuda.synchronize()
     dt = (time.perf_counter() - t0) / reps
+    blk.timing_begin(reps)
+    torch.cuda._sleep(int(2.4e9 * 0.05))
+    for _ in range(reps):
+        blk.forward(x, router_bias=bias, workspace=ws, out=y)
+    torch.cuda.synchronize()
     kern = {k: v[0] / v[1] * 1e3 for k, v in blk.timing_end().items() if v[1]}
-    H, I, Is, E, k = cfg.hidden_size, cfg.moe_intermediate_size, cfg.shared_expert_intermediate_size, \
-        cfg.num_experts, cfg.num_experts_per_tok
-    flops = 2 * T * k * 3 * H * I + 2 * T * 3 * H * Is + 2 * T * H * E
-    nbytes = (U * (gguf_bytes(fmts["gate"], I, H) * 2 + gguf_bytes(fmts["down"], H, I))
-              + gguf_bytes(fmts["sgate"], Is, H) * 2 + gguf_bytes(fmts["sdown"], H, Is)
-              + (E + 1) * H * 2 + 2 * T * H * 2)
     blk.close()
-    return {"workload": f"C3: {T}-token prefill, Q4_K_M (gate/up Q4_K, down Q6_K), bf16", "tokens": T,
-            "us": round(dt * 1e6, 1), "tok_per_s": round(T / dt, 1),
-            "mfma_frac": round(flops / dt / (MFMA_BF16_PEAK_TFS * 1e12), 4),
-            "hbm_frac": round(nbytes / dt / (HBM_PEAK_GBS * 1e9), 4),
-            "algorithmic_flops": flops, "algorithmic_bytes": nbytes, "unique_experts": U,
-            "kernel_us": {k: round(v, 1) for k, v in kern.items()}}
+    total_flops, total_bytes, kflops, kbytes = prefill_work(cfg, fmts, T, U)
+    d_us = kern.get("gate_up", float("nan"))
+    tfs = kflops["gate_up"] / (d_us * 1e-6) / 1e12
+    roof = {"bound": "mfma", "kernel": "gate_up (" + PREFILL_KERNELS["gate_up"] + ")", "achieved": round(tfs, 1),
+            "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s", "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4),
+            "algorithmic_flops_per_launch": kflops["gate_up"], "algorithmic_bytes_per_launch": kbytes["gate_up"],
+            "avg_launch_us": round(d_us, 2),
+            "hbm_frac": round(kbytes["gate_up"] / (d_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
+    if pmc_file:
+        tr = read_pmc(os.path.join(ROOT, "profiles", pmc_file), PREFILL_KERNELS["gate_up"])
+        roof["traffic"] = int(tr) if tr else None
+        roof["traffic_source"] = f"profiles/{pmc_file} (FETCH_SIZE + WRITE_SIZE, copy-calibrated)" if tr else None
+    if trace_file:
+        roof["trace_avg_us"] = read_stats_avg(os.path.join(ROOT, "profiles", trace_file), PREFILL_KERNELS["gate_up"])
+        roof["trace_source"] = f"profiles/{trace_file}"
+    if mfma_file:
+        mf = read_mfma(os.path.join(ROOT, "profiles", mfma_file), PREFILL_KERNELS["gate_up"])
+        if mf:
+            roof["mfma_counters"] = mf
+            roof["mfma_source"] = f"profiles/{mfma_file}"
+    kr = {k: {"us": round(v, 1),
+              "mfma_frac": round(kflops[k] / (v * 1e-6) / (MFMA_BF16_PEAK_TFS * 1e12), 4) if k in kflops else None,
+              "hbm_frac": round(kbytes[k] / (v * 1e-6) / (HBM_PEAK_GBS * 1e9), 4) if k in kbytes else None}
+          for k, v in kern.items()}
+    return {"workload": workload, "tokens": T, "us": round(dt * 1e6, 1), "tok_per_s": round(T / dt, 1),
+            "mfma_frac": round(total_flops / dt / (MFMA_BF16_PEAK_TFS * 1e12), 4),
+            "hbm_frac": round(total_bytes / dt / (HBM_PEAK_GBS * 1e9), 4),
+            "algorithmic_flops": total_flops, "algorithmic_bytes": total_bytes, "unique_experts": U,
+            "max_expert_rows": int(counts.max()), "roofline": roof, "kernels": kr}
+
+
+def bench_prefill(T=2048, reps=5):
+    """C3 (T = 2048) and the production chunk (T = 512): Q4_K_M prefill, seeded
+    near-uniform routing"""
+    from helexa_amd import synth
+    tag = "C3" if T == 2048 else "production chunk"
+    return prefill_run(synth.A3B, synth.FMT_Q4_K_M, 4242, 77, T,
+                       f"{tag}: {T}-token prefill, Q4_K_M (gate/up Q4_K, down Q6_K), bf16", reps,
+                       pmc_file="c3_prefill_pmc.txt" if T == 2048 else None,
+                       mfma_file="c3_prefill_mfma.txt" if T == 2048 else None,
+                       trace_file="c3_prefill_kernels.txt" if T == 2048 else None)
 
 
 def bench_c4(n_layers=48, batches=(1, 4, 8), reps=20):
@@ -349,7 +421,6 @@ def bench_c5(T=4096, target_share=0.40, reps=5):
     """C5: 4096-token prefill of the Q4_K_M layer with a seeded Zipf(1.1) router
     bias (router_bias[e] = alpha ln p_{pi(e)}), alpha calibrated on this layer so
     the top 8 experts take about 40% of the assignments."""
-    import numpy as np
     import torch
     import helexa_amd as hx
     from helexa_amd import synth
@@ -358,7 +429,7 @@ def bench_c5(T=4096, target_share=0.40, reps=5):
     blk = hx.Qwen3_5MoeBlock.load(cfg, w, act_dtype=hx.BF16)
     del w
     x = synth.make_x(cfg, T, 78)
-    E, k = cfg.num_experts, cfg.num_experts_per_tok
+    E = cfg.num_experts
     base = synth.zipf_bias(E, 1.1, 1.0, 11)
     top8 = torch.argsort(base, descending=True)[:8]
 
@@ -374,36 +445,13 @@ def bench_c5(T=4096, target_share=0.40, reps=5):
         else:
             hi = mid
     alpha = 0.5 * (lo + hi)
-    bias = base * alpha
     achieved = share(alpha)
-    r = blk.route(x, router_bias=bias)
-    counts = np.diff(r["offsets"].cpu().numpy())
-    U = int((counts > 0).sum())
-    ws = torch.empty(blk.workspace_size(T), dtype=torch.uint8, device="cuda")
-    y = torch.empty_like(x)
-    for _ in range(2):
-        blk.forward(x, router_bias=bias, workspace=ws, out=y)
-    torch.cuda.synchronize()
-    blk.timing_begin(reps)
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        blk.forward(x, router_bias=bias, workspace=ws, out=y)
-    torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / reps
-    kern = {kk: v[0] / v[1] * 1e3 for kk, v in blk.timing_end().items() if v[1]}
-    H, I, Is = cfg.hidden_size, cfg.moe_intermediate_size, cfg.shared_expert_intermediate_size
-    flops = 2 * T * k * 3 * H * I + 2 * T * 3 * H * Is + 2 * T * H * E
-    nbytes = (U * (gguf_bytes(fmts["gate"], I, H) * 2 + gguf_bytes(fmts["down"], H, I))
-              + gguf_bytes(fmts["sgate"], Is, H) * 2 + gguf_bytes(fmts["sdown"], H, Is)
-              + (E + 1) * H * 2 + 2 * T * H * 2)
     blk.close()
-    return {"workload": f"C5: {T}-token prefill, Q4_K_M, Zipf(1.1) router bias", "tokens": T,
-            "alpha": round(alpha, 4), "top8_share": round(achieved, 4), "max_expert_rows": int(counts.max()),
-            "unique_experts": U, "us": round(dt * 1e6, 1), "tok_per_s": round(T / dt, 1),
-            "mfma_frac": round(flops / dt / (MFMA_BF16_PEAK_TFS * 1e12), 4),
-            "hbm_frac": round(nbytes / dt / (HBM_PEAK_GBS * 1e9), 4),
-            "algorithmic_flops": flops, "algorithmic_bytes": nbytes,
-            "kernel_us": {kk: round(v, 1) for kk, v in kern.items()}}
+    del blk
+    out = prefill_run(cfg, fmts, 4243, 78, T, f"C5: {T}-token prefill, Q4_K_M, Zipf(1.1) router bias", reps,
+                      bias=base * alpha, mfma_file="c5_prefill_mfma.txt", trace_file="c5_prefill_kernels.txt")
+    out.update({"alpha": round(alpha, 4), "top8_share": round(achieved, 4)})
+    return out
 
 
 def probe(args):
@@ -441,6 +489,7 @@ def main():
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--probe", action="store_true", help="short workload for rocprofv3 --pmc runs")
     ap.add_argument("--prefill-only", action="store_true", help="only the C3 prefill line (for profiling)")
+    ap.add_argument("--c5-only", action="store_true", help="only the C5 skewed prefill line (for profiling)")
     ap.add_argument("--no-c4", action="store_true", help="skip the 48-layer stack line")
     ap.add_argument("--no-c5", action="store_true", help="skip the skewed 4096-token prefill line")
     args = ap.parse_args()
@@ -459,6 +508,9 @@ def main():
     if args.prefill_only:
         print(json.dumps(bench_prefill()), flush=True)
         return
+    if args.c5_only:
+        print(json.dumps(bench_c5()), flush=True)
+        return
     out, blocks, host0, xs = bench_decode(args)
     log(f"[bench] decode {out['value']} us/layer; kernels {out['layer']['kernel_us']}")
     if not args.no_cpu:
@@ -473,6 +525,9 @@ def main():
     if not args.no_prefill:
         log("[bench] prefill")
         out["prefill"] = bench_prefill()
+        torch.cuda.empty_cache()
+        log("[bench] prefill, production chunk of 512 tokens")
+        out["prefill_512"] = bench_prefill(512)
         torch.cuda.empty_cache()
     if not args.no_c5:
         log("[bench] C5 skewed prefill")

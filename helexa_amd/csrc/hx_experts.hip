@@ -447,7 +447,7 @@ hipError_t launch_down_prefill(const ExpertArgs& a, hipStream_t s) {
 
 hipError_t launch_combine(const ExpertArgs& a, hipStream_t s) {
   // H % 8 == 0 holds for every block this library creates with a combine step
-  hipLaunchKernelGGL(k_combine, dim3((unsigned)a.T, (unsigned)((a.H / 8 + 255) / 256)), dim3(256), 0, s, a);
+  hx_launch(k_combine, dim3((unsigned)a.T, (unsigned)((a.H / 8 + 255) / 256)), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 

@@ -146,6 +146,7 @@ hipError_t launch_gate_up_gemv(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_down_gemv_combine(const ExpertArgs& a, hipStream_t s);
 // prefill
 bool prefill_mfma_ok(const ExpertArgs& a);   // bf16 activations, GGUF experts: MFMA grouped GEMMs
+hipError_t launch_x_to_f16(const ExpertArgs& a, hipStream_t s);       // tokens -> f16 for the MFMA kernels
 hipError_t launch_gate_up_mfma(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_down_mfma(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_gate_up_prefill(const ExpertArgs& a, hipStream_t s);

@@ -83,11 +83,12 @@ extern "C" int64_t hx_row_bytes(int dtype, int64_t n) {
 // ----------------------------------------------------------------------------
 // timing slots
 // ----------------------------------------------------------------------------
-enum { SLOT_ROUTER = 0, SLOT_ROUTE_TOKENS, SLOT_DISPATCH, SLOT_GATE_UP, SLOT_DOWN, SLOT_COMBINE, N_SLOTS };
-static const char* kSlotNames[N_SLOTS] = {"router", "route_tokens", "dispatch", "gate_up", "down", "combine"};
+enum { SLOT_ROUTER = 0, SLOT_ROUTE_TOKENS, SLOT_DISPATCH, SLOT_GATE_UP, SLOT_DOWN, SLOT_COMBINE, SLOT_X_F16, N_SLOTS };
+static const char* kSlotNames[N_SLOTS] = {"router", "route_tokens", "dispatch", "gate_up", "down", "combine", "x_f16"};
 
 struct Timing {
   bool on = false;
+  bool ext_armed = false;   // tm_ext handed this call's events to the next hx_launch
   int max_calls = 0, calls = 0;
   std::vector<hipEvent_t> ev;  // [max_calls][N_SLOTS][2]
   std::vector<int> used;       // [max_calls][N_SLOTS]
@@ -440,14 +441,19 @@ thread_local ExtTiming g_ext_timing;
 }
 
 // event helpers for the optional per-kernel timing
-static void tm_mark(hx_moe* m, int slot, int which, hipStream_t s) {
-  Timing& t = m->tm;
-  if (!t.on || t.calls >= t.max_calls) return;
-  hipEvent_t ev = t.ev[((size_t)t.calls * N_SLOTS + slot) * 2 + which];
+// forwards recorded under stream capture are not timed: no event is recorded
+// into the graph, no slot is marked and the call is not counted
+static bool capturing(hipStream_t s) {
   hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
   (void)hipStreamIsCapturing(s, &st);
-  // timing events are not recorded into graphs under capture
-  if (st == hipStreamCaptureStatusNone) (void)hipEventRecord(ev, s);
+  return st != hipStreamCaptureStatusNone;
+}
+
+static void tm_mark(hx_moe* m, int slot, int which, hipStream_t s) {
+  Timing& t = m->tm;
+  if (!t.on || t.calls >= t.max_calls || capturing(s)) return;
+  hipEvent_t ev = t.ev[((size_t)t.calls * N_SLOTS + slot) * 2 + which];
+  (void)hipEventRecord(ev, s);
   if (which == 1) t.used[(size_t)t.calls * N_SLOTS + slot] = 1;
 }
 
@@ -457,18 +463,18 @@ static void tm_mark(hx_moe* m, int slot, int which, hipStream_t s) {
 // untimed for this call)
 static void tm_ext(hx_moe* m, int slot, hipStream_t s) {
   Timing& t = m->tm;
-  if (!t.on || t.calls >= t.max_calls) return;
-  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-  (void)hipStreamIsCapturing(s, &st);
-  if (st != hipStreamCaptureStatusNone) return;
+  t.ext_armed = false;
+  if (!t.on || t.calls >= t.max_calls || capturing(s)) return;
   const size_t k = ((size_t)t.calls * N_SLOTS + slot) * 2;
   g_ext_timing.start = t.ev[k];
   g_ext_timing.stop = t.ev[k + 1];
+  t.ext_armed = true;
 }
 static void tm_ext_done(hx_moe* m, int slot) {
   Timing& t = m->tm;
-  if (!t.on || t.calls >= t.max_calls) return;
-  if (g_ext_timing.start) {
+  if (!t.ext_armed) return;
+  t.ext_armed = false;
+  if (g_ext_timing.start) {   // no launch consumed the events
     g_ext_timing.start = g_ext_timing.stop = nullptr;
     return;
   }
@@ -477,19 +483,19 @@ static void tm_ext_done(hx_moe* m, int slot) {
 
 static int run_routing(hx_moe* m, Plan& p, hipStream_t s) {
   const bool xbf = m->cfg.act_dtype == HX_BF16, rbf = m->rdt == HX_BF16;
-  tm_mark(m, SLOT_ROUTER, 0, s);
+  tm_ext(m, SLOT_ROUTER, s);
   launch_router(p.ra, xbf, rbf, s);
-  tm_mark(m, SLOT_ROUTER, 1, s);
+  tm_ext_done(m, SLOT_ROUTER);
   HX_HIP(hipGetLastError());
   if (p.ra.T <= HX_DECODE_MAX_T) {
-    tm_mark(m, SLOT_ROUTE_TOKENS, 0, s);
+    tm_ext(m, SLOT_ROUTE_TOKENS, s);
     launch_route_small(p.ra, s);
-    tm_mark(m, SLOT_ROUTE_TOKENS, 1, s);
+    tm_ext_done(m, SLOT_ROUTE_TOKENS);
     HX_HIP(hipGetLastError());
   } else {
-    tm_mark(m, SLOT_ROUTE_TOKENS, 0, s);
+    tm_ext(m, SLOT_ROUTE_TOKENS, s);
     launch_route_tokens(p.ra, s);
-    tm_mark(m, SLOT_ROUTE_TOKENS, 1, s);
+    tm_ext_done(m, SLOT_ROUTE_TOKENS);
     HX_HIP(hipGetLastError());
     tm_mark(m, SLOT_DISPATCH, 0, s);
     launch_dispatch(p.ra.d, s);
@@ -569,18 +575,31 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
   } else {
     if ((rc = run_routing(m, p, s))) return rc;
     const bool mfma = prefill_mfma_ok(p.ea);
-    tm_mark(m, SLOT_GATE_UP, 0, s);
-    HX_HIP(mfma ? launch_gate_up_mfma(p.ea, s) : launch_gate_up_prefill(p.ea, s));
-    tm_mark(m, SLOT_GATE_UP, 1, s);
-    tm_mark(m, SLOT_DOWN, 0, s);
-    HX_HIP(mfma ? launch_down_mfma(p.ea, s) : launch_down_prefill(p.ea, s));
-    tm_mark(m, SLOT_DOWN, 1, s);
-    tm_mark(m, SLOT_COMBINE, 0, s);
+    // MFMA path: one kernel per slot, each timed by its own dispatch
+    if (mfma) {
+      tm_ext(m, SLOT_X_F16, s);
+      HX_HIP(launch_x_to_f16(p.ea, s));
+      tm_ext_done(m, SLOT_X_F16);
+      tm_ext(m, SLOT_GATE_UP, s);
+      HX_HIP(launch_gate_up_mfma(p.ea, s));
+      tm_ext_done(m, SLOT_GATE_UP);
+      tm_ext(m, SLOT_DOWN, s);
+      HX_HIP(launch_down_mfma(p.ea, s));
+      tm_ext_done(m, SLOT_DOWN);
+    } else {
+      tm_mark(m, SLOT_GATE_UP, 0, s);
+      HX_HIP(launch_gate_up_prefill(p.ea, s));
+      tm_mark(m, SLOT_GATE_UP, 1, s);
+      tm_mark(m, SLOT_DOWN, 0, s);
+      HX_HIP(launch_down_prefill(p.ea, s));
+      tm_mark(m, SLOT_DOWN, 1, s);
+    }
+    tm_ext(m, SLOT_COMBINE, s);
     HX_HIP(launch_combine(p.ea, s));
-    tm_mark(m, SLOT_COMBINE, 1, s);
+    tm_ext_done(m, SLOT_COMBINE);
   }
   if (fz && !p.ea.resid) HX_HIP(launch_residual_add(fz->x, y, bf, T * H, s));
-  if (m->tm.on && m->tm.calls < m->tm.max_calls) m->tm.calls++;
+  if (m->tm.on && m->tm.calls < m->tm.max_calls && !capturing(s)) m->tm.calls++;
   return HX_OK;
 }
 

@@ -889,14 +889,19 @@ bool prefill_mfma_ok(const ExpertArgs& a) {
   return a.xbf && q(a.gate.fmt) && q(a.down.fmt) && a.H % 256 == 0 && a.I % 256 == 0 && (a.Is == 0 || a.Is == a.I);
 }
 
-hipError_t launch_gate_up_mfma(const ExpertArgs& a, hipStream_t s) {
+hipError_t launch_x_to_f16(const ExpertArgs& a, hipStream_t s) {
   const int64_t n8 = (int64_t)a.T * a.H / 8;
-  hipLaunchKernelGGL(k_x_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, (const uint16_t*)a.x, n8, a.xh);
+  hx_launch(k_x_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, (const uint16_t*)a.x, n8, a.xh);
+  return hipGetLastError();
+}
+
+// reads the f16 tokens launch_x_to_f16 wrote
+hipError_t launch_gate_up_mfma(const ExpertArgs& a, hipStream_t s) {
   const dim3 grid(a.I / 64, (a.max_tiles + 7) / 8 * 8);
   switch (a.gate.fmt) {
-    case HX_Q4_K: hipLaunchKernelGGL((k_gate_up_q4k<1, 4>), grid, dim3(256), 0, s, a); break;
-    case HX_Q8_0: hipLaunchKernelGGL(k_gate_up_mfma<HX_Q8_0>, grid, dim3(256), 0, s, a); break;
-    case HX_Q6_K: hipLaunchKernelGGL(k_gate_up_mfma<HX_Q6_K>, grid, dim3(256), 0, s, a); break;
+    case HX_Q4_K: hx_launch(k_gate_up_q4k<1, 4>, grid, dim3(256), 0, s, a); break;
+    case HX_Q8_0: hx_launch(k_gate_up_mfma<HX_Q8_0>, grid, dim3(256), 0, s, a); break;
+    case HX_Q6_K: hx_launch(k_gate_up_mfma<HX_Q6_K>, grid, dim3(256), 0, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -905,11 +910,11 @@ hipError_t launch_gate_up_mfma(const ExpertArgs& a, hipStream_t s) {
 hipError_t launch_down_mfma(const ExpertArgs& a, hipStream_t s) {
   const dim3 grid(a.H / 128, (a.max_tiles + 7) / 8 * 8);
   switch (a.down.fmt) {
-    case HX_Q4_K: hipLaunchKernelGGL(k_down_mfma<HX_Q4_K>, grid, dim3(256), 0, s, a); break;
-    case HX_Q8_0: hipLaunchKernelGGL(k_down_mfma<HX_Q8_0>, grid, dim3(256), 0, s, a); break;
+    case HX_Q4_K: hx_launch(k_down_mfma<HX_Q4_K>, grid, dim3(256), 0, s, a); break;
+    case HX_Q8_0: hx_launch(k_down_mfma<HX_Q8_0>, grid, dim3(256), 0, s, a); break;
     case HX_Q6_K:
-      if (a.I == DQ_K && a.wpos) hipLaunchKernelGGL(k_down_q6k, grid, dim3(256), 0, s, a);
-      else hipLaunchKernelGGL(k_down_mfma<HX_Q6_K>, grid, dim3(256), 0, s, a);
+      if (a.I == DQ_K && a.wpos) hx_launch(k_down_q6k, grid, dim3(256), 0, s, a);
+      else hx_launch(k_down_mfma<HX_Q6_K>, grid, dim3(256), 0, s, a);
       break;
     default: return hipErrorInvalidValue;
   }

@@ -386,19 +386,19 @@ template <bool XBF, bool RBF>
 static void launch_router_t(const RouterArgs& a, hipStream_t s) {
   if (a.T <= 2) {
     dim3 grid((a.E1 + 3) / 4, ((a.T + 1) / 2 + 7) / 8 * 8);
-    hipLaunchKernelGGL((k_router<XBF, RBF, 2, 1>), grid, dim3(256), 0, s, a);
+    hx_launch(k_router<XBF, RBF, 2, 1>, grid, dim3(256), 0, s, a);
   } else if (a.T <= HX_DECODE_MAX_T) {
     dim3 grid((a.E1 + 3) / 4, ((a.T + 7) / 8 + 7) / 8 * 8);
-    hipLaunchKernelGGL((k_router<XBF, RBF, 8, 1>), grid, dim3(256), 0, s, a);
+    hx_launch(k_router<XBF, RBF, 8, 1>, grid, dim3(256), 0, s, a);
   } else if (a.H % 8 == 0 && a.H <= 8 * 256) {
     dim3 grid((a.E1 + 31) / 32, ((a.T + 7) / 8 + 7) / 8 * 8);
-    if (a.H <= 8 * 64) hipLaunchKernelGGL((k_router88<XBF, RBF, 1>), grid, dim3(256), 0, s, a);
-    else if (a.H <= 8 * 128) hipLaunchKernelGGL((k_router88<XBF, RBF, 2>), grid, dim3(256), 0, s, a);
-    else hipLaunchKernelGGL((k_router88<XBF, RBF, 4>), grid, dim3(256), 0, s, a);
+    if (a.H <= 8 * 64) hx_launch(k_router88<XBF, RBF, 1>, grid, dim3(256), 0, s, a);
+    else if (a.H <= 8 * 128) hx_launch(k_router88<XBF, RBF, 2>, grid, dim3(256), 0, s, a);
+    else hx_launch(k_router88<XBF, RBF, 4>, grid, dim3(256), 0, s, a);
   } else {
     constexpr int TT = 8, TE = 4;
     dim3 grid((a.E1 + 4 * TE - 1) / (4 * TE), ((a.T + TT - 1) / TT + 7) / 8 * 8);
-    hipLaunchKernelGGL((k_router<XBF, RBF, TT, TE>), grid, dim3(256), 0, s, a);
+    hx_launch(k_router<XBF, RBF, TT, TE>, grid, dim3(256), 0, s, a);
   }
 }
 
@@ -410,14 +410,14 @@ void launch_router(const RouterArgs& a, bool xbf, bool rbf, hipStream_t s) {
 }
 
 void launch_route_small(const RouterArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(k_route_small, dim3(1), dim3(a.T > 4 ? 512 : 256), 0, s, a);
+  hx_launch(k_route_small, dim3(1), dim3(a.T > 4 ? 512 : 256), 0, s, a);
 }
 
 void launch_route_tokens(const RouterArgs& a, hipStream_t s) {
   const dim3 g((a.T + 3) / 4), b(256);
 #define RT(EPL)                                                                                           \
-  hipLaunchKernelGGL(k_route_tokens<EPL>, g, b, 0, s, a.logits, a.E1, a.T, a.E, a.k, a.norm, a.has_shared, \
-                     a.d.topk_idx, a.topk_w, a.sgw)
+  hx_launch(k_route_tokens<EPL>, g, b, 0, s, (const float*)a.logits, a.E1, a.T, a.E, a.k, a.norm, a.has_shared, \
+            a.d.topk_idx, a.topk_w, a.sgw)
   if (a.E <= 64) RT(1);
   else if (a.E <= 128) RT(2);
   else if (a.E <= 256) RT(4);
