@@ -4,9 +4,9 @@
 //
 // Reference: quantize_parallel / quantize_blocks
 // (crates/neuron/src/harness/tp/isq.rs:39-113): f32 rows, last dim tiled by the
-// block size, blocks independent. The per-block search here is our own
-// (documented in the quantiser below) and is byte-identical to the library's
-// CPU quantiser; Qwen3_5RmsNorm (crates/neuron/src/harness/arch/qwen3_5/rmsnorm.rs:67-80).
+// block size, blocks independent, each quantised by candle's from_float block
+// rule (restated below); Qwen3_5RmsNorm
+// (crates/neuron/src/harness/arch/qwen3_5/rmsnorm.rs:67-80).
 #include "hx_internal.h"
 
 namespace hx {
@@ -31,138 +31,257 @@ int64_t gguf_block_bytes(int fmt) {
   }
 }
 
-HX_DEV int nearest_int(float v) { return (int)__builtin_rintf(v); }
-
 HX_DEV void st_u16(uint8_t* p, uint16_t v) {
   p[0] = (uint8_t)(v & 0xff);
   p[1] = (uint8_t)(v >> 8);
 }
 HX_DEV uint16_t ld_u16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
 
-// Q8_0: d = amax / 127, q = round-to-nearest-even(x / d)
+// ---------------------------------------------------------------- quantiser
+// The block rules of candle's GgmlType::from_float, which quantize_parallel
+// calls per block (isq.rs:98, 104-112; isq.rs:1-19 and 123-161 hold it
+// byte-identical to candle's QTensor::quantize). candle's k_quants port of
+// ggml's first k_quants.c reference quantisers, restated from the published
+// algorithms: one thread per block, every float operation in the published
+// order (no contraction), so the bytes equal the CPU restatement's.
+
+// candle's nearest_int: f32::round (half away from zero), then Rust's
+// saturating float -> i32 cast (NaN -> 0)
+HX_DEV int rs_nearest(float v) {
+  const float r = roundf(v);
+  if (r != r) return 0;
+  if (r >= 2147483648.0f) return 2147483647;
+  if (r < -2147483648.0f) return -2147483647 - 1;
+  return (int)r;
+}
+HX_DEV int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+// Q8_0 (BlockQ8_0::from_float): d = amax / 127, q = (i8)round(x * (1 / d))
 HX_DEV void qz_q8_0(const float* x, uint8_t* b) {
   float amax = 0.0f;
-  for (int j = 0; j < 32; j++) {
-    float a = fabsf(x[j]);
-    if (a > amax) amax = a;
-  }
-  float d = amax / 127.0f;
-  float id = d != 0.0f ? 1.0f / d : 0.0f;
+  for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(x[j]));
+  const float d = amax / 127.0f;
+  const float id = d != 0.0f ? 1.0f / d : 0.0f;
   st_u16(b, f32_to_f16(d));
   for (int j = 0; j < 32; j++) {
-    int q = nearest_int(x[j] * id);
-    q = q > 127 ? 127 : (q < -127 ? -127 : q);
+    const float r = roundf(x[j] * id);   // Rust `as i8`: saturating, NaN -> 0
+    const int q = r != r ? 0 : (r >= 127.0f ? 127 : (r <= -128.0f ? -128 : (int)r));
     b[2 + j] = (uint8_t)(int8_t)q;
   }
 }
 
-// Q4_K: per 32-element sub-block, min = min(0, min x), scale = (max - min) / 15;
-// the 8 scales and 8 mins quantised to 6 bits against their maxima; then each
-// element re-fitted to 4 bits with the stored (f16, 6-bit) scale and min.
+// make_qkx1_quants(nmax, ntry, x[n]) -> (scale, -min): codes
+// clamp(round((x - min) / scale), 0, nmax) alternated with the least-squares
+// scale and the mean-residual min (<= 0), from min = min(0, min x) and
+// scale = (max - min) / nmax, until the codes stop changing or ntry rounds
+HX_DEV void make_qkx1(const float* x, int n, int nmax, int ntry, float& scale_out, float& min_out) {
+  float mn = x[0], mx = x[0];
+  for (int i = 1; i < n; i++) {
+    const float v = x[i];
+    mn = v < mn ? v : mn;
+    mx = v > mx ? v : mx;
+  }
+  if (mx == mn) {
+    scale_out = 0.0f;
+    min_out = 0.0f;
+    return;
+  }
+  if (mn > 0.0f) mn = 0.0f;
+  float iscale = (float)nmax / (mx - mn);
+  float scale = 1.0f / iscale;
+  uint8_t L[32];
+  for (int i = 0; i < n; i++) L[i] = 0;
+  for (int t = 0; t < ntry; t++) {
+    float sumlx = 0.0f;
+    int suml2 = 0;
+    bool changed = false;
+    for (int i = 0; i < n; i++) {
+      const int li = clampi(rs_nearest(iscale * (x[i] - mn)), 0, nmax);
+      if ((uint8_t)li != L[i]) {
+        L[i] = (uint8_t)li;
+        changed = true;
+      }
+      sumlx += (x[i] - mn) * (float)li;
+      suml2 += li * li;
+    }
+    scale = sumlx / (float)suml2;
+    float sum = -0.0f;
+    for (int i = 0; i < n; i++) sum += x[i] - scale * (float)L[i];
+    mn = sum / (float)n;
+    if (mn > 0.0f) mn = 0.0f;
+    iscale = 1.0f / scale;
+    if (!changed) break;
+  }
+  scale_out = scale;
+  min_out = -mn;
+}
+
+// Q4_K (BlockQ4K::from_float): make_qkx1_quants(15, 5) per 32 elements; scales
+// and mins to 6 bits against their maxima; codes re-fitted with the stored ones
 HX_DEV void qz_q4_k(const float* x, uint8_t* b) {
-  float scale[8], mins[8];
+  float scales[8], mins[8];
+  for (int j = 0; j < 8; j++) make_qkx1(x + 32 * j, 32, 15, 5, scales[j], mins[j]);
   float max_scale = 0.0f, max_min = 0.0f;
   for (int j = 0; j < 8; j++) {
-    float mn = 0.0f, mx = x[32 * j];
-    for (int l = 0; l < 32; l++) {
-      float v = x[32 * j + l];
-      if (v < mn) mn = v;
-      if (v > mx) mx = v;
-    }
-    scale[j] = (mx - mn) / 15.0f;
-    mins[j] = -mn;
-    if (scale[j] > max_scale) max_scale = scale[j];
-    if (mins[j] > max_min) max_min = mins[j];
+    max_scale = fmaxf(scales[j], max_scale);
+    max_min = fmaxf(mins[j], max_min);
   }
-  float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
-  float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
-  uint8_t ls[8], lm[8];
+  const float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
+  const float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
+  uint8_t s[12];
+  for (int j = 0; j < 12; j++) s[j] = 0;
   for (int j = 0; j < 8; j++) {
-    int a = nearest_int(inv_scale * scale[j]), m = nearest_int(inv_min * mins[j]);
-    ls[j] = (uint8_t)(a > 63 ? 63 : a);
-    lm[j] = (uint8_t)(m > 63 ? 63 : m);
+    const int a = rs_nearest(inv_scale * scales[j]), m = rs_nearest(inv_min * mins[j]);
+    const uint8_t ls = (uint8_t)(a < 63 ? a : 63), lm = (uint8_t)(m < 63 ? m : 63);
+    if (j < 4) {
+      s[j] = ls;
+      s[j + 4] = lm;
+    } else {
+      s[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+      s[j - 4] |= (uint8_t)((ls >> 4) << 6);
+      s[j] |= (uint8_t)((lm >> 4) << 6);
+    }
   }
-  uint16_t dh = f32_to_f16(max_scale / 63.0f), mh = f32_to_f16(max_min / 63.0f);
+  const uint16_t dh = f32_to_f16(max_scale / 63.0f), mh = f32_to_f16(max_min / 63.0f);
   st_u16(b, dh);
   st_u16(b + 2, mh);
-  uint8_t* s = b + 4;
-  for (int j = 0; j < 4; j++) {
-    s[j] = (uint8_t)((ls[j] & 63) | ((ls[j + 4] >> 4) << 6));
-    s[j + 4] = (uint8_t)((lm[j] & 63) | ((lm[j + 4] >> 4) << 6));
-    s[j + 8] = (uint8_t)((ls[j + 4] & 0xF) | ((lm[j + 4] & 0xF) << 4));
-  }
-  float d = f16_to_f32(dh), dmin = f16_to_f32(mh);
+  for (int j = 0; j < 12; j++) b[4 + j] = s[j];
+  const float d = f16_to_f32(dh), dmin = f16_to_f32(mh);
   uint8_t* qs = b + 16;
   for (int c = 0; c < 4; c++) {
-    float dd0 = d * (float)ls[2 * c], dm0 = dmin * (float)lm[2 * c];
-    float dd1 = d * (float)ls[2 * c + 1], dm1 = dmin * (float)lm[2 * c + 1];
-    for (int l = 0; l < 32; l++) {
-      int v0 = 0, v1 = 0;
-      if (dd0 != 0.0f) {
-        v0 = nearest_int((x[64 * c + l] + dm0) / dd0);
-        v0 = v0 < 0 ? 0 : (v0 > 15 ? 15 : v0);
+    int code[2][32];
+    for (int h = 0; h < 2; h++) {
+      const int j = 2 * c + h;
+      int sc, m;
+      if (j < 4) {
+        sc = s[j] & 63;
+        m = s[j + 4] & 63;
+      } else {
+        sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
       }
-      if (dd1 != 0.0f) {
-        v1 = nearest_int((x[64 * c + 32 + l] + dm1) / dd1);
-        v1 = v1 < 0 ? 0 : (v1 > 15 ? 15 : v1);
-      }
-      qs[32 * c + l] = (uint8_t)(v0 | (v1 << 4));
+      const float dd = d * (float)sc, dm = dmin * (float)m;
+      for (int l = 0; l < 32; l++)
+        code[h][l] = dd == 0.0f ? 0 : clampi(rs_nearest((x[32 * j + l] + dm) / dd), 0, 15);
     }
+    for (int l = 0; l < 32; l++) qs[32 * c + l] = (uint8_t)(code[0][l] | (code[1][l] << 4));
   }
 }
 
-// Q6_K: per 16-element sub-block, scale = (signed max-|x| element) / -32; the 16
-// scales quantised to int8 against the largest-|.| one (-128 / max); elements
-// re-fitted to [-32, 31] with the stored scales.
-HX_DEV void qz_q6_k(const float* x, uint8_t* b) {
-  float scale[16];
-  float max_scale = 0.0f, max_abs_scale = 0.0f;
-  for (int i = 0; i < 16; i++) {
-    float vmax = 0.0f, amax = 0.0f;
-    for (int l = 0; l < 16; l++) {
-      float v = x[16 * i + l], a = fabsf(v);
-      if (a > amax) {
-        amax = a;
-        vmax = v;
+// make_qx_quants(n, nmax, x, L, rmse_type = 1), weights x^2: codes from the
+// largest-|x| element, up to 3 rounds re-deriving them from the least-squares
+// scale while the weighted fit improves, up to 5 rounds of single-code moves
+// that improve it. Returns the scale; L holds code + nmax.
+HX_DEV float make_qx(int n, int nmax, const float* x, int8_t* L) {
+  float max = 0.0f, amax = 0.0f;
+  for (int i = 0; i < n; i++) {
+    const float ax = fabsf(x[i]);
+    if (ax > amax) {
+      amax = ax;
+      max = x[i];
+    }
+  }
+  if (amax == 0.0f) {
+    for (int i = 0; i < n; i++) L[i] = 0;
+    return 0.0f;
+  }
+  const float iscale = -(float)nmax / max;
+  float sumlx = 0.0f, suml2 = 0.0f;
+  for (int i = 0; i < n; i++) {
+    const int l = clampi(rs_nearest(iscale * x[i]), -nmax, nmax - 1);
+    L[i] = (int8_t)(l + nmax);
+    const float w = x[i] * x[i];
+    sumlx += w * x[i] * (float)l;
+    suml2 += w * (float)l * (float)l;
+  }
+  float scale = sumlx / suml2;
+  float best = scale * sumlx;
+  for (int t = 0; t < 3; t++) {
+    const float is = 1.0f / scale;
+    float slx = 0.0f, sl2 = 0.0f;
+    bool changed = false;
+    for (int i = 0; i < n; i++) {
+      const int l = clampi(rs_nearest(is * x[i]), -nmax, nmax - 1);
+      if (l + nmax != (int)L[i]) changed = true;
+      const float w = x[i] * x[i];
+      slx += w * x[i] * (float)l;
+      sl2 += w * (float)l * (float)l;
+    }
+    if (!changed || sl2 == 0.0f || slx * slx <= best * sl2) break;
+    for (int i = 0; i < n; i++) L[i] = (int8_t)(nmax + clampi(rs_nearest(is * x[i]), -nmax, nmax - 1));
+    sumlx = slx;
+    suml2 = sl2;
+    scale = sumlx / suml2;
+    best = scale * sumlx;
+  }
+  for (int t = 0; t < 5; t++) {
+    int n_changed = 0;
+    for (int i = 0; i < n; i++) {
+      const float w = x[i] * x[i];
+      const int l = (int)L[i] - nmax;
+      float slx = sumlx - w * x[i] * (float)l;
+      if (slx > 0.0f) {
+        float sl2 = suml2 - w * (float)l * (float)l;
+        const int new_l = clampi(rs_nearest(x[i] * sl2 / slx), -nmax, nmax - 1);
+        if (new_l != l) {
+          slx += w * x[i] * (float)new_l;
+          sl2 += w * (float)new_l * (float)new_l;
+          if (sl2 > 0.0f && slx * slx * suml2 > sumlx * sumlx * sl2) {
+            L[i] = (int8_t)(nmax + new_l);
+            sumlx = slx;
+            suml2 = sl2;
+            scale = sumlx / suml2;
+            best = scale * sumlx;
+            n_changed++;
+          }
+        }
       }
     }
-    scale[i] = vmax != 0.0f ? vmax / -32.0f : 0.0f;
-    float as = fabsf(scale[i]);
-    if (as > max_abs_scale) {
-      max_abs_scale = as;
-      max_scale = scale[i];
+    if (!n_changed) break;
+  }
+  return scale;
+}
+
+// Q6_K (BlockQ6K::from_float): make_qx_quants(16, 32, rmse 1) per 16 elements;
+// scales to int8 against -128 / (largest-|.| scale); codes re-fitted to [-32, 31]
+HX_DEV void qz_q6_k(const float* x, uint8_t* b) {
+  int8_t L[256];
+  float scales[16];
+  float max_scale = 0.0f, max_abs_scale = 0.0f;
+  for (int ib = 0; ib < 16; ib++) {
+    const float sc = make_qx(16, 32, x + 16 * ib, L + 16 * ib);
+    scales[ib] = sc;
+    if (fabsf(sc) > max_abs_scale) {
+      max_abs_scale = fabsf(sc);
+      max_scale = sc;
     }
   }
-  float iscale = max_scale != 0.0f ? -128.0f / max_scale : 0.0f;
-  int8_t sc[16];
+  const float iscale = -128.0f / max_scale;
+  const uint16_t dh = f32_to_f16(1.0f / iscale);
+  int8_t ysc[16];
   for (int i = 0; i < 16; i++) {
-    int v = nearest_int(iscale * scale[i]);
-    v = v > 127 ? 127 : (v < -128 ? -128 : v);
-    sc[i] = (int8_t)v;
+    const int v = rs_nearest(iscale * scales[i]);
+    ysc[i] = (int8_t)(uint8_t)(v < 127 ? v : 127);
   }
-  uint16_t dh = f32_to_f16(iscale != 0.0f ? 1.0f / iscale : 0.0f);
-  float d = f16_to_f32(dh);
+  const float d = f16_to_f32(dh);
+  for (int j = 0; j < 16; j++) {
+    const float dj = d * (float)ysc[j];
+    if (dj == 0.0f) continue;
+    for (int l = 0; l < 16; l++) L[16 * j + l] = (int8_t)(clampi(rs_nearest(x[16 * j + l] / dj), -32, 31) + 32);
+  }
   uint8_t* ql = b;
   uint8_t* qh = b + 128;
   for (int n = 0; n < 2; n++) {
     for (int l = 0; l < 32; l++) {
-      uint8_t q[4];
-      for (int s = 0; s < 4; s++) {
-        int e = 128 * n + 32 * s + l;
-        float di = d * (float)sc[e / 16];
-        int v = 0;
-        if (di != 0.0f) {
-          v = nearest_int(x[e] / di);
-          v = v < -32 ? -32 : (v > 31 ? 31 : v);
-        }
-        q[s] = (uint8_t)(v + 32);
-      }
-      ql[64 * n + l] = (uint8_t)((q[0] & 0xF) | ((q[2] & 0xF) << 4));
-      ql[64 * n + 32 + l] = (uint8_t)((q[1] & 0xF) | ((q[3] & 0xF) << 4));
-      qh[32 * n + l] = (uint8_t)((q[0] >> 4) | ((q[1] >> 4) << 2) | ((q[2] >> 4) << 4) | ((q[3] >> 4) << 6));
+      const uint8_t q1 = (uint8_t)L[128 * n + l], q2 = (uint8_t)L[128 * n + 32 + l];
+      const uint8_t q3 = (uint8_t)L[128 * n + 64 + l], q4 = (uint8_t)L[128 * n + 96 + l];
+      ql[64 * n + l] = (uint8_t)((q1 & 0xF) | ((q3 & 0xF) << 4));
+      ql[64 * n + 32 + l] = (uint8_t)((q2 & 0xF) | ((q4 & 0xF) << 4));
+      qh[32 * n + l] = (uint8_t)(((q1 >> 4) & 3) | (((q2 >> 4) & 3) << 2) | (((q3 >> 4) & 3) << 4) |
+                                 (((q4 >> 4) & 3) << 6));
     }
   }
-  for (int i = 0; i < 16; i++) b[192 + i] = (uint8_t)sc[i];
+  for (int i = 0; i < 16; i++) b[192 + i] = (uint8_t)ysc[i];
   st_u16(b + 208, dh);
 }
 

@@ -151,8 +151,10 @@ int hx_moe_decoder_mlp(hx_moe* m, void* x, int64_t n_tokens, const float* norm_w
 
 /* quantize_parallel (isq.rs:39-113) on the device: f32 [rows, cols] -> GGUF
  * rows of dtype (HX_Q8_0, HX_Q4_K, HX_Q6_K, HX_BF16, HX_F16). cols must tile
- * into whole blocks. The block rules are the library's own (Q8_0: d = amax/127,
- * round to nearest); byte parity with candle's quantiser is not claimed. */
+ * into whole blocks. Each block follows the rule of candle's
+ * GgmlType::from_float, which quantize_parallel calls (isq.rs:98): Q8_0
+ * d = amax/127 with rounding half away from zero; Q4_K make_qkx1_quants
+ * (5 tries) per 32 elements; Q6_K make_qx_quants (rmse_type 1) per 16. */
 int hx_quantize(int dtype, const float* src, int64_t rows, int64_t cols, void* dst, void* stream);
 
 /* GGUF rows of dtype -> f32 [rows, cols] on the device. */

@@ -18,7 +18,9 @@
  *   - MaybeQuantLinear         crates/neuron/src/harness/tp/tp_linear.rs:98-140
  *       (quantised weights: GGUF Q8_0 / Q4_K / Q6_K blocks, public ggml format)
  *   - quantize_blocks          crates/neuron/src/harness/tp/isq.rs:57-113
- *       (block layout and divisibility; the per-block search is our own)
+ *       (block layout and divisibility) with the block rules of candle's
+ *       GgmlType::from_float, which isq.rs:98 calls (Q8_0, Q4_K, Q6_K; see the
+ *       quantiser section)
  *   - Qwen3_5RmsNorm::forward  crates/neuron/src/harness/arch/qwen3_5/rmsnorm.rs:67-80
  *   - decoder residual         crates/neuron/src/harness/arch/qwen3_5/decoder.rs:129-132
  *
@@ -50,9 +52,15 @@
  *     token independence, and an f32 golden from transformers'
  *     Qwen3NextSparseMoeBlock on the C1 shape.
  *   - rmsnorm: closed forms.
+ *   - quantisers (candle's from_float rules): known-answer blocks (Q8_0
+ *     halves rounded away from zero, Q4_K positive-constant sub-blocks stored
+ *     as zero, exact Q4_K / Q6_K lattice round trips that fix d, dmin and the
+ *     packed 6-bit / int8 scales), and invariants of the make_qx_quants /
+ *     make_qkx1_quants searches (least-squares scale of the returned codes, no
+ *     worse than the starting codes, closed forms on two-valued blocks).
  * Parity unpinned (no reference vector or buildable reference exists here):
- *   - hxo_quantize's per-block scale search is the library's own rule; byte
- *     parity with candle's GgmlType::from_float is unpinned (forward parity
+ *   - hxo_quantize restates candle's from_float rules from the published
+ *     algorithms; byte parity with candle itself is unpinned (forward parity
  *     never depends on it: both sides are fed the same GGUF bytes).
  *   - candle's quantised-matmul arithmetic (QMatMul activation quantisation to
  *     Q8_K / Q8_0 at m <= 64, the f16 path at m > 64) is not restated; the
@@ -251,70 +259,130 @@ int hxo_dequant(int dtype, const void* src, int64_t n, float* dst) {
 }
 
 /* ------------------------------------------------------------------------- */
-/* quantisers (our own per-block search; block layout per isq.rs:57-113)      */
+/* quantisers: candle's GgmlType::from_float, which quantize_parallel calls   */
+/* (isq.rs:98, 104-112) and which isq.rs:1-19, 123-161 hold byte-identical to  */
+/* QTensor::quantize. candle-core 0.11's k_quants port of ggml's first         */
+/* k_quants.c reference quantisers (third-party, not vendored in the          */
+/* reference; restated from the published algorithms):                        */
+/*   Q8_0  d = amax / 127, q = round-half-away(x / d)  (BlockQ8_0::from_float) */
+/*   Q4_K  make_qkx1_quants(nmax 15, 5 tries) per 32 elements, scales / mins  */
+/*         to 6 bits against their maxima, codes re-fitted (BlockQ4K)         */
+/*   Q6_K  make_qx_quants(16, nmax 32, rmse_type 1) per 16 elements, scales   */
+/*         to int8 against -128 / (largest-|.| scale), codes re-fitted        */
+/* nearest_int is f32::round (half away from zero) followed by Rust's          */
+/* saturating float -> int cast (NaN -> 0).                                   */
 /* ------------------------------------------------------------------------- */
-static inline int nearest(float v) { return (int)rintf(v); }
+static inline int rs_nearest(float v) {
+    float r = roundf(v);
+    if (r != r) return 0;
+    if (r >= 2147483648.0f) return INT32_MAX;
+    if (r < -2147483648.0f) return INT32_MIN;
+    return (int)r;
+}
+
+static inline int clampi(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+
+/* Rust `as i8` from f32: round toward zero, saturate, NaN -> 0 (the value here
+ * is already rounded) */
+static inline int8_t rs_f32_to_i8(float v) {
+    if (v != v) return 0;
+    if (v >= 127.0f) return 127;
+    if (v <= -128.0f) return -128;
+    return (int8_t)v;
+}
 
 static void qz_q8_0(const float* x, uint8_t* b) {
     float amax = 0.0f;
-    for (int j = 0; j < 32; j++) { float a = fabsf(x[j]); if (a > amax) amax = a; }
+    for (int j = 0; j < 32; j++) amax = fmaxf(amax, fabsf(x[j]));
     float d = amax / 127.0f;
     float id = d != 0.0f ? 1.0f / d : 0.0f;
     uint16_t dh = hxo_f32_to_f16(d);
     memcpy(b, &dh, 2);
-    for (int j = 0; j < 32; j++) {
-        int q = nearest(x[j] * id);
-        if (q > 127) q = 127;
-        if (q < -127) q = -127;
-        b[2 + j] = (uint8_t)(int8_t)q;
+    for (int j = 0; j < 32; j++) b[2 + j] = (uint8_t)rs_f32_to_i8(roundf(x[j] * id));
+}
+
+/* make_qkx1_quants(nmax, ntry, x[n]) -> (scale, -min): alternate the codes
+ * l = clamp(round((x - min) / scale), 0, nmax) with the least-squares scale
+ * sum((x - min) l) / sum(l^2) and the mean residual min (clamped to <= 0),
+ * starting from min = min(0, min x), scale = (max - min) / nmax, until the
+ * codes stop changing or ntry rounds ran. The codes start at 0. */
+static void make_qkx1(const float* x, int n, int nmax, int ntry, float* scale_out, float* min_out) {
+    float mn = x[0], mx = x[0];
+    for (int i = 1; i < n; i++) {
+        if (x[i] < mn) mn = x[i];
+        if (x[i] > mx) mx = x[i];
     }
+    if (mx == mn) {
+        *scale_out = 0.0f;
+        *min_out = 0.0f;
+        return;
+    }
+    if (mn > 0.0f) mn = 0.0f;
+    float iscale = (float)nmax / (mx - mn);
+    float scale = 1.0f / iscale;
+    uint8_t L[256];
+    memset(L, 0, sizeof L);
+    for (int t = 0; t < ntry; t++) {
+        float sumlx = 0.0f;
+        int suml2 = 0, changed = 0;
+        for (int i = 0; i < n; i++) {
+            int li = clampi(rs_nearest(iscale * (x[i] - mn)), 0, nmax);
+            if ((uint8_t)li != L[i]) {
+                L[i] = (uint8_t)li;
+                changed = 1;
+            }
+            sumlx += (x[i] - mn) * (float)li;
+            suml2 += li * li;
+        }
+        scale = sumlx / (float)suml2;
+        float sum = -0.0f;
+        for (int i = 0; i < n; i++) sum += x[i] - scale * (float)L[i];
+        mn = sum / (float)n;
+        if (mn > 0.0f) mn = 0.0f;
+        iscale = 1.0f / scale;
+        if (!changed) break;
+    }
+    *scale_out = scale;
+    *min_out = -mn;
 }
 
 static void qz_q4_k(const float* x, uint8_t* b) {
-    float scale[8], mins[8];
+    float scales[8], mins[8];
+    for (int j = 0; j < 8; j++) make_qkx1(x + 32 * j, 32, 15, 5, &scales[j], &mins[j]);
     float max_scale = 0.0f, max_min = 0.0f;
     for (int j = 0; j < 8; j++) {
-        float mn = 0.0f, mx = x[32 * j];
-        for (int l = 0; l < 32; l++) {
-            float v = x[32 * j + l];
-            if (v < mn) mn = v;
-            if (v > mx) mx = v;
-        }
-        scale[j] = (mx - mn) / 15.0f;
-        mins[j] = -mn;
-        if (scale[j] > max_scale) max_scale = scale[j];
-        if (mins[j] > max_min) max_min = mins[j];
+        max_scale = fmaxf(scales[j], max_scale);
+        max_min = fmaxf(mins[j], max_min);
     }
     float inv_scale = max_scale > 0.0f ? 63.0f / max_scale : 0.0f;
     float inv_min = max_min > 0.0f ? 63.0f / max_min : 0.0f;
-    uint8_t ls[8], lm[8];
+    uint8_t* s = b + 4;
+    memset(s, 0, 12);
     for (int j = 0; j < 8; j++) {
-        int a = nearest(inv_scale * scale[j]), m = nearest(inv_min * mins[j]);
-        ls[j] = (uint8_t)(a > 63 ? 63 : a);
-        lm[j] = (uint8_t)(m > 63 ? 63 : m);
+        int a = rs_nearest(inv_scale * scales[j]), m = rs_nearest(inv_min * mins[j]);
+        uint8_t ls = (uint8_t)(a < 63 ? a : 63), lm = (uint8_t)(m < 63 ? m : 63);
+        if (j < 4) {
+            s[j] = ls;
+            s[j + 4] = lm;
+        } else {
+            s[j + 4] = (uint8_t)((ls & 0xF) | ((lm & 0xF) << 4));
+            s[j - 4] |= (uint8_t)((ls >> 4) << 6);
+            s[j] |= (uint8_t)((lm >> 4) << 6);
+        }
     }
     uint16_t dh = hxo_f32_to_f16(max_scale / 63.0f), mh = hxo_f32_to_f16(max_min / 63.0f);
     memcpy(b, &dh, 2);
     memcpy(b + 2, &mh, 2);
-    uint8_t* s = b + 4;
-    for (int j = 0; j < 4; j++) {
-        s[j] = (uint8_t)((ls[j] & 63) | ((ls[j + 4] >> 4) << 6));
-        s[j + 4] = (uint8_t)((lm[j] & 63) | ((lm[j + 4] >> 4) << 6));
-        s[j + 8] = (uint8_t)((ls[j + 4] & 0xF) | ((lm[j + 4] & 0xF) << 4));
-    }
     float d = hxo_f16_to_f32(dh), dmin = hxo_f16_to_f32(mh);
     uint8_t q[256];
+    memset(q, 0, sizeof q);
     for (int j = 0; j < 8; j++) {
-        float dd = d * (float)ls[j], dm = dmin * (float)lm[j];
-        for (int l = 0; l < 32; l++) {
-            int v = 0;
-            if (dd != 0.0f) {
-                v = nearest((x[32 * j + l] + dm) / dd);
-                if (v < 0) v = 0;
-                if (v > 15) v = 15;
-            }
-            q[32 * j + l] = (uint8_t)v;
-        }
+        int sc, m;
+        q4k_scale_min(j, s, &sc, &m);
+        float dd = d * (float)sc;
+        if (dd == 0.0f) continue;
+        float dm = dmin * (float)m;
+        for (int l = 0; l < 32; l++) q[32 * j + l] = (uint8_t)clampi(rs_nearest((x[32 * j + l] + dm) / dd), 0, 15);
     }
     uint8_t* qs = b + 16;
     for (int c = 0; c < 4; c++)
@@ -322,55 +390,128 @@ static void qz_q4_k(const float* x, uint8_t* b) {
             qs[32 * c + l] = (uint8_t)(q[64 * c + l] | (q[64 * c + 32 + l] << 4));
 }
 
-static void qz_q6_k(const float* x, uint8_t* b) {
-    float scale[16];
-    float max_scale = 0.0f, max_abs_scale = 0.0f;
-    for (int i = 0; i < 16; i++) {
-        float vmax = 0.0f, amax = 0.0f;
-        for (int l = 0; l < 16; l++) {
-            float v = x[16 * i + l], a = fabsf(v);
-            if (a > amax) { amax = a; vmax = v; }
+/* make_qx_quants(n, nmax, x, L, rmse_type) for rmse_type 1 (weights x^2):
+ * codes l in [-nmax, nmax - 1] from the largest-|x| element's scale, then up to
+ * 3 rounds re-deriving the codes from the least-squares scale while the
+ * weighted fit improves, then up to 5 rounds of single-code moves that
+ * improve it. Returns the scale; L holds l + nmax. */
+static float make_qx(int n, int nmax, const float* x, int8_t* L) {
+    float max = 0.0f, amax = 0.0f;
+    for (int i = 0; i < n; i++) {
+        float ax = fabsf(x[i]);
+        if (ax > amax) {
+            amax = ax;
+            max = x[i];
         }
-        scale[i] = vmax != 0.0f ? vmax / -32.0f : 0.0f;
-        float as = fabsf(scale[i]);
-        if (as > max_abs_scale) { max_abs_scale = as; max_scale = scale[i]; }
     }
-    float iscale = max_scale != 0.0f ? -128.0f / max_scale : 0.0f;
-    int8_t sc[16];
-    for (int i = 0; i < 16; i++) {
-        int v = nearest(iscale * scale[i]);
-        if (v > 127) v = 127;
-        if (v < -128) v = -128;
-        sc[i] = (int8_t)v;
+    if (amax == 0.0f) {
+        for (int i = 0; i < n; i++) L[i] = 0;
+        return 0.0f;
     }
-    uint16_t dh = hxo_f32_to_f16(iscale != 0.0f ? 1.0f / iscale : 0.0f);
-    float d = hxo_f16_to_f32(dh);
-    uint8_t L[256];
-    for (int i = 0; i < 16; i++) {
-        float di = d * (float)sc[i];
-        for (int l = 0; l < 16; l++) {
-            int v = 0;
-            if (di != 0.0f) {
-                v = nearest(x[16 * i + l] / di);
-                if (v < -32) v = -32;
-                if (v > 31) v = 31;
+    float iscale = -(float)nmax / max;
+    float sumlx = 0.0f, suml2 = 0.0f;
+    for (int i = 0; i < n; i++) {
+        int l = clampi(rs_nearest(iscale * x[i]), -nmax, nmax - 1);
+        L[i] = (int8_t)(l + nmax);
+        float w = x[i] * x[i];
+        sumlx += w * x[i] * (float)l;
+        suml2 += w * (float)l * (float)l;
+    }
+    float scale = sumlx / suml2;
+    float best = scale * sumlx;
+    for (int t = 0; t < 3; t++) {
+        float is = 1.0f / scale;
+        float slx = 0.0f, sl2 = 0.0f;
+        int changed = 0;
+        for (int i = 0; i < n; i++) {
+            int l = clampi(rs_nearest(is * x[i]), -nmax, nmax - 1);
+            if (l + nmax != (int)L[i]) changed = 1;
+            float w = x[i] * x[i];
+            slx += w * x[i] * (float)l;
+            sl2 += w * (float)l * (float)l;
+        }
+        if (!changed || sl2 == 0.0f || slx * slx <= best * sl2) break;
+        for (int i = 0; i < n; i++) L[i] = (int8_t)(nmax + clampi(rs_nearest(is * x[i]), -nmax, nmax - 1));
+        sumlx = slx;
+        suml2 = sl2;
+        scale = sumlx / suml2;
+        best = scale * sumlx;
+    }
+    for (int t = 0; t < 5; t++) {
+        int n_changed = 0;
+        for (int i = 0; i < n; i++) {
+            float w = x[i] * x[i];
+            int l = (int)L[i] - nmax;
+            float slx = sumlx - w * x[i] * (float)l;
+            if (slx > 0.0f) {
+                float sl2 = suml2 - w * (float)l * (float)l;
+                int new_l = clampi(rs_nearest(x[i] * sl2 / slx), -nmax, nmax - 1);
+                if (new_l != l) {
+                    slx += w * x[i] * (float)new_l;
+                    sl2 += w * (float)new_l * (float)new_l;
+                    if (sl2 > 0.0f && slx * slx * suml2 > sumlx * sumlx * sl2) {
+                        L[i] = (int8_t)(nmax + new_l);
+                        sumlx = slx;
+                        suml2 = sl2;
+                        scale = sumlx / suml2;
+                        best = scale * sumlx;
+                        n_changed++;
+                    }
+                }
             }
-            L[16 * i + l] = (uint8_t)(v + 32);
         }
+        if (!n_changed) break;
+    }
+    return scale;
+}
+
+static void qz_q6_k(const float* x, uint8_t* b) {
+    int8_t L[256];
+    float scales[16];
+    float max_scale = 0.0f, max_abs_scale = 0.0f;
+    for (int ib = 0; ib < 16; ib++) {
+        float sc = make_qx(16, 32, x + 16 * ib, L + 16 * ib);
+        scales[ib] = sc;
+        float as = fabsf(sc);
+        if (as > max_abs_scale) {
+            max_abs_scale = as;
+            max_scale = sc;
+        }
+    }
+    float iscale = -128.0f / max_scale;
+    uint16_t dh = hxo_f32_to_f16(1.0f / iscale);
+    int8_t* ysc = (int8_t*)(b + 192);
+    for (int i = 0; i < 16; i++) {
+        int v = rs_nearest(iscale * scales[i]);
+        ysc[i] = (int8_t)(uint8_t)(v < 127 ? v : 127);
+    }
+    float d = hxo_f16_to_f32(dh);
+    for (int j = 0; j < 16; j++) {
+        float dj = d * (float)ysc[j];
+        if (dj == 0.0f) continue;
+        for (int l = 0; l < 16; l++) L[16 * j + l] = (int8_t)(clampi(rs_nearest(x[16 * j + l] / dj), -32, 31) + 32);
     }
     uint8_t* ql = b;
     uint8_t* qh = b + 128;
     for (int n = 0; n < 2; n++) {
         for (int l = 0; l < 32; l++) {
-            uint8_t q1 = L[128 * n + l], q2 = L[128 * n + 32 + l];
-            uint8_t q3 = L[128 * n + 64 + l], q4 = L[128 * n + 96 + l];
+            uint8_t q1 = (uint8_t)L[128 * n + l], q2 = (uint8_t)L[128 * n + 32 + l];
+            uint8_t q3 = (uint8_t)L[128 * n + 64 + l], q4 = (uint8_t)L[128 * n + 96 + l];
             ql[64 * n + l] = (uint8_t)((q1 & 0xF) | ((q3 & 0xF) << 4));
             ql[64 * n + 32 + l] = (uint8_t)((q2 & 0xF) | ((q4 & 0xF) << 4));
-            qh[32 * n + l] = (uint8_t)((q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6));
+            qh[32 * n + l] = (uint8_t)(((q1 >> 4) & 3) | (((q2 >> 4) & 3) << 2) | (((q3 >> 4) & 3) << 4) |
+                                       (((q4 >> 4) & 3) << 6));
         }
     }
-    memcpy(b + 192, sc, 16);
     memcpy(b + 208, &dh, 2);
+}
+
+/* the per-sub-block searches on their own (test hooks) */
+float hxo_make_qx(int n, int nmax, const float* x, int8_t* L) {
+    return n > 0 && n <= 256 ? make_qx(n, nmax, x, L) : 0.0f;
+}
+void hxo_make_qkx1(int n, int nmax, int ntry, const float* x, float* scale, float* min) {
+    if (n > 0 && n <= 256) make_qkx1(x, n, nmax, ntry, scale, min);
 }
 
 /* quantise a [rows, cols] f32 matrix into GGUF rows; cols must tile into blocks

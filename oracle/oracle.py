@@ -59,6 +59,10 @@ def lib() -> C.CDLL:
         L.hxo_dispatch.argtypes = [vp, i64, i32, i64, vp, vp, vp]
         L.hxo_moe_forward.restype = i32
         L.hxo_moe_forward.argtypes = [vp, vp, i64, vp, vp, i32]
+        L.hxo_make_qx.restype = C.c_float
+        L.hxo_make_qx.argtypes = [i32, i32, vp, vp]
+        L.hxo_make_qkx1.restype = None
+        L.hxo_make_qkx1.argtypes = [i32, i32, i32, vp, C.POINTER(C.c_float), C.POINTER(C.c_float)]
         L.hxo_rmsnorm.restype = i32
         L.hxo_rmsnorm.argtypes = [i32, vp, i64, i64, vp, C.c_float, vp]
         _lib = L
@@ -114,6 +118,22 @@ def dequantize(dtype: int, q: np.ndarray, cols: int) -> np.ndarray:
     if rc:
         raise ValueError(f"hxo_dequant rc={rc}")
     return out
+
+
+def make_qx(x: np.ndarray, nmax: int):
+    """candle's make_qx_quants(n, nmax, x, L, 1) -> (scale, L - nmax as int32)"""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    L = np.empty(x.size, np.int8)
+    sc = lib().hxo_make_qx(x.size, nmax, _p(x), _p(L))
+    return float(np.float32(sc)), L.astype(np.int32) - nmax
+
+
+def make_qkx1(x: np.ndarray, nmax: int, ntry: int):
+    """candle's make_qkx1_quants(nmax, ntry, x) -> (scale, -min)"""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    sc, mn = C.c_float(), C.c_float()
+    lib().hxo_make_qkx1(x.size, nmax, ntry, _p(x), C.byref(sc), C.byref(mn))
+    return sc.value, mn.value
 
 
 # ---------------------------------------------------------------- block

@@ -76,6 +76,13 @@ def test_device_quantiser_matches_oracle_bytes(dt):
     w = torch.randn((96, 2048), generator=g, device="cuda") * 0.02
     w[3, :256] = 0.0                                  # all-zero blocks
     w[4, :32] = 1e-3                                  # constant block
+    w[5, :256] = 0.3                                  # positive-constant superblock
+    w[6, 32:64] = -0.01                               # negative-constant sub-block
+    w[7, :32] = torch.tensor([127.0, 0.5, 4.5, -2.5, -0.5] + [0.0] * 27)   # Q8_0 halves
+    lat = torch.arange(256, device="cuda", dtype=torch.float32)
+    w[8, :256] = ((lat % 16) * 63.0 * 4.0 - 21.0) / 4096.0                 # Q4_K lattice
+    w[9, :256] = ((lat % 64) - 32.0) * 77.0 / 4096.0                       # Q6_K lattice
+    w[10, :] = torch.randn((2048,), generator=g, device="cuda") * 3.0      # large magnitudes
     q = hx.quantize(dt, w).cpu().numpy()
     ref = O.quantize(dt, w.cpu().numpy())
     assert np.array_equal(q.reshape(-1), ref.reshape(-1))

@@ -165,6 +165,100 @@ def test_quantizer_is_exact_on_representable_q8_0():
     assert np.array_equal(O.dequantize(O.Q8_0, blk, 32), w)
 
 
+# ------------------------------------------- quantiser rules (candle's from_float)
+def test_q8_0_rounds_half_away_from_zero():
+    """BlockQ8_0::from_float rounds x / d with f32::round: with amax 127 (d = 1)
+    the halves go away from zero (round-half-even would give 0, 4, -2, -0)"""
+    x = np.zeros((1, 32), np.float32)
+    x[0, :5] = [127.0, 0.5, 4.5, -2.5, -0.5]
+    blk = O.quantize(O.Q8_0, x)[0]
+    assert blk[:2].view(np.uint16)[0] == 0x3C00            # f16 1.0
+    assert list(blk[2:7].view(np.int8)) == [127, 1, 5, -3, -1]
+
+
+def test_q4_k_constant_subblock_quantises_to_zero():
+    """make_qkx1_quants returns (scale 0, min 0) when a sub-block's max equals its
+    min -- before min is clamped to <= 0 -- so a sub-block holding one positive
+    constant dequantises to 0, and a whole block of it stores nothing but zeros"""
+    assert not O.quantize(O.Q4_K, np.full((1, 256), 0.3, np.float32)).any()
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((1, 256)) * 0.02).astype(np.float32)
+    x[0, 64:96] = 0.01
+    d = O.dequantize(O.Q4_K, O.quantize(O.Q4_K, x), 256)[0]
+    assert not d[64:96].any() and np.abs(d[:64] - x[0, :64]).max() < 0.01
+
+
+def test_q4_k_lattice_round_trip_is_exact():
+    """sub-block j holding s_j l - m_j (l = 0..15, both ends present) with
+    s_j = sc_j 2^-10, m_j = mm_j 2^-12 and the largest sc, mm equal to 63: the
+    search converges to (s_j, m_j), d = 2^-10, dmin = 2^-12 and the 6-bit
+    scales/mins are sc_j, mm_j (ones above 15 use the high-bit packing of
+    sub-blocks 4-7), so dequantisation gives x back exactly"""
+    sc = [63, 17, 40, 5, 33, 63, 18, 50]
+    mm = [0, 63, 21, 7, 48, 16, 63, 31]
+    rng = np.random.default_rng(8)
+    x = np.empty(256, np.float32)
+    for j in range(8):
+        l = rng.integers(0, 16, 32)
+        l[0], l[1] = 0, 15
+        x[32 * j:32 * j + 32] = (sc[j] * l * 4.0 - mm[j]) / 4096.0
+    blk = O.quantize(O.Q4_K, x.reshape(1, 256))[0]
+    assert blk[:4].view(np.uint16).tolist() == [0x1400, 0x0C00]     # 2^-10, 2^-12
+    assert np.array_equal(O.dequantize(O.Q4_K, blk, 256), x)
+
+
+def test_q6_k_lattice_round_trip_is_exact():
+    """sub-block i holding n_i 2^-12 l (l in [-32, 31], -32 present so it is the
+    largest-|x| element): make_qx_quants keeps the lattice codes, the largest
+    scale (n = 128) sets iscale = -4096, d = -2^-12 and the int8 scales -n_i"""
+    n = [128, 1, 77, 3, 100, 64, 9, 128, 31, 2, 127, 50, 12, 90, 45, 7]
+    rng = np.random.default_rng(9)
+    x = np.empty(256, np.float32)
+    for i in range(16):
+        l = rng.integers(-32, 32, 16)
+        l[0] = -32
+        x[16 * i:16 * i + 16] = n[i] * l / 4096.0
+    blk = O.quantize(O.Q6_K, x.reshape(1, 256))[0]
+    assert blk[208:210].view(np.uint16)[0] == 0x8C00                # -2^-12
+    assert list(blk[192:208].view(np.int8)) == [-v for v in n]
+    assert np.array_equal(O.dequantize(O.Q6_K, blk, 256), x)
+
+
+def test_make_qx_quants_improves_on_its_start_and_returns_the_fit_scale():
+    """on random sub-blocks: the returned scale is the x^2-weighted least-squares
+    scale of the returned codes, the codes lie in [-32, 31], and the weighted
+    error is no larger than that of the starting codes (round(-32 x / max))
+    with their own least-squares scale"""
+    rng = np.random.default_rng(11)
+    for _ in range(200):
+        x = (rng.standard_normal(16) * 0.02).astype(np.float32)
+        scale, l = O.make_qx(x, 32)
+        assert l.min() >= -32 and l.max() <= 31
+        w = x.astype(np.float64) ** 2
+        ls = (w * x * l).sum() / (w * l * l).sum()
+        assert abs(scale - ls) <= 1e-5 * abs(ls)
+        mx = x[np.argmax(np.abs(x))]
+        l0 = np.clip(np.floor(-32.0 / mx * x.astype(np.float64) + 0.5), -32, 31)
+        s0 = (w * x * l0).sum() / (w * l0 * l0).sum()
+        assert (w * (x - scale * l) ** 2).sum() <= (w * (x - s0 * l0) ** 2).sum() * (1 + 1e-6)
+
+
+def test_make_qkx1_quants_closed_forms():
+    """two-valued sub-blocks: {a, b} with a < 0 < b converges to scale (b - a) / 15
+    and min -a (codes 0 and 15 fit exactly); an all-positive sub-block keeps min 0
+    and its scale is the least-squares fit of codes against x; equal values give
+    (0, 0)"""
+    x = np.array([-0.3, 0.6] * 16, np.float32)
+    s, m = O.make_qkx1(x, 15, 5)
+    assert abs(s - 0.06) < 1e-6 and abs(m - 0.3) < 1e-6
+    x = np.linspace(0.1, 0.7, 32).astype(np.float32)
+    s, m = O.make_qkx1(x, 15, 5)
+    assert m == 0.0
+    l = np.clip(np.floor(x / s + 0.5), 0, 15)
+    assert abs(s - (x * l).sum() / (l * l).sum()) < 1e-6
+    assert O.make_qkx1(np.full(32, -0.2, np.float32), 15, 5) == (0.0, 0.0)
+
+
 # ------------------------------------------------------------------ router
 def tiny(seed=0, H=64, E=8, k=2, I=16, Is=16, norm=True, act=O.F32, fmt=None):
     w = make_f32_block(seed, H, E, I, Is, std=0.5)
