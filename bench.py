@@ -24,8 +24,11 @@ Method
     of K up to 256, replayed K / G times).
   * Algorithmic bytes per step are computed from the actual routing (unique
     experts touched) and the GGUF sizes of what must be read once.
-  * cpu_baseline: the CPU restatement of the reference's candle path (oracle/)
-    on the host cores, on a bounded sample of the same workload.
+  * cpu_baseline: the reference's CPU arithmetic for GGUF experts, restated in
+    oracle/ (candle's activation quantisation and integer vec_dot at m <= 64
+    rows, its f16 path above), on the host cores with the same weights and
+    tokens: C2 per layer here; C3, the 512-token chunk and C5 full forwards in
+    their lines, C4 B = 1 (one layer x 48) in the C3 line.
   * `prefill` (secondary): C3, 2048 tokens of the same layer in Q4_K_M (gate/up
     Q4_K, down Q6_K), tokens/s with its MFMA and HBM fractions, and a roofline
     object for the gate/up MFMA kernel (event-timed; traced average, HBM traffic
@@ -225,25 +228,39 @@ def bench_decode(args):
     return out, blocks, host0, xs
 
 
-def cpu_baseline(cfg, fmts, host0, x0, budget_s):
+def cpu_candle(cfg, wnp, x, runs, bias=None):
+    """the oracle's candle-arithmetic forward (the reference's CPU path for GGUF
+    experts: Q8_0 / Q8_K activation quantisation and candle's integer vec_dot at
+    m <= 64 rows, its f16 path above) on the host cores: median of `runs` after
+    one warm-up; -> (seconds, threads)"""
     import numpy as np
     import torch
     from oracle import oracle as O
     orc = O.OracleMoe(cfg.hidden_size, cfg.num_experts, cfg.num_experts_per_tok, cfg.moe_intermediate_size,
-                      cfg.shared_expert_intermediate_size, cfg.norm_topk_prob, O.BF16, host0)
-    xn = x0.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+                      cfg.shared_expert_intermediate_size, cfg.norm_topk_prob, O.BF16, wnp)
+    xn = x.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+    bn = None if bias is None else bias.detach().cpu().numpy()
     threads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
-    orc.forward(xn, nthreads=threads)                     # warm-up
-    n, t0 = 0, time.perf_counter()
-    while True:
-        orc.forward(xn, nthreads=threads)
-        n += 1
-        if time.perf_counter() - t0 > budget_s or n >= 20000:
-            break
-    dt = (time.perf_counter() - t0) / n
-    return {"value": round(dt * 1e6, 1), "unit": "us/layer (C2 decode)", "cores": threads, "kind": "port",
-            "sample": f"{n} single-token decodes of layer 0 (same weights and token as the GPU run), "
-                      f"oracle/hx_oracle.c scatter loop, {threads} OpenMP threads"}
+    orc.forward_candle(xn, bias=bn, nthreads=threads)
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        orc.forward_candle(xn, bias=bn, nthreads=threads)
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), threads
+
+
+ARITH = ("candle CPU arithmetic restated (oracle/hx_oracle.c hxo_moe_forward_candle): per expert call of m rows, "
+         "m <= 64: activations quantised to Q8_0 / Q8_K and candle's generic integer vec_dot; m > 64: f16 "
+         "weights and activations, f32 accumulation, f16 output; f32 SwiGLU and combine")
+
+
+def cpu_baseline_c2(cfg, host0, x0, runs=50):
+    s, th = cpu_candle(cfg, host0, x0, runs)
+    return {"value": round(s * 1e6, 1), "unit": "us/layer (C2 decode)", "cores": th, "kind": "port",
+            "arithmetic": ARITH,
+            "sample": f"one single-token decode of layer 0 (the GPU run's weights and first token), median of "
+                      f"{runs} runs after a warm-up, {th} OpenMP threads"}
 
 
 PREFILL_KERNELS = {"gate_up": "k_gate_up_q4k", "down": "k_down_q6k", "router": "k_router88"}
@@ -269,7 +286,7 @@ def prefill_work(cfg, fmts, T, U):
 
 
 def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=5, bias=None, pmc_file=None, mfma_file=None,
-                trace_file=None):
+                trace_file=None, cpu_runs=0, c4_layer=False):
     """One prefill line: wall-clock time of `reps` forwards, then the same forwards
     again with every kernel timed by its own dispatch's HIP events, queued behind
     a sleep kernel; roofline of the gate/up MFMA kernel (the largest)."""
@@ -279,6 +296,7 @@ def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=5, bias=None, pmc_f
     from helexa_amd.profsum import read_pmc, read_stats_avg, read_mfma
     w = synth.make_weights(cfg, fmts, w_seed)
     blk = hx.Qwen3_5MoeBlock.load(cfg, w, act_dtype=hx.BF16)
+    wnp = synth.to_numpy(w) if cpu_runs else None
     del w
     x = synth.make_x(cfg, T, x_seed)
     ws = torch.empty(blk.workspace_size(T), dtype=torch.uint8, device="cuda")
@@ -325,14 +343,30 @@ def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=5, bias=None, pmc_f
               "mfma_frac": round(kflops[k] / (v * 1e-6) / (MFMA_BF16_PEAK_TFS * 1e12), 4) if k in kflops else None,
               "hbm_frac": round(kbytes[k] / (v * 1e-6) / (HBM_PEAK_GBS * 1e9), 4) if k in kbytes else None}
           for k, v in kern.items()}
-    return {"workload": workload, "tokens": T, "us": round(dt * 1e6, 1), "tok_per_s": round(T / dt, 1),
-            "mfma_frac": round(total_flops / dt / (MFMA_BF16_PEAK_TFS * 1e12), 4),
-            "hbm_frac": round(total_bytes / dt / (HBM_PEAK_GBS * 1e9), 4),
-            "algorithmic_flops": total_flops, "algorithmic_bytes": total_bytes, "unique_experts": U,
-            "max_expert_rows": int(counts.max()), "roofline": roof, "kernels": kr}
+    out = {"workload": workload, "tokens": T, "us": round(dt * 1e6, 1), "tok_per_s": round(T / dt, 1),
+           "mfma_frac": round(total_flops / dt / (MFMA_BF16_PEAK_TFS * 1e12), 4),
+           "hbm_frac": round(total_bytes / dt / (HBM_PEAK_GBS * 1e9), 4),
+           "algorithmic_flops": total_flops, "algorithmic_bytes": total_bytes, "unique_experts": U,
+           "max_expert_rows": int(counts.max()), "roofline": roof, "kernels": kr}
+    if cpu_runs:
+        log(f"[bench] cpu baseline, {T} tokens")
+        sec, th = cpu_candle(cfg, wnp, x, cpu_runs, bias)
+        out["cpu_baseline"] = {"value": round(T / sec, 1), "unit": "tok/s", "us": round(sec * 1e6, 1),
+                               "cores": th, "kind": "port", "arithmetic": ARITH,
+                               "sample": f"the same {T} tokens and weights, full forward, median of {cpu_runs} "
+                                         f"runs after a warm-up, {th} OpenMP threads"}
+        if c4_layer:
+            # C4 at B = 1: one Q4_K_M layer's single-token forward (RMSNorm and
+            # residual add are O(H)), times the 48 layers of the stack
+            sec1, th = cpu_candle(cfg, wnp, x[:1], 20)
+            out["cpu_baseline_c4_b1"] = {"value": round(sec1 * 48 * 1e6, 1), "unit": "us/token (C4 B=1, 48 layers)",
+                                         "cores": th, "kind": "port", "arithmetic": ARITH,
+                                         "sample": "one single-token layer forward of this Q4_K_M layer, median "
+                                                   "of 20 runs after a warm-up, times 48 layers"}
+    return out
 
 
-def bench_prefill(T=2048, reps=5):
+def bench_prefill(T=2048, reps=5, cpu_runs=0):
     """C3 (T = 2048) and the production chunk (T = 512): Q4_K_M prefill, seeded
     near-uniform routing"""
     from helexa_amd import synth
@@ -341,7 +375,8 @@ def bench_prefill(T=2048, reps=5):
                        f"{tag}: {T}-token prefill, Q4_K_M (gate/up Q4_K, down Q6_K), bf16", reps,
                        pmc_file="c3_prefill_pmc.txt" if T == 2048 else None,
                        mfma_file="c3_prefill_mfma.txt" if T == 2048 else None,
-                       trace_file="c3_prefill_kernels.txt" if T == 2048 else None)
+                       trace_file="c3_prefill_kernels.txt" if T == 2048 else None,
+                       cpu_runs=cpu_runs, c4_layer=cpu_runs > 0 and T == 2048)
 
 
 def bench_c4(n_layers=48, batches=(1, 4, 8), reps=20):
@@ -417,7 +452,7 @@ def b_rms(x, w, eps=1e-6):
     return y.to(x.dtype)
 
 
-def bench_c5(T=4096, target_share=0.40, reps=5):
+def bench_c5(T=4096, target_share=0.40, reps=5, cpu_runs=0):
     """C5: 4096-token prefill of the Q4_K_M layer with a seeded Zipf(1.1) router
     bias (router_bias[e] = alpha ln p_{pi(e)}), alpha calibrated on this layer so
     the top 8 experts take about 40% of the assignments."""
@@ -449,7 +484,8 @@ def bench_c5(T=4096, target_share=0.40, reps=5):
     blk.close()
     del blk
     out = prefill_run(cfg, fmts, 4243, 78, T, f"C5: {T}-token prefill, Q4_K_M, Zipf(1.1) router bias", reps,
-                      bias=base * alpha, mfma_file="c5_prefill_mfma.txt", trace_file="c5_prefill_kernels.txt")
+                      bias=base * alpha, mfma_file="c5_prefill_mfma.txt", trace_file="c5_prefill_kernels.txt",
+                      cpu_runs=cpu_runs)
     out.update({"alpha": round(alpha, 4), "top8_share": round(achieved, 4)})
     return out
 
@@ -484,7 +520,6 @@ def main():
     ap.add_argument("--steps", type=int, default=4096)
     ap.add_argument("--warmup", type=int, default=512)
     ap.add_argument("--layers", type=int, default=16)
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--probe", action="store_true", help="short workload for rocprofv3 --pmc runs")
@@ -513,9 +548,10 @@ def main():
         return
     out, blocks, host0, xs = bench_decode(args)
     log(f"[bench] decode {out['value']} us/layer; kernels {out['layer']['kernel_us']}")
+    cpu_runs = 0 if args.no_cpu else 5
     if not args.no_cpu:
         log("[bench] cpu baseline")
-        out["cpu_baseline"] = cpu_baseline(synth.A3B, synth.FMT_Q8_0, host0, xs[0], args.cpu_seconds)
+        out["cpu_baseline"] = cpu_baseline_c2(synth.A3B, host0, xs[0])
     else:
         out["cpu_baseline"] = None
     for b in blocks:
@@ -524,14 +560,14 @@ def main():
     torch.cuda.empty_cache()
     if not args.no_prefill:
         log("[bench] prefill")
-        out["prefill"] = bench_prefill()
+        out["prefill"] = bench_prefill(cpu_runs=cpu_runs)
         torch.cuda.empty_cache()
         log("[bench] prefill, production chunk of 512 tokens")
-        out["prefill_512"] = bench_prefill(512)
+        out["prefill_512"] = bench_prefill(512, cpu_runs=cpu_runs)
         torch.cuda.empty_cache()
     if not args.no_c5:
         log("[bench] C5 skewed prefill")
-        out["c5_skew"] = bench_c5()
+        out["c5_skew"] = bench_c5(cpu_runs=cpu_runs)
         torch.cuda.empty_cache()
     if not args.no_c4:
         log("[bench] C4 stack")

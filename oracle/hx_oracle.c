@@ -67,6 +67,7 @@
  *     forward here accumulates dequantised weights in double, and agreement
  *     with candle is only to the tolerance the tests state.
  */
+#include <immintrin.h>
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -587,10 +588,57 @@ typedef struct hxo_moe {
 
 /* logits [T, E] exactly as the router kernel produces them (rounded to the
  * activation dtype, then + bias if given) */
+/* the same chains with the operands laid out lane-major, p[(g * 8 + i) * 64 + l]
+ * = v[8 (64 g + l) + i] for H a multiple of 512: lane l's fmaf chain runs over
+ * its groups g and their elements i in the canonical order, 64 lanes side by
+ * side (one vector instruction per 8 lanes) */
+static void lane_major(int dtype, const void* v, int64_t H, float* p) {
+    for (int64_t g = 0; g < H / 512; g++)
+        for (int i = 0; i < 8; i++)
+            for (int l = 0; l < 64; l++) p[(g * 8 + i) * 64 + l] = ld_act(dtype, v, 8 * (64 * g + l) + i);
+}
+
+static float router_dot_lm(const float* xp, const float* wp, int64_t H) {
+    float acc[64];
+    for (int l = 0; l < 64; l++) acc[l] = 0.0f;
+    for (int64_t gi = 0; gi < H / 64; gi++)
+        for (int l = 0; l < 64; l++) acc[l] = fmaf(xp[gi * 64 + l], wp[gi * 64 + l], acc[l]);
+    return butterfly64(acc);
+}
+
 int hxo_router_logits(const hxo_moe* m, const void* x, int64_t T, const float* bias, float* logits) {
     int64_t H = m->hidden, E = m->num_experts;
     int64_t wrow = H * (m->router_dtype == HXO_BF16 ? 2 : 4);
     int64_t xrow = H * (m->act_dtype == HXO_BF16 ? 2 : 4);
+    if (H % 512 == 0) {
+        float* wp = (float*)malloc(sizeof(float) * (size_t)(E * H));
+        if (!wp) return 2;
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static)
+#endif
+        for (int64_t e = 0; e < E; e++) lane_major(m->router_dtype, (const uint8_t*)m->router + e * wrow, H, wp + e * H);
+#ifdef _OPENMP
+#pragma omp parallel
+#endif
+        {
+            float* xp = (float*)malloc(sizeof(float) * (size_t)H);
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+            for (int64_t t = 0; t < T; t++) {
+                lane_major(m->act_dtype, (const uint8_t*)x + t * xrow, H, xp);
+                for (int64_t e = 0; e < E; e++) {
+                    float v = router_dot_lm(xp, wp + e * H, H);
+                    if (m->act_dtype == HXO_BF16) v = hxo_bf16_to_f32(hxo_f32_to_bf16(v));
+                    if (bias) v = v + bias[e];
+                    logits[t * E + e] = v;
+                }
+            }
+            free(xp);
+        }
+        free(wp);
+        return 0;
+    }
 #ifdef _OPENMP
 #pragma omp parallel for schedule(static)
 #endif
@@ -828,4 +876,419 @@ int hxo_rmsnorm(int act_dtype, const void* x, int64_t T, int64_t H, const float*
         for (int64_t i = 0; i < H; i++) y[t * H + i] = ld_act(act_dtype, x, t * H + i) * inv * (1.0f + w[i]);
     }
     return 0;
+}
+
+/* ------------------------------------------------------------------------- */
+/* candle's quantised-matmul arithmetic: the second forward mode             */
+/* ------------------------------------------------------------------------- */
+/* hxo_moe_forward_candle restates the reference's CPU path for quantised
+ * experts (the Scatter store, tp_qwen3_5.rs:1105-1138, each expert a TpExpert
+ * at world size 1, tp_qwen3_5.rs:840-850, whose projections are
+ * MaybeQuantLinear, tp_linear.rs:98-140) with candle's CPU arithmetic
+ * (candle-core 0.11, third-party, not vendored; restated from the published
+ * algorithms):
+ *   - m = rows of the call (the tokens routed to the expert; T for the shared
+ *     expert). m <= 64: x is quantised per row to the weight type's vec_dot
+ *     type (Q8_0 for Q8_0 weights, Q8_K for Q4_K / Q6_K) and every output is
+ *     candle's generic vec_dot (vec_dot_unopt: what x86-64 runs without
+ *     target-cpu flags, which the reference's build does not set): integer
+ *     block dot products, then the per-block float steps in candle's order.
+ *   - m > 64 (forward_via_f16): weights dequantised and rounded to f16, x
+ *     rounded to f16, f32 accumulation (an fmaf chain over k), the output
+ *     rounded to f16 and cast back.
+ *   - f32 / bf16 weights: an f32 fmaf chain over k.
+ *   - SwiGLU silu(g) * u with silu(v) = v / (1 + exp(-v)), f32 (mlp.rs:54-60);
+ *     ys[t] += out * w per expert ascending (index_add, moe.rs:178-189); then
+ *     ys + shared * sigmoid(x . w_sg) (moe.rs:191-195).
+ * Routing (ids, weights) is the canonical routing of hxo_route, so both modes
+ * and the GPU combine the same experts with the same weights.
+ * Parity unpinned against candle itself: its CPU build is not available here.
+ * Pinned by tests/test_oracle.py: the Q8_K quantiser's invariants, the vec_dot
+ * integer identities (each equals the f64 dot of the dequantised operands up
+ * to float rounding), and agreement with the exact mode within tolerance. */
+
+/* Q8_K block (the k-quants vec_dot type): f32 d, 256 int8, 16 sums of 16 */
+typedef struct {
+    float d;
+    int8_t qs[256];
+    int16_t bsums[16];
+} q8k_t;
+
+/* BlockQ8K::from_float: iscale = -128 / (signed largest-|x| value),
+ * q = min(round(iscale x), 127), d = 1 / iscale; an all-zero block is zero */
+static void quant_q8_k(const float* x, q8k_t* y) {
+    float max = 0.0f, amax = 0.0f;
+    for (int j = 0; j < 256; j++) {
+        float ax = fabsf(x[j]);
+        if (amax < ax) {
+            amax = ax;
+            max = x[j];
+        }
+    }
+    memset(y, 0, sizeof *y);
+    if (amax == 0.0f) return;
+    float iscale = -128.0f / max;
+    for (int j = 0; j < 256; j++) {
+        float v = roundf(iscale * x[j]);
+        y->qs[j] = rs_f32_to_i8(v < 127.0f ? v : 127.0f);
+    }
+    for (int j = 0; j < 16; j++) {
+        int s = 0;
+        for (int i = 0; i < 16; i++) s += y->qs[16 * j + i];
+        y->bsums[j] = (int16_t)s;
+    }
+    y->d = 1.0f / iscale;
+}
+
+/* test hook: one row of Q8_K blocks, as (d, qs, bsums) arrays */
+int hxo_quant_q8_k(const float* x, int64_t n, float* d, int8_t* qs, int16_t* bsums) {
+    if (n <= 0 || n % 256) return 1;
+    for (int64_t b = 0; b < n / 256; b++) {
+        q8k_t y;
+        quant_q8_k(x + 256 * b, &y);
+        d[b] = y.d;
+        memcpy(qs + 256 * b, y.qs, 256);
+        memcpy(bsums + 16 * b, y.bsums, 32);
+    }
+    return 0;
+}
+
+/* one weight row decoded once for the vec_dot loop over the activation rows */
+typedef struct {
+    int8_t* a;       /* [K] codes: Q8_0 quants, Q4_K 0..15, Q6_K -32..31 */
+    float* d;        /* per block: f16 d (Q8_0, Q4_K, Q6_K) */
+    float* dmin;     /* per superblock: f16 dmin (Q4_K) */
+    int32_t* sc;     /* per sub-block: 6-bit scale (Q4_K, 8 per superblock) or int8 scale (Q6_K, 16) */
+    int32_t* mn;     /* per sub-block: 6-bit min (Q4_K) */
+} wrow_t;
+
+static void decode_row(int dt, const uint8_t* r, int64_t K, wrow_t* w) {
+    if (dt == HXO_Q8_0) {
+        for (int64_t b = 0; b < K / 32; b++) {
+            const uint8_t* p = r + 34 * b;
+            w->d[b] = ld_f16(p);
+            memcpy(w->a + 32 * b, p + 2, 32);
+        }
+    } else if (dt == HXO_Q4_K) {
+        for (int64_t b = 0; b < K / 256; b++) {
+            const uint8_t* p = r + 144 * b;
+            w->d[b] = ld_f16(p);
+            w->dmin[b] = ld_f16(p + 2);
+            for (int j = 0; j < 8; j++) {
+                int s, m;
+                q4k_scale_min(j, p + 4, &s, &m);
+                w->sc[8 * b + j] = s;
+                w->mn[8 * b + j] = m;
+            }
+            int8_t* a = w->a + 256 * b;
+            for (int c = 0; c < 4; c++)
+                for (int l = 0; l < 32; l++) {
+                    a[64 * c + l] = (int8_t)(p[16 + 32 * c + l] & 0xF);
+                    a[64 * c + 32 + l] = (int8_t)(p[16 + 32 * c + l] >> 4);
+                }
+        }
+    } else {   /* Q6_K */
+        for (int64_t b = 0; b < K / 256; b++) {
+            const uint8_t* p = r + 210 * b;
+            const uint8_t* ql = p;
+            const uint8_t* qh = p + 128;
+            w->d[b] = ld_f16(p + 208);
+            for (int j = 0; j < 16; j++) w->sc[16 * b + j] = (int8_t)p[192 + j];
+            int8_t* a = w->a + 256 * b;
+            for (int n = 0; n < 2; n++)
+                for (int l = 0; l < 32; l++) {
+                    a[128 * n + l] = (int8_t)(((ql[64 * n + l] & 0xF) | ((qh[32 * n + l] & 3) << 4)) - 32);
+                    a[128 * n + l + 32] = (int8_t)(((ql[64 * n + l + 32] & 0xF) | (((qh[32 * n + l] >> 2) & 3) << 4)) - 32);
+                    a[128 * n + l + 64] = (int8_t)(((ql[64 * n + l] >> 4) | (((qh[32 * n + l] >> 4) & 3) << 4)) - 32);
+                    a[128 * n + l + 96] = (int8_t)(((ql[64 * n + l + 32] >> 4) | (((qh[32 * n + l] >> 6) & 3) << 4)) - 32);
+                }
+        }
+    }
+}
+
+/* The integer parts of the vec_dot products below are exact, so they are
+ * computed with AVX2 integer vectors in whatever order is fast; only the
+ * float steps follow candle's order. lane8(q, a, n) returns, for l = 0..7,
+ * the sum over the n / 8 groups g of q[8g + l] * a[8g + l] (n = 16 or 32):
+ * candle's per-lane aux16 / aux32 partial for one sub-block. */
+static inline __m256i lane8_16(const int8_t* q, const int8_t* a) {
+    const __m256i p = _mm256_mullo_epi16(_mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)q)),
+                                         _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)a)));
+    return _mm256_add_epi32(_mm256_cvtepi16_epi32(_mm256_castsi256_si128(p)),
+                            _mm256_cvtepi16_epi32(_mm256_extracti128_si256(p, 1)));
+}
+static inline __m256i lane8_32(const int8_t* q, const int8_t* a) {
+    const __m256i p = _mm256_add_epi16(
+        _mm256_mullo_epi16(_mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)q)),
+                           _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)a))),
+        _mm256_mullo_epi16(_mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)(q + 16))),
+                           _mm256_cvtepi8_epi16(_mm_loadu_si128((const __m128i*)(a + 16)))));
+    return _mm256_add_epi32(_mm256_cvtepi16_epi32(_mm256_castsi256_si128(p)),
+                            _mm256_cvtepi16_epi32(_mm256_extracti128_si256(p, 1)));
+}
+static inline void store8(__m256i v, int32_t* o) { _mm256_storeu_si256((__m256i*)o, v); }
+
+/* vec_dot_unopt of a Q8_0 weight row with a Q8_0 activation row:
+ * sumf += (float)isum * d_w * d_x, block by block */
+static float vd_q8_0(const wrow_t* w, const uint8_t* xq, const float* xd, int64_t K) {
+    float sumf = 0.0f;
+    for (int64_t b = 0; b < K / 32; b++) {
+        int32_t t[8];
+        store8(lane8_32((const int8_t*)(xq + 34 * b + 2), w->a + 32 * b), t);
+        const int32_t s = t[0] + t[1] + t[2] + t[3] + t[4] + t[5] + t[6] + t[7];
+        sumf += (float)s * w->d[b] * xd[b];
+    }
+    return sumf;
+}
+
+/* vec_dot_unopt Q4_K x Q8_K: per superblock, 8 lane sums
+ * aux32[l] = sum_j scale_j sum_g q8 a (lane l of each 8-group of sub-block j),
+ * sums[l] += (d_w d_x) aux32[l]; sumf -= (dmin_w d_x) sum_j bsums_j min_{j/2};
+ * result sumf + sum_l sums[l] */
+static float vd_q4_k(const wrow_t* w, const q8k_t* xq, int64_t K) {
+    float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    float sumf = 0.0f;
+    for (int64_t b = 0; b < K / 256; b++) {
+        const q8k_t* y = xq + b;
+        const int8_t* a = w->a + 256 * b;
+        __m256i aux = _mm256_setzero_si256();
+        int32_t sumi = 0;
+        for (int j = 0; j < 16; j++) sumi += (int32_t)y->bsums[j] * w->mn[8 * b + j / 2];
+        for (int j = 0; j < 8; j++)
+            aux = _mm256_add_epi32(aux, _mm256_mullo_epi32(_mm256_set1_epi32(w->sc[8 * b + j]),
+                                                           lane8_32(y->qs + 32 * j, a + 32 * j)));
+        int32_t a32[8];
+        store8(aux, a32);
+        const float d = w->d[b] * y->d;
+        for (int l = 0; l < 8; l++) sums[l] += d * (float)a32[l];
+        const float dmin = w->dmin[b] * y->d;
+        sumf -= dmin * (float)sumi;
+    }
+    float s = -0.0f;
+    for (int l = 0; l < 8; l++) s += sums[l];
+    return sumf + s;
+}
+
+/* vec_dot_unopt Q6_K x Q8_K: per superblock, aux32[l] = sum_j scale_j sum_g q8 a
+ * over the sixteen 16-element groups, sums[l] += aux32[l] d; result
+ * sum_l sums[l]. candle accumulates aux32 in f32: every partial sum is an
+ * integer of magnitude at most 2^24 (32 terms of at most 128 * 128 * 32), so
+ * the int32 sums converted once are the same values. */
+static float vd_q6_k(const wrow_t* w, const q8k_t* xq, int64_t K) {
+    float sums[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int64_t b = 0; b < K / 256; b++) {
+        const q8k_t* y = xq + b;
+        const int8_t* a = w->a + 256 * b;
+        __m256i aux = _mm256_setzero_si256();
+        for (int j = 0; j < 16; j++)
+            aux = _mm256_add_epi32(aux, _mm256_mullo_epi32(_mm256_set1_epi32(w->sc[16 * b + j]),
+                                                           lane8_16(y->qs + 16 * j, a + 16 * j)));
+        int32_t a32[8];
+        store8(aux, a32);
+        const float d = w->d[b] * y->d;
+        for (int l = 0; l < 8; l++) sums[l] += (float)a32[l] * d;
+    }
+    float s = -0.0f;
+    for (int l = 0; l < 8; l++) s += sums[l];
+    return s;
+}
+
+/* f32 fmaf chain over k */
+static float dot_chain(const float* a, const float* b, int64_t K) {
+    float s = 0.0f;
+    for (int64_t k = 0; k < K; k++) s = fmaf(a[k], b[k], s);
+    return s;
+}
+
+/* out[r] = dot_chain(X row r, w) for 8 rows at once: the rows' chains run side
+ * by side in the 8 lanes of one vector (each lane the same sequential fmaf
+ * chain); xt holds the 8 rows transposed, xt[k][r] */
+typedef float v8f __attribute__((vector_size(32)));
+static void dot_chain8(const float* xt, const float* w, int64_t K, float* out) {
+    v8f acc = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int64_t k = 0; k < K; k++) {
+        v8f xv;
+        memcpy(&xv, xt + 8 * k, sizeof xv);
+        const v8f wv = {w[k], w[k], w[k], w[k], w[k], w[k], w[k], w[k]};
+        for (int l = 0; l < 8; l++) acc[l] = fmaf(xv[l], wv[l], acc[l]);
+    }
+    memcpy(out, &acc, sizeof acc);
+}
+
+/* MaybeQuantLinear::forward over m rows: out[m][N] = X[m][K] . W[N][K]^T */
+static void qlinear(int dt, const void* W, int64_t N, int64_t K, const float* X, int64_t m, float* out,
+                    int nthreads) {
+    const int64_t rb = hxo_row_bytes(dt, K);
+    const int quant = dt == HXO_Q8_0 || dt == HXO_Q4_K || dt == HXO_Q6_K;
+    if (!quant || m > 64) {
+        /* plain f32 Linear, or forward_via_f16: f16 weights and x, f16 output */
+        const int f16 = quant;
+        float* xr = (float*)malloc(sizeof(float) * m * K);
+        for (int64_t i = 0; i < m * K; i++) xr[i] = f16 ? hxo_f16_to_f32(hxo_f32_to_f16(X[i])) : X[i];
+        /* rows in blocks of 8, transposed: xt[blk][k][8] (padding rows zero) */
+        const int64_t nblk = (m + 7) / 8;
+        float* xt = (float*)calloc((size_t)(nblk * K * 8), sizeof(float));
+        for (int64_t r = 0; r < m; r++)
+            for (int64_t k = 0; k < K; k++) xt[((r / 8) * K + k) * 8 + (r % 8)] = xr[r * K + k];
+#ifdef _OPENMP
+#pragma omp parallel num_threads(nthreads)
+#endif
+        {
+            float* wr = (float*)malloc(sizeof(float) * K);
+            float o8[8];
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+            for (int64_t n = 0; n < N; n++) {
+                hxo_dequant(dt, (const uint8_t*)W + n * rb, K, wr);
+                if (f16)
+                    for (int64_t k = 0; k < K; k++) wr[k] = hxo_f16_to_f32(hxo_f32_to_f16(wr[k]));
+                for (int64_t b = 0; b < nblk; b++) {
+                    dot_chain8(xt + b * K * 8, wr, K, o8);
+                    for (int64_t r = 8 * b; r < m && r < 8 * b + 8; r++) {
+                        const float v = o8[r - 8 * b];
+                        out[r * N + n] = f16 ? hxo_f16_to_f32(hxo_f32_to_f16(v)) : v;
+                    }
+                }
+            }
+            free(wr);
+        }
+        free(xt);
+        free(xr);
+        return;
+    }
+    /* GGUF vec_dot: activations quantised per row to the vec_dot type */
+    const int64_t nsb = K / 256, nb = K / 32;
+    uint8_t* xq8 = NULL;
+    float* xd8 = NULL;   /* the Q8_0 activation blocks' d as f32 */
+    q8k_t* xqk = NULL;
+    if (dt == HXO_Q8_0) {
+        xq8 = (uint8_t*)malloc((size_t)(m * nb * 34));
+        xd8 = (float*)malloc(sizeof(float) * (size_t)(m * nb));
+        for (int64_t r = 0; r < m; r++)
+            for (int64_t b = 0; b < nb; b++) {
+                qz_q8_0(X + r * K + 32 * b, xq8 + (r * nb + b) * 34);
+                xd8[r * nb + b] = ld_f16(xq8 + (r * nb + b) * 34);
+            }
+    } else {
+        xqk = (q8k_t*)malloc(sizeof(q8k_t) * (size_t)(m * nsb));
+        for (int64_t r = 0; r < m; r++)
+            for (int64_t b = 0; b < nsb; b++) quant_q8_k(X + r * K + 256 * b, xqk + r * nsb + b);
+    }
+#ifdef _OPENMP
+#pragma omp parallel num_threads(nthreads)
+#endif
+    {
+        wrow_t w;
+        w.a = (int8_t*)malloc((size_t)K);
+        w.d = (float*)malloc(sizeof(float) * (size_t)nb);
+        w.dmin = (float*)malloc(sizeof(float) * (size_t)(nsb + 1));
+        w.sc = (int32_t*)malloc(sizeof(int32_t) * (size_t)(16 * nsb + 1));
+        w.mn = (int32_t*)malloc(sizeof(int32_t) * (size_t)(8 * nsb + 1));
+#ifdef _OPENMP
+#pragma omp for schedule(static)
+#endif
+        for (int64_t n = 0; n < N; n++) {
+            decode_row(dt, (const uint8_t*)W + n * rb, K, &w);
+            for (int64_t r = 0; r < m; r++) {
+                float v;
+                if (dt == HXO_Q8_0) v = vd_q8_0(&w, xq8 + r * nb * 34, xd8 + r * nb, K);
+                else if (dt == HXO_Q4_K) v = vd_q4_k(&w, xqk + r * nsb, K);
+                else v = vd_q6_k(&w, xqk + r * nsb, K);
+                out[r * N + n] = v;
+            }
+        }
+        free(w.a); free(w.d); free(w.dmin); free(w.sc); free(w.mn);
+    }
+    free(xq8);
+    free(xd8);
+    free(xqk);
+}
+
+/* test hook: one MaybeQuantLinear call (m rows) */
+int hxo_qlinear(int dt, const void* W, int64_t N, int64_t K, const float* X, int64_t m, float* out, int nthreads) {
+    if (hxo_row_bytes(dt, K) < 0 || N <= 0 || m < 0) return 1;
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#endif
+    qlinear(dt, W, N, K, X, m, out, nthreads);
+    return 0;
+}
+
+/* TpExpert::forward_partial at world size 1 over m rows of xf (gathered):
+ * out[m][H] = down(silu(gate x) * up x) */
+static void candle_expert(int gdt, const void* g, int udt, const void* u, int ddt, const void* d, int64_t H,
+                          int64_t I, const float* X, int64_t m, float* out, float* gbuf, float* ubuf, int nthreads) {
+    qlinear(gdt, g, I, H, X, m, gbuf, nthreads);
+    qlinear(udt, u, I, H, X, m, ubuf, nthreads);
+    for (int64_t i = 0; i < m * I; i++) {
+        const float v = gbuf[i];
+        gbuf[i] = (v / (1.0f + expf(-v))) * ubuf[i];
+    }
+    qlinear(ddt, d, H, I, gbuf, m, out, nthreads);
+}
+
+int hxo_moe_forward_candle(const hxo_moe* m, const void* x, int64_t T, const float* bias, float* y, int nthreads) {
+    int64_t H = m->hidden, E = m->num_experts, I = m->inter, Is = m->shared_inter;
+    int k = m->top_k;
+    if (hxo_row_bytes(m->gate_dtype, H) < 0 || hxo_row_bytes(m->up_dtype, H) < 0 ||
+        hxo_row_bytes(m->down_dtype, I) < 0)
+        return 1;
+    if (Is > 0 && (hxo_row_bytes(m->sgate_dtype, H) < 0 || hxo_row_bytes(m->sup_dtype, H) < 0 ||
+                   hxo_row_bytes(m->sdown_dtype, Is) < 0 || !m->seg))
+        return 1;
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#else
+    nthreads = 1;
+#endif
+    const int64_t F = T * k, KM = I > Is ? I : Is, R = T > F ? T : F;
+    int32_t* idx = (int32_t*)malloc(sizeof(int32_t) * F);
+    float* w = (float*)malloc(sizeof(float) * F);
+    int32_t* perm = (int32_t*)malloc(sizeof(int32_t) * F);
+    int32_t* offs = (int32_t*)malloc(sizeof(int32_t) * (E + 1));
+    float* xf = (float*)malloc(sizeof(float) * T * H);
+    float* xg = (float*)malloc(sizeof(float) * R * H);
+    float* og = (float*)malloc(sizeof(float) * R * H);
+    float* gbuf = (float*)malloc(sizeof(float) * R * KM);
+    float* ubuf = (float*)malloc(sizeof(float) * R * KM);
+    int rc = 0;
+    if (!idx || !w || !perm || !offs || !xf || !xg || !og || !gbuf || !ubuf) { rc = 2; goto done; }
+    rc = hxo_route(m, x, T, bias, NULL, NULL, idx, w);
+    if (rc) goto done;
+    rc = hxo_dispatch(idx, T, k, E, perm, offs, NULL);
+    if (rc) goto done;
+    for (int64_t i = 0; i < T * H; i++) xf[i] = ld_act(m->act_dtype, x, i);
+    for (int64_t i = 0; i < T * H; i++) y[i] = 0.0f;
+    {
+        const int64_t gb = hxo_row_bytes(m->gate_dtype, H) * I, ub = hxo_row_bytes(m->up_dtype, H) * I;
+        const int64_t db = hxo_row_bytes(m->down_dtype, I) * H;
+        for (int64_t e = 0; e < E; e++) {
+            const int64_t n = offs[e + 1] - offs[e];
+            if (n == 0) continue;
+            for (int64_t p = 0; p < n; p++)
+                memcpy(xg + p * H, xf + (int64_t)(perm[offs[e] + p] / k) * H, sizeof(float) * H);
+            candle_expert(m->gate_dtype, (const uint8_t*)m->gate + e * gb, m->up_dtype, (const uint8_t*)m->up + e * ub,
+                          m->down_dtype, (const uint8_t*)m->down + e * db, H, I, xg, n, og, gbuf, ubuf, nthreads);
+            for (int64_t p = 0; p < n; p++) {
+                const int32_t f = perm[offs[e] + p];
+                float* yt = y + (int64_t)(f / k) * H;
+                for (int64_t h = 0; h < H; h++) yt[h] = yt[h] + og[p * H + h] * w[f];
+            }
+        }
+    }
+    if (Is > 0) {
+        float* wr = (float*)malloc(sizeof(float) * H);
+        hxo_dequant(m->seg_dtype, m->seg, H, wr);
+        candle_expert(m->sgate_dtype, m->sgate, m->sup_dtype, m->sup, m->sdown_dtype, m->sdown, H, Is, xf, T, og,
+                      gbuf, ubuf, nthreads);
+        for (int64_t t = 0; t < T; t++) {
+            const float mix = 1.0f / (1.0f + expf(-dot_chain(xf + t * H, wr, H)));
+            for (int64_t h = 0; h < H; h++) y[t * H + h] = y[t * H + h] + og[t * H + h] * mix;
+        }
+        free(wr);
+    }
+done:
+    free(idx); free(w); free(perm); free(offs); free(xf); free(xg); free(og); free(gbuf); free(ubuf);
+    return rc;
 }

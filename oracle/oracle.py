@@ -59,6 +59,12 @@ def lib() -> C.CDLL:
         L.hxo_dispatch.argtypes = [vp, i64, i32, i64, vp, vp, vp]
         L.hxo_moe_forward.restype = i32
         L.hxo_moe_forward.argtypes = [vp, vp, i64, vp, vp, i32]
+        L.hxo_moe_forward_candle.restype = i32
+        L.hxo_moe_forward_candle.argtypes = [vp, vp, i64, vp, vp, i32]
+        L.hxo_qlinear.restype = i32
+        L.hxo_qlinear.argtypes = [i32, vp, i64, i64, vp, i64, vp, i32]
+        L.hxo_quant_q8_k.restype = i32
+        L.hxo_quant_q8_k.argtypes = [vp, i64, vp, vp, vp]
         L.hxo_make_qx.restype = C.c_float
         L.hxo_make_qx.argtypes = [i32, i32, vp, vp]
         L.hxo_make_qkx1.restype = None
@@ -118,6 +124,32 @@ def dequantize(dtype: int, q: np.ndarray, cols: int) -> np.ndarray:
     if rc:
         raise ValueError(f"hxo_dequant rc={rc}")
     return out
+
+
+def qlinear(dtype: int, w: np.ndarray, x: np.ndarray, nthreads: int = 0) -> np.ndarray:
+    """one MaybeQuantLinear call in candle's arithmetic: w GGUF rows [N, row_bytes]
+    (or f32 [N, K]), x f32 [m, K] -> [m, N]"""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w)
+    m, K = x.shape
+    N = w.shape[0]
+    out = np.empty((m, N), np.float32)
+    rc = lib().hxo_qlinear(dtype, _p(w), N, K, _p(x), m, _p(out), nthreads)
+    if rc:
+        raise ValueError(f"hxo_qlinear rc={rc}")
+    return out
+
+
+def quant_q8_k(x: np.ndarray):
+    """candle's BlockQ8K::from_float over a row -> (d [nb], qs int8 [n], bsums int16 [nb, 16])"""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    nb = x.size // 256
+    d = np.empty(nb, np.float32)
+    qs = np.empty(x.size, np.int8)
+    bs = np.empty((nb, 16), np.int16)
+    if lib().hxo_quant_q8_k(_p(x), x.size, _p(d), _p(qs), _p(bs)):
+        raise ValueError("row length must be a multiple of 256")
+    return d, qs, bs
 
 
 def make_qx(x: np.ndarray, nmax: int):
@@ -207,12 +239,25 @@ class OracleMoe:
         return lg, pr, ix, wt
 
     def forward(self, x, bias=None, nthreads=0):
+        """exact mode: dequantised weights, products accumulated in double"""
         x, T = self._x(x)
         y = np.empty((T, self.cfg[0]), np.float32)
         b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
         rc = lib().hxo_moe_forward(C.byref(self.s), _p(x), T, _p(b), _p(y), nthreads)
         if rc:
             raise ValueError(f"hxo_moe_forward rc={rc}")
+        return y
+
+    def forward_candle(self, x, bias=None, nthreads=0):
+        """candle-arithmetic mode: the reference's CPU path for quantised experts
+        (Q8_0 / Q8_K activation quantisation and integer vec_dot at m <= 64, the
+        f16 path above), same routing as forward()"""
+        x, T = self._x(x)
+        y = np.empty((T, self.cfg[0]), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        rc = lib().hxo_moe_forward_candle(C.byref(self.s), _p(x), T, _p(b), _p(y), nthreads)
+        if rc:
+            raise ValueError(f"hxo_moe_forward_candle rc={rc}")
         return y
 
 

@@ -67,3 +67,22 @@ def rel_err(got, ref):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     return float(np.abs(got - ref).max() / max(np.abs(ref).max(), 1e-30))
+
+
+def errors(got, ref):
+    """the three figures reported for a float output: normwise
+    max|y-r| / max|r| (the gate), cosine, and elementwise
+    max |y-r| / (|r| + 1e-3 max|r|)"""
+    got = np.asarray(got, np.float64).ravel()
+    ref = np.asarray(ref, np.float64).ravel()
+    m = max(np.abs(ref).max(), 1e-30)
+    return {"normwise": float(np.abs(got - ref).max() / m),
+            "cosine": float(got @ ref / max(np.linalg.norm(got) * np.linalg.norm(ref), 1e-300)),
+            "elementwise": float((np.abs(got - ref) / (np.abs(ref) + 1e-3 * m)).max())}
+
+
+def report(tag, got, ref):
+    e = errors(got, ref)
+    print(f"[err] {tag}: normwise {e['normwise']:.3e} cosine {e['cosine']:.7f} elementwise {e['elementwise']:.3e}",
+          flush=True)
+    return e

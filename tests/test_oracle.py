@@ -259,6 +259,169 @@ def test_make_qkx1_quants_closed_forms():
     assert O.make_qkx1(np.full(32, -0.2, np.float32), 15, 5) == (0.0, 0.0)
 
 
+# ------------------------------------------- candle's quantised-matmul arithmetic
+def _round_away(v):
+    """f32::round on float32 values: half away from zero (exact)"""
+    v = np.asarray(v, np.float32)
+    t = np.trunc(v)
+    return (t + np.sign(v) * (np.abs(v - t) >= 0.5)).astype(np.float32)
+
+
+def _q8k_np(x):
+    """BlockQ8K::from_float restated in numpy float32 ops"""
+    x = np.asarray(x, np.float32).reshape(-1, 256)
+    d = np.zeros(len(x), np.float32)
+    qs = np.zeros(x.shape, np.int32)
+    for b, row in enumerate(x):
+        i = int(np.argmax(np.abs(row)))           # first largest |x|
+        if row[i] == 0:
+            continue
+        iscale = np.float32(-128.0) / row[i]
+        qs[b] = np.minimum(_round_away(iscale * row), 127).astype(np.int32)
+        d[b] = np.float32(1.0) / iscale
+    return d, qs, qs.reshape(-1, 16, 16).sum(-1)
+
+
+def test_quant_q8_k_known_answer():
+    """iscale = -128 / (signed largest-|x| value), q = min(round(iscale x), 127):
+    the largest element maps to -128 and its negation saturates at 127;
+    bsums are sums of 16"""
+    x = np.zeros(256, np.float32)
+    x[:6] = [2.0, -2.0, 1.0, 0.0078125, -0.01171875, 0.5]
+    d, qs, bs = O.quant_q8_k(x)
+    assert d[0] == np.float32(-1.0 / 64.0)
+    assert list(qs[:6]) == [-128, 127, -64, -1, 1, -32]       # 0.5 and -0.75 round away from zero
+    assert bs[0, 0] == -128 + 127 - 64 - 1 + 1 - 32 and not bs[0, 1:].any()
+    x = np.random.default_rng(4).standard_normal(1024).astype(np.float32)
+    d2, q2, b2 = O.quant_q8_k(x)
+    dn, qn, bn = _q8k_np(x)
+    assert np.array_equal(d2, dn) and np.array_equal(q2.astype(np.int32), qn.ravel()) and np.array_equal(b2, bn)
+    assert not O.quant_q8_k(np.zeros(256, np.float32))[1].any()
+
+
+def _f16(b):
+    return np.frombuffer(np.ascontiguousarray(b).tobytes(), np.float16).astype(np.float32)
+
+
+def _vec_dot_np(dt, wrow, xrow):
+    """candle's vec_dot_unopt (weights GGUF row, activations f32 row) restated
+    with numpy float32 scalar ops in the published order"""
+    f32 = np.float32
+    if dt == O.Q8_0:
+        xb = O.quantize(O.Q8_0, xrow.reshape(1, -1))[0].reshape(-1, 34)
+        wb = wrow.reshape(-1, 34)
+        sumf = f32(0)
+        for bw, bx in zip(wb, xb):
+            si = int((bw[2:].view(np.int8).astype(np.int64) * bx[2:].view(np.int8).astype(np.int64)).sum())
+            sumf = f32(sumf + f32(f32(f32(si) * _f16(bw[:2])[0]) * _f16(bx[:2])[0]))
+        return sumf
+    d_x, q_x, bs_x = _q8k_np(xrow)
+    if dt == O.Q4_K:
+        wb = wrow.reshape(-1, 144)
+        sums = np.zeros(8, np.float32)
+        sumf = f32(0)
+        for b, blk in enumerate(wb):
+            sc = blk[4:16].astype(np.int64)
+            scale = [(sc[j] & 63) if j < 4 else ((sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4)) for j in range(8)]
+            mins = [(sc[j + 4] & 63) if j < 4 else ((sc[j + 4] >> 4) | ((sc[j] >> 6) << 4)) for j in range(8)]
+            qs = blk[16:].astype(np.int64).reshape(4, 32)
+            a = np.concatenate([np.concatenate([q & 0xF, q >> 4]) for q in qs])
+            q8 = q_x[b].astype(np.int64)
+            aux = np.zeros(8, np.int64)
+            for j in range(8):
+                aux += scale[j] * (q8[32 * j:32 * j + 32] * a[32 * j:32 * j + 32]).reshape(4, 8).sum(0)
+            sumi = sum(int(bs_x[b][j]) * mins[j // 2] for j in range(16))
+            d = f32(_f16(blk[0:2])[0] * d_x[b])
+            for l in range(8):
+                sums[l] = f32(sums[l] + f32(d * f32(aux[l])))
+            sumf = f32(sumf - f32(f32(_f16(blk[2:4])[0] * d_x[b]) * f32(sumi)))
+        s = f32(-0.0)
+        for l in range(8):
+            s = f32(s + sums[l])
+        return f32(sumf + s)
+    wb = wrow.reshape(-1, 210)
+    sums = np.zeros(8, np.float32)
+    for b, blk in enumerate(wb):
+        ql, qh = blk[:128].astype(np.int64), blk[128:192].astype(np.int64)
+        a = np.zeros(256, np.int64)
+        for n in range(2):
+            for l in range(32):
+                a[128 * n + l] = ((ql[64 * n + l] & 0xF) | ((qh[32 * n + l] & 3) << 4)) - 32
+                a[128 * n + l + 32] = ((ql[64 * n + l + 32] & 0xF) | (((qh[32 * n + l] >> 2) & 3) << 4)) - 32
+                a[128 * n + l + 64] = ((ql[64 * n + l] >> 4) | (((qh[32 * n + l] >> 4) & 3) << 4)) - 32
+                a[128 * n + l + 96] = ((ql[64 * n + l + 32] >> 4) | (((qh[32 * n + l] >> 6) & 3) << 4)) - 32
+        sc = blk[192:208].view(np.int8).astype(np.int64)
+        q8 = q_x[b].astype(np.int64)
+        aux = np.zeros(8, np.int64)
+        for j in range(16):
+            aux += sc[j] * (q8[16 * j:16 * j + 16] * a[16 * j:16 * j + 16]).reshape(2, 8).sum(0)
+        d = f32(_f16(blk[208:210])[0] * d_x[b])
+        for l in range(8):
+            sums[l] = f32(sums[l] + f32(f32(aux[l]) * d))
+    s = f32(-0.0)
+    for l in range(8):
+        s = f32(s + sums[l])
+    return s
+
+
+@pytest.mark.parametrize("dt", [O.Q8_0, O.Q4_K, O.Q6_K])
+def test_candle_vec_dot_matches_independent_restatement(dt):
+    """m <= 64: the oracle's vectorised vec_dot equals a plain numpy restatement
+    of candle's vec_dot_unopt bit for bit, and (the integer identity) agrees with
+    the f64 dot of the dequantised weights and dequantised activations"""
+    rng = np.random.default_rng(20 + dt)
+    K, N, m = 512, 6, 3
+    w = O.quantize(dt, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((m, K)).astype(np.float32)
+    got = O.qlinear(dt, w, x)
+    for r in range(m):
+        for n in range(N):
+            assert got[r, n].view(np.uint32) == np.float32(_vec_dot_np(dt, w[n], x[r])).view(np.uint32)
+    wd = O.dequantize(dt, w, K).astype(np.float64)
+    if dt == O.Q8_0:
+        xd = O.dequantize(O.Q8_0, O.quantize(O.Q8_0, x), K).astype(np.float64)
+    else:
+        xd = np.stack([np.concatenate([(d * q).astype(np.float64) for d, q in zip(*_q8k_np(row)[:2])])
+                       for row in x])
+    ref = xd @ wd.T
+    assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max()
+
+
+def test_candle_f16_path_above_64_rows():
+    """m > 64 (forward_via_f16): weights and x rounded to f16, an f32 fmaf chain
+    over k, the output rounded to f16"""
+    rng = np.random.default_rng(31)
+    K, N, m = 256, 3, 70
+    w = O.quantize(O.Q4_K, (rng.standard_normal((N, K)) * 0.02).astype(np.float32))
+    x = rng.standard_normal((m, K)).astype(np.float32)
+    got = O.qlinear(O.Q4_K, w, x)
+    wh = O.dequantize(O.Q4_K, w, K).astype(np.float16).astype(np.float64)
+    xh = x.astype(np.float16).astype(np.float64)
+    for r in (0, 33, 69):
+        for n in range(N):
+            acc = np.float32(0)
+            for kk in range(K):                      # fmaf: one rounding of an exact f64 a*b + c
+                acc = np.float32(xh[r, kk] * wh[n, kk] + np.float64(acc))
+            assert got[r, n] == np.float32(np.float16(acc))
+
+
+@pytest.mark.parametrize("fmt", [O.Q8_0, O.Q4_K])
+def test_candle_mode_close_to_exact_mode(fmt):
+    """the two forward modes share the routing and differ only by candle's
+    activation quantisation / f16 rounding: close (within 3e-2: 8-bit
+    activations move single outputs by a few tenths of a percent of max|y|,
+    more at small H), not equal"""
+    H, E, k, I, Is = 512, 16, 4, 256, 256
+    w = make_f32_block(40, H, E, I, Is)
+    fm = {"gate": fmt, "up": fmt, "down": O.Q6_K if fmt == O.Q4_K else fmt, "router": O.BF16, "seg": O.BF16}
+    fm.update({"sgate": fm["gate"], "sup": fm["up"], "sdown": fm["down"]})
+    orc = oracle_block((H, E, k, I, Is, True), store(w, fm), O.BF16)
+    for T in (1, 80):
+        x = bf16_bits(make_x(41, T, H))
+        a, c = orc.forward(x), orc.forward_candle(x)
+        assert 0 < rel_err(c, a) <= 3e-2
+
+
 # ------------------------------------------------------------------ router
 def tiny(seed=0, H=64, E=8, k=2, I=16, Is=16, norm=True, act=O.F32, fmt=None):
     w = make_f32_block(seed, H, E, I, Is, std=0.5)
