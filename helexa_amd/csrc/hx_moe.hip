@@ -108,6 +108,10 @@ struct hx_moe {
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// token counts above this are refused by every entry point: the kernels index
+// the T * k assignments with 32-bit integers (k <= HX_MAX_TOPK)
+#define HX_MAX_TOKENS ((int64_t)1 << 24)
+
 struct WsLayout {
   size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, hist, hbuf, hbf, xh, xcv, obuf, xn, ym, dpart,
       wpos, total;
@@ -607,7 +611,7 @@ extern "C" int hx_moe_forward(hx_moe* m, const void* x, int64_t n_tokens, void* 
                               size_t workspace_bytes, const float* router_bias, void* stream) {
   if (!m || n_tokens < 0 || (n_tokens > 0 && (!x || !y))) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
   if (n_tokens == 0) return HX_OK;
-  if (n_tokens > (int64_t)1 << 24) return fail(HX_ERR_UNSUPPORTED, "too many tokens in one call");
+  if (n_tokens > HX_MAX_TOKENS) return fail(HX_ERR_UNSUPPORTED, "too many tokens in one call");
   HX_HIP(hipSetDevice(m->device));
   return forward_impl(m, x, n_tokens, y, workspace, workspace_bytes, router_bias, (hipStream_t)stream);
 }
@@ -616,7 +620,7 @@ extern "C" int hx_moe_forward_noalloc(hx_moe* m, const void* x, int64_t n_tokens
                                       const float* router_bias, void* stream) {
   if (!m || n_tokens < 0 || (n_tokens > 0 && (!x || !y))) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
   if (n_tokens == 0) return HX_OK;
-  if (n_tokens > (int64_t)1 << 24) return fail(HX_ERR_UNSUPPORTED, "too many tokens in one call");
+  if (n_tokens > HX_MAX_TOKENS) return fail(HX_ERR_UNSUPPORTED, "too many tokens in one call");
   const size_t need = ws_layout(m, n_tokens).total;
   if (need > HX_NOALLOC_SCRATCH_BYTES)
     return fail(HX_ERR_WORKSPACE_TOO_SMALL,
@@ -633,6 +637,7 @@ extern "C" int hx_moe_forward_host(hx_moe* m, const void* x_host, int64_t n_toke
   if (!m || n_tokens < 0 || (n_tokens > 0 && (!x_host || !y_host)))
     return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
   if (n_tokens == 0) return HX_OK;
+  if (n_tokens > HX_MAX_TOKENS) return fail(HX_ERR_UNSUPPORTED, "too many tokens in one call");
   HX_HIP(hipSetDevice(m->device));
   const size_t bytes = (size_t)n_tokens * m->cfg.hidden_size * (m->cfg.act_dtype == HX_BF16 ? 2 : 4);
   void *dx = nullptr, *dy = nullptr;
@@ -659,6 +664,7 @@ extern "C" int hx_moe_route(hx_moe* m, const void* x, int64_t n_tokens, const fl
                             size_t workspace_bytes, void* stream) {
   if (!m || n_tokens < 0 || (n_tokens > 0 && !x)) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
   if (n_tokens == 0) return HX_OK;
+  if (n_tokens > HX_MAX_TOKENS) return fail(HX_ERR_UNSUPPORTED, "too many tokens in one call");
   HX_HIP(hipSetDevice(m->device));
   hipStream_t s = (hipStream_t)stream;
   WsLayout L;
@@ -681,6 +687,7 @@ extern "C" int hx_moe_router_logits(hx_moe* m, const void* x, int64_t n_tokens, 
                                     float* logits, void* stream) {
   if (!m || n_tokens < 0 || (n_tokens > 0 && (!x || !logits))) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
   if (n_tokens == 0) return HX_OK;
+  if (n_tokens > HX_MAX_TOKENS) return fail(HX_ERR_UNSUPPORTED, "too many tokens in one call");
   HX_HIP(hipSetDevice(m->device));
   hipStream_t s = (hipStream_t)stream;
   void* ws = nullptr;
@@ -702,6 +709,7 @@ extern "C" int hx_moe_decoder_mlp(hx_moe* m, void* x, int64_t n_tokens, const fl
                                   void* workspace, size_t workspace_bytes, void* stream) {
   if (!m || n_tokens < 0 || (n_tokens > 0 && (!x || !norm_w))) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
   if (n_tokens == 0) return HX_OK;
+  if (n_tokens > HX_MAX_TOKENS) return fail(HX_ERR_UNSUPPORTED, "too many tokens in one call");
   HX_HIP(hipSetDevice(m->device));
   hipStream_t s = (hipStream_t)stream;
   WsLayout L;

@@ -162,6 +162,25 @@ def _stream(stream=None) -> int:
     return int(s.cuda_stream)
 
 
+def _check_bias(bias, E: int, device) -> None:
+    """router_bias: None or a contiguous float32 [E] tensor on the block's device"""
+    import torch
+    if bias is None:
+        return
+    if bias.dtype != torch.float32 or tuple(bias.shape) != (E,) or not bias.is_contiguous() or bias.device != device:
+        raise ValueError(f"router_bias must be a contiguous float32 [{E}] tensor on {device}")
+
+
+def _check_acts(x, H: int, act: int, what: str = "xs") -> None:
+    """activations: a CUDA tensor of the block's dtype with last dim H"""
+    if not getattr(x, "is_cuda", False):
+        raise ValueError(f"{what} must be a CUDA tensor")
+    if x.shape[-1] != H:
+        raise ValueError(f"{what}: last dim {x.shape[-1]} != hidden {H}")
+    if _act_dtype(x.dtype) != act:
+        raise TypeError(f"{what}: activation dtype differs from the block's")
+
+
 def _act_dtype(torch_dtype) -> int:
     import torch
     if torch_dtype == torch.bfloat16:
@@ -234,11 +253,9 @@ class Qwen3_5MoeBlock:
         """Module::forward: xs (b, l, hidden) or (T, hidden) on this GPU -> same shape.
         `out`, if given, is a contiguous tensor of xs's shape and dtype to write."""
         import torch
-        if xs.shape[-1] != self.cfg.hidden_size:
-            raise ValueError(f"last dim {xs.shape[-1]} != hidden {self.cfg.hidden_size}")
-        if _act_dtype(xs.dtype) != self.act_dtype:
-            raise TypeError("activation dtype differs from the block's")
+        _check_acts(xs, self.cfg.hidden_size, self.act_dtype)
         x = xs.contiguous()
+        _check_bias(router_bias, self.cfg.num_experts, x.device)
         if out is None:
             y = torch.empty_like(x)
         else:
@@ -255,10 +272,8 @@ class Qwen3_5MoeBlock:
         """forward() through hx_moe_forward_noalloc: no workspace argument and no
         allocation inside the library (its per-GPU scratch is the workspace). `out`
         is required, a contiguous tensor of xs's shape and dtype."""
-        if xs.shape[-1] != self.cfg.hidden_size:
-            raise ValueError(f"last dim {xs.shape[-1]} != hidden {self.cfg.hidden_size}")
-        if _act_dtype(xs.dtype) != self.act_dtype:
-            raise TypeError("activation dtype differs from the block's")
+        _check_acts(xs, self.cfg.hidden_size, self.act_dtype)
+        _check_bias(router_bias, self.cfg.num_experts, xs.device)
         if not xs.is_contiguous():
             raise ValueError("xs must be contiguous (no copy is made here)")
         if out.shape != xs.shape or out.dtype != xs.dtype or not out.is_contiguous():
@@ -271,7 +286,9 @@ class Qwen3_5MoeBlock:
     def route(self, xs, router_bias=None, stream=None):
         """-> dict(topk_idx [T,k] i32, topk_w [T,k] f32, perm [T*k], offsets [E+1], inv [T*k])"""
         import torch
+        _check_acts(xs, self.cfg.hidden_size, self.act_dtype)
         x = xs.contiguous()
+        _check_bias(router_bias, self.cfg.num_experts, x.device)
         T = x.numel() // self.cfg.hidden_size
         k, E = self.cfg.num_experts_per_tok, self.cfg.num_experts
         dev = x.device
@@ -287,7 +304,9 @@ class Qwen3_5MoeBlock:
 
     def router_logits(self, xs, router_bias=None, stream=None):
         import torch
+        _check_acts(xs, self.cfg.hidden_size, self.act_dtype)
         x = xs.contiguous()
+        _check_bias(router_bias, self.cfg.num_experts, x.device)
         T = x.numel() // self.cfg.hidden_size
         out = torch.empty((T, self.cfg.num_experts), dtype=torch.float32, device=x.device)
         check(lib().hx_moe_router_logits(self._h, _ptr(x), T, _ptr(router_bias), _ptr(out), _stream(stream)),
@@ -295,8 +314,18 @@ class Qwen3_5MoeBlock:
         return out
 
     def decoder_mlp_(self, x, norm_w, eps: float, workspace=None, stream=None):
-        """x <- x + moe(rmsnorm(x)) in place (decoder.rs:129-132)."""
-        T = x.numel() // self.cfg.hidden_size
+        """x <- x + moe(rmsnorm(x)) in place (decoder.rs:129-132). x: contiguous
+        CUDA tensor [..., hidden] of the block's dtype; norm_w: contiguous float32
+        [hidden] on the same device."""
+        import torch
+        H = self.cfg.hidden_size
+        _check_acts(x, H, self.act_dtype, "x")
+        if not x.is_contiguous():
+            raise ValueError("x must be contiguous (it is updated in place)")
+        if (norm_w.dtype != torch.float32 or tuple(norm_w.shape) != (H,) or not norm_w.is_contiguous()
+                or norm_w.device != x.device):
+            raise ValueError(f"norm_w must be a contiguous float32 [{H}] tensor on {x.device}")
+        T = x.numel() // H
         ws_ptr, ws_n = (None, 0) if workspace is None else (_ptr(workspace), workspace.numel() * workspace.element_size())
         check(lib().hx_moe_decoder_mlp(self._h, _ptr(x), T, _ptr(norm_w), float(eps), ws_ptr, ws_n, _stream(stream)),
               "hx_moe_decoder_mlp")

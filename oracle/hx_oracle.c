@@ -770,7 +770,8 @@ static void expert_rows(int gdt, const void* g, int udt, const void* u, int ddt,
 #pragma omp parallel num_threads(nthreads)
 #endif
     {
-        float* wg = (float*)malloc(sizeof(float) * H);
+        /* wg also holds a down row (I elements) in the second loop */
+        float* wg = (float*)malloc(sizeof(float) * (H > I ? H : I));
         float* wu = (float*)malloc(sizeof(float) * H);
 #ifdef _OPENMP
 #pragma omp for schedule(static)
