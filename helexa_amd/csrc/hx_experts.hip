@@ -291,6 +291,9 @@ __global__ __launch_bounds__(256) void k_combine(ExpertArgs a) {
   const int n0 = (blockIdx.y * 256 + threadIdx.x) * 8;
   if (n0 >= a.H) return;
   const int nrows = k + (a.Is > 0 ? 1 : 0);
+  // the shared expert's row (row k) scaled here when the down GEMM stored it
+  // unweighted; the routed rows are multiplied by 1 (exact)
+  const float shs = a.shared_raw && a.Is > 0 ? a.sgw[t] : 1.f;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (a.xbf) {
     // rows loaded B at a time without branches: indices past the last row are
@@ -307,10 +310,11 @@ __global__ __launch_bounds__(256) void k_combine(ExpertArgs a) {
       for (int j = 0; j < B; j++) {
         const uint32_t m = j0 + j < nrows ? 0xffffffffu : 0u;
         const uint32_t w[4] = {q[j].x & m, q[j].y & m, q[j].z & m, q[j].w & m};
+        const float sc = j0 + j == k ? shs : 1.f;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          acc[2 * i] += __uint_as_float(w[i] << 16);
-          acc[2 * i + 1] += __uint_as_float(w[i] & 0xffff0000u);
+          acc[2 * i] += __uint_as_float(w[i] << 16) * sc;
+          acc[2 * i + 1] += __uint_as_float(w[i] & 0xffff0000u) * sc;
         }
       }
     }
@@ -324,8 +328,9 @@ __global__ __launch_bounds__(256) void k_combine(ExpertArgs a) {
     for (int j = 0; j < nrows; j++) {
       const float4* q = (const float4*)((const float*)a.obuf + (int64_t)spos[j] * a.H + n0);
       const float4 u = q[0], v = q[1];
-      acc[0] += u.x; acc[1] += u.y; acc[2] += u.z; acc[3] += u.w;
-      acc[4] += v.x; acc[5] += v.y; acc[6] += v.z; acc[7] += v.w;
+      const float sc = j == k ? shs : 1.f;
+      acc[0] += u.x * sc; acc[1] += u.y * sc; acc[2] += u.z * sc; acc[3] += u.w * sc;
+      acc[4] += v.x * sc; acc[5] += v.y * sc; acc[6] += v.z * sc; acc[7] += v.w * sc;
     }
     float4* p = (float4*)((float*)a.y + (int64_t)t * a.H + n0);
     p[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);

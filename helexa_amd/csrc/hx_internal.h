@@ -124,7 +124,19 @@ struct ExpertArgs {
   // decode down partial sums [groups of HX_DOWN_ROWS rows of h][T][H] when the
   // rows of h take more than one group
   float* dpart = nullptr;
+  // prefill MFMA kernels: which M tiles a launch covers -- HX_TILES_ALL: every
+  // tile of the dispatch list; HX_TILES_ROUTED: the routed experts' tiles of
+  // the list; HX_TILES_SHARED: the shared expert's tiles, computed from T (no
+  // list: such a launch needs no routing)
+  int tsel = 0;
+  // prefill: the shared expert's rows of the down GEMM are stored unweighted
+  // and the combine applies its sigmoid gate (the shared expert then runs
+  // before the routing has computed that gate)
+  bool shared_raw = false;
 };
+#define HX_TILES_ALL 0
+#define HX_TILES_ROUTED 1
+#define HX_TILES_SHARED 2
 
 // rows of h one decode down workgroup takes (4 waves x 6 rows each)
 constexpr int HX_XCV_WORDS = 20;

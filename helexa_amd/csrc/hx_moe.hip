@@ -83,8 +83,12 @@ extern "C" int64_t hx_row_bytes(int dtype, int64_t n) {
 // ----------------------------------------------------------------------------
 // timing slots
 // ----------------------------------------------------------------------------
-enum { SLOT_ROUTER = 0, SLOT_ROUTE_TOKENS, SLOT_DISPATCH, SLOT_GATE_UP, SLOT_DOWN, SLOT_COMBINE, SLOT_X_F16, N_SLOTS };
-static const char* kSlotNames[N_SLOTS] = {"router", "route_tokens", "dispatch", "gate_up", "down", "combine", "x_f16"};
+enum {
+  SLOT_ROUTER = 0, SLOT_ROUTE_TOKENS, SLOT_DISPATCH, SLOT_GATE_UP, SLOT_DOWN, SLOT_COMBINE, SLOT_X_F16,
+  SLOT_SH_GATE_UP, SLOT_SH_DOWN, N_SLOTS
+};
+static const char* kSlotNames[N_SLOTS] = {"router", "route_tokens", "dispatch", "gate_up", "down", "combine",
+                                          "x_f16", "shared_gate_up", "shared_down"};
 
 struct Timing {
   bool on = false;
@@ -104,6 +108,10 @@ struct hx_moe {
   void* own_ws = nullptr;
   size_t own_ws_bytes = 0;
   Timing tm;
+  // prefill: the shared expert's GEMMs run on `side` (default priority) while
+  // the caller's stream routes and dispatches; fork / join by the two events
+  hipStream_t side = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -229,6 +237,9 @@ extern "C" int hx_moe_destroy(hx_moe* m) {
   if (m->router) (void)hipFree(m->router);
   if (m->own_ws) (void)hipFree(m->own_ws);
   for (hipEvent_t e : m->tm.ev) (void)hipEventDestroy(e);
+  if (m->ev_fork) (void)hipEventDestroy(m->ev_fork);
+  if (m->ev_join) (void)hipEventDestroy(m->ev_join);
+  if (m->side) (void)hipStreamDestroy(m->side);
   delete m;
   return HX_OK;
 }
@@ -315,6 +326,12 @@ extern "C" int hx_moe_create(const hx_moe_config* cfg, const hx_moe_weights* w, 
   hx_moe* m = new hx_moe();
   m->cfg = c;
   m->device = device;
+  if (hipStreamCreateWithFlags(&m->side, hipStreamNonBlocking) != hipSuccess ||
+      hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming) != hipSuccess ||
+      hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming) != hipSuccess) {
+    hx_moe_destroy(m);
+    return fail(HX_ERR_DEVICE, "cannot create the handle's side stream / events");
+  }
   const int E = c.num_experts;
   if ((rc = build_router(m, w)) || (rc = upload_proj(m->gate, "experts.gate_proj", w->gate_dtype, w->experts_gate, w->location, E, I, H)) ||
       (rc = upload_proj(m->up, "experts.up_proj", w->up_dtype, w->experts_up, w->location, E, I, H)) ||
@@ -485,12 +502,17 @@ static void tm_ext_done(hx_moe* m, int slot) {
   t.used[(size_t)t.calls * N_SLOTS + slot] = 1;
 }
 
-static int run_routing(hx_moe* m, Plan& p, hipStream_t s) {
+static int run_router(hx_moe* m, Plan& p, hipStream_t s) {
   const bool xbf = m->cfg.act_dtype == HX_BF16, rbf = m->rdt == HX_BF16;
   tm_ext(m, SLOT_ROUTER, s);
   launch_router(p.ra, xbf, rbf, s);
   tm_ext_done(m, SLOT_ROUTER);
   HX_HIP(hipGetLastError());
+  return HX_OK;
+}
+
+// per-token routing and dispatch from the router's logits
+static int run_route_dispatch(hx_moe* m, Plan& p, hipStream_t s) {
   if (p.ra.T <= HX_DECODE_MAX_T) {
     tm_ext(m, SLOT_ROUTE_TOKENS, s);
     launch_route_small(p.ra, s);
@@ -507,6 +529,11 @@ static int run_routing(hx_moe* m, Plan& p, hipStream_t s) {
     HX_HIP(hipGetLastError());
   }
   return HX_OK;
+}
+
+static int run_routing(hx_moe* m, Plan& p, hipStream_t s) {
+  int rc = run_router(m, p, s);
+  return rc ? rc : run_route_dispatch(m, p, s);
 }
 
 // the decoder's RMSNorm and residual around the block (hx_moe_decoder_mlp)
@@ -577,19 +604,46 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
     HX_HIP(launch_down_gemv_combine(p.ea, s));
     tm_mark(m, SLOT_DOWN, 1, s);
   } else {
-    if ((rc = run_routing(m, p, s))) return rc;
     const bool mfma = prefill_mfma_ok(p.ea);
-    // MFMA path: one kernel per slot, each timed by its own dispatch
+    // MFMA path: one kernel per slot, each timed by its own dispatch. With a
+    // shared expert, its gate/up and down need only the f16 tokens: after the
+    // router kernel (which keeps every CU busy) they run on the side stream,
+    // next to the per-token routing and the dispatch (small kernels that leave
+    // most CUs idle), their down rows unweighted (the combine applies the
+    // sigmoid gate the routing computes); the routed GEMMs follow the dispatch
+    // on the caller's stream and the combine waits for both.
+    const bool split = mfma && m->cfg.shared_expert_intermediate_size > 0;
     if (mfma) {
       tm_ext(m, SLOT_X_F16, s);
       HX_HIP(launch_x_to_f16(p.ea, s));
       tm_ext_done(m, SLOT_X_F16);
+    }
+    if ((rc = run_router(m, p, s))) return rc;
+    if (split) {
+      ExpertArgs sa = p.ea;
+      sa.tsel = HX_TILES_SHARED;
+      sa.shared_raw = true;
+      HX_HIP(hipEventRecord(m->ev_fork, s));
+      HX_HIP(hipStreamWaitEvent(m->side, m->ev_fork, 0));
+      tm_ext(m, SLOT_SH_GATE_UP, m->side);
+      HX_HIP(launch_gate_up_mfma(sa, m->side));
+      tm_ext_done(m, SLOT_SH_GATE_UP);
+      tm_ext(m, SLOT_SH_DOWN, m->side);
+      HX_HIP(launch_down_mfma(sa, m->side));
+      tm_ext_done(m, SLOT_SH_DOWN);
+      HX_HIP(hipEventRecord(m->ev_join, m->side));
+      p.ea.tsel = HX_TILES_ROUTED;
+      p.ea.shared_raw = true;
+    }
+    if ((rc = run_route_dispatch(m, p, s))) return rc;
+    if (mfma) {
       tm_ext(m, SLOT_GATE_UP, s);
       HX_HIP(launch_gate_up_mfma(p.ea, s));
       tm_ext_done(m, SLOT_GATE_UP);
       tm_ext(m, SLOT_DOWN, s);
       HX_HIP(launch_down_mfma(p.ea, s));
       tm_ext_done(m, SLOT_DOWN);
+      if (split) HX_HIP(hipStreamWaitEvent(s, m->ev_join, 0));
     } else {
       tm_mark(m, SLOT_GATE_UP, 0, s);
       HX_HIP(launch_gate_up_prefill(p.ea, s));

@@ -213,6 +213,25 @@ HX_DEV void xcd_tile(int& nt, int& tile) {
 
 HX_DEV f16x8_t frag(const uint16_t* base) { return __builtin_bit_cast(f16x8_t, *(const uint4*)base); }
 
+// the M tile of a workgroup (expert, first permuted row, rows): from the
+// dispatch list, or for a shared-expert-only launch computed from T; false if
+// the workgroup has no tile (past the end, or a tile the launch skips)
+HX_DEV bool get_tile(const ExpertArgs& a, int tile, int& e, int& p0, int& rows) {
+  if (a.tsel == HX_TILES_SHARED) {
+    const int m0 = tile * PM;
+    if (m0 >= a.T) return false;
+    e = a.E;
+    p0 = a.F + m0;
+    rows = min(PM, a.T - m0);
+    return true;
+  }
+  if (tile >= a.counts[1]) return false;
+  e = a.tiles[4 * tile + 1];
+  p0 = a.tiles[4 * tile + 2];
+  rows = a.tiles[4 * tile + 3];
+  return !(a.tsel == HX_TILES_ROUTED && e == a.E);
+}
+
 // ---------------------------------------------------------------- Q4_K gate/up, streamed
 // k_gate_up_q4k<FPW, NW>: the gate/up GEMM for Q4_K weights, operands
 // streamed into LDS by the memory unit (global_load_lds_dwordx4: lane l's 16
@@ -478,8 +497,8 @@ __global__ __launch_bounds__(64 * NW, 3) void k_gate_up_q4k(ExpertArgs a) {
   __shared__ int rowsrc[PM];
   int nt, tile;
   xcd_tile(nt, tile);
-  if (tile >= a.counts[1]) return;
-  const int e = a.tiles[4 * tile + 1], p0 = a.tiles[4 * tile + 2], rows = a.tiles[4 * tile + 3];
+  int e, p0, rows;
+  if (!get_tile(a, tile, e, p0, rows)) return;
   const bool sh = e == a.E;
   const int n0 = nt * Q::COLS;
   const uint8_t* G = sh ? a.sgate.base : a.gate.mat(e);
@@ -695,15 +714,15 @@ __global__ __launch_bounds__(256, 3) void k_down_q6k(ExpertArgs a) {
   __shared__ float rws[PM];
   int nt, tile;
   xcd_tile(nt, tile);
-  if (tile >= a.counts[1]) return;
-  const int e = a.tiles[4 * tile + 1], p0 = a.tiles[4 * tile + 2], rows = a.tiles[4 * tile + 3];
+  int e, p0, rows;
+  if (!get_tile(a, tile, e, p0, rows)) return;
   const bool sh = e == a.E;
   const int n0 = nt * 128;
   const uint8_t* W = sh ? a.sdown.base : a.down.mat(e);
   const int lane = lane_id(), wave = threadIdx.x >> 6, l16 = lane & 15, kq = lane >> 4;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   // routing weights, loaded before the DMAs and first used after the last one
-  const float rw = threadIdx.x < PM ? a.wpos[p0 + min((int)threadIdx.x, rows - 1)] : 0.f;
+  const float rw = threadIdx.x >= PM ? 0.f : e == a.E && a.shared_raw ? 1.f : a.wpos[p0 + min((int)threadIdx.x, rows - 1)];
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)ring;
   // d of both superblocks of the 128 weight rows (waves 0 and 1, one dword each)
   if (wave_u < 2)
@@ -730,8 +749,8 @@ __global__ __launch_bounds__(256) void k_gate_up_mfma(ExpertArgs a) {
   __shared__ int rowsrc[PM];
   int nt, tile;
   xcd_tile(nt, tile);
-  if (tile >= a.counts[1]) return;
-  const int e = a.tiles[4 * tile + 1], p0 = a.tiles[4 * tile + 2], rows = a.tiles[4 * tile + 3];
+  int e, p0, rows;
+  if (!get_tile(a, tile, e, p0, rows)) return;
   const bool sh = e == a.E;
   const int I = sh ? a.Is : a.I, n0 = nt * 64;
   if (n0 >= I) return;
@@ -804,15 +823,15 @@ __global__ __launch_bounds__(256) void k_down_mfma(ExpertArgs a) {
   __shared__ float rw[PM];
   int nt, tile;
   xcd_tile(nt, tile);
-  if (tile >= a.counts[1]) return;
-  const int e = a.tiles[4 * tile + 1], p0 = a.tiles[4 * tile + 2], rows = a.tiles[4 * tile + 3];
+  int e, p0, rows;
+  if (!get_tile(a, tile, e, p0, rows)) return;
   const bool sh = e == a.E;
   const int K = sh ? a.Is : a.I, n0 = nt * 128, nk = K / PKC;
   const uint8_t* W = sh ? a.sdown.base : a.down.mat(e);
   if (threadIdx.x < PM) {
     const int p = p0 + threadIdx.x;
     rowsrc[threadIdx.x] = p0 + (threadIdx.x < rows ? threadIdx.x : 0);
-    rw[threadIdx.x] = threadIdx.x < rows ? (sh ? a.sgw[p - a.F] : a.topk_w[a.perm[p]]) : 0.f;
+    rw[threadIdx.x] = threadIdx.x < rows ? (sh ? (a.shared_raw ? 1.f : a.sgw[p - a.F]) : a.topk_w[a.perm[p]]) : 0.f;
   }
   __syncthreads();
   const int lane = lane_id(), wave = threadIdx.x >> 6, l16 = lane & 15, kq = lane >> 4;
@@ -895,9 +914,15 @@ hipError_t launch_x_to_f16(const ExpertArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// M tiles a launch's grid covers
+static int grid_tiles(const ExpertArgs& a) {
+  const int n = a.tsel == HX_TILES_SHARED ? (a.T + PM - 1) / PM : a.max_tiles;
+  return (n + 7) / 8 * 8;
+}
+
 // reads the f16 tokens launch_x_to_f16 wrote
 hipError_t launch_gate_up_mfma(const ExpertArgs& a, hipStream_t s) {
-  const dim3 grid(a.I / 64, (a.max_tiles + 7) / 8 * 8);
+  const dim3 grid(a.I / 64, grid_tiles(a));
   switch (a.gate.fmt) {
     case HX_Q4_K: hx_launch(k_gate_up_q4k<1, 4>, grid, dim3(256), 0, s, a); break;
     case HX_Q8_0: hx_launch(k_gate_up_mfma<HX_Q8_0>, grid, dim3(256), 0, s, a); break;
@@ -908,7 +933,7 @@ hipError_t launch_gate_up_mfma(const ExpertArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_down_mfma(const ExpertArgs& a, hipStream_t s) {
-  const dim3 grid(a.H / 128, (a.max_tiles + 7) / 8 * 8);
+  const dim3 grid(a.H / 128, grid_tiles(a));
   switch (a.down.fmt) {
     case HX_Q4_K: hx_launch(k_down_mfma<HX_Q4_K>, grid, dim3(256), 0, s, a); break;
     case HX_Q8_0: hx_launch(k_down_mfma<HX_Q8_0>, grid, dim3(256), 0, s, a); break;

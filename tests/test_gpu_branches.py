@@ -311,3 +311,33 @@ def test_wrapper_rejects_bad_arguments():
     assert L.hx_moe_forward_host(b.block.handle, fake, big, fake, None) == 2
     # still usable
     b.check(x, TOL_BF16)
+
+
+def test_prefill_shared_expert_side_stream_in_a_graph():
+    """prefill with a shared expert runs the shared expert's GEMMs on the
+    handle's side stream (forked from and joined back to the caller's stream):
+    captured into a HIP graph on a caller stream and replayed three times with
+    eager forwards between the replays, every replay equals the eager result
+    bit for bit, which is within tolerance of the oracle"""
+    _, synth = _hx()
+    b = Blk(2048, 64, 8, 512, 512, True, synth.FMT_Q4_K_M, O.BF16, 313)
+    x = b.x(200, seed=13)
+    ref = b.block.forward(x)
+    e = report("side-stream prefill T=200", ref.float().cpu().numpy(), b.oracle.forward(x_np(x)))
+    assert e["normwise"] <= TOL_BF16
+    ws = torch.empty(b.block.workspace_size(200), dtype=torch.uint8, device="cuda")
+    out = torch.zeros_like(x)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(g, stream=s):
+            b.block.forward(x, workspace=ws, stream=s, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    for r in range(3):
+        out.fill_(float("nan"))
+        b.block.forward(b.x(50, seed=100 + r))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {r}"
