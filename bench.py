@@ -263,25 +263,30 @@ def cpu_baseline_c2(cfg, host0, x0, runs=50):
                       f"{runs} runs after a warm-up, {th} OpenMP threads"}
 
 
-PREFILL_KERNELS = {"gate_up": "k_gate_up_q4k", "down": "k_down_q6k", "router": "k_router88"}
+# the routed gate/up launch is the dominant prefill kernel; the shared expert's
+# GEMMs are separate launches (template argument 2) on the handle's side stream
+PREFILL_KERNELS = {"gate_up": "k_gate_up_q4k<1, 4, 1>", "down": "k_down_q6k<1>", "router": "k_router88",
+                   "shared_gate_up": "k_gate_up_q4k<1, 4, 2>", "shared_down": "k_down_q6k<2>"}
 
 
 def prefill_work(cfg, fmts, T, U):
-    """Algorithmic flops and HBM bytes of one prefill forward, in total and for
-    the two MFMA kernels (each needed weight byte once; tokens in/out once; the
-    kernels' own inputs and outputs: f16 tokens, f16 SwiGLU rows h, weighted
-    bf16 rows)."""
+    """Algorithmic flops and HBM bytes of one prefill forward, in total and per
+    kernel (each needed weight byte once; tokens in/out once; a kernel's own
+    inputs and outputs: f16 tokens, f16 SwiGLU rows h, weighted bf16 rows):
+    gate_up / down are the routed experts' launches, shared_* the shared
+    expert's."""
     H, I, Is, E, k = cfg.hidden_size, cfg.moe_intermediate_size, cfg.shared_expert_intermediate_size, \
         cfg.num_experts, cfg.num_experts_per_tok
     F = T * k
-    gu_w = U * 2 * gguf_bytes(fmts["gate"], I, H) + 2 * gguf_bytes(fmts["sgate"], Is, H)
-    dn_w = U * gguf_bytes(fmts["down"], H, I) + gguf_bytes(fmts["sdown"], H, Is)
-    flops = {"gate_up": 2 * (F * 2 * H * I + T * 2 * H * Is), "down": 2 * (F * H * I + T * H * Is),
-             "router": 2 * T * H * (E + 1)}
-    kbytes = {"gate_up": gu_w + T * H * 2 + (F + T) * I * 2, "down": dn_w + (F + T) * I * 2 + (F + T) * H * 2,
+    gu_w, sgu_w = U * 2 * gguf_bytes(fmts["gate"], I, H), 2 * gguf_bytes(fmts["sgate"], Is, H)
+    dn_w, sdn_w = U * gguf_bytes(fmts["down"], H, I), gguf_bytes(fmts["sdown"], H, Is)
+    flops = {"gate_up": 2 * F * 2 * H * I, "down": 2 * F * H * I, "shared_gate_up": 2 * T * 2 * H * Is,
+             "shared_down": 2 * T * H * Is, "router": 2 * T * H * (E + 1)}
+    kbytes = {"gate_up": gu_w + T * H * 2 + F * I * 2, "down": dn_w + F * I * 2 + F * H * 2,
+              "shared_gate_up": sgu_w + T * H * 2 + T * Is * 2, "shared_down": sdn_w + T * Is * 2 + T * H * 2,
               "router": (E + 1) * H * 2 + T * H * 2}
     total_flops = 2 * T * k * 3 * H * I + 2 * T * 3 * H * Is + 2 * T * H * E
-    total_bytes = gu_w + dn_w + (E + 1) * H * 2 + 2 * T * H * 2
+    total_bytes = gu_w + sgu_w + dn_w + sdn_w + (E + 1) * H * 2 + 2 * T * H * 2
     return total_flops, total_bytes, flops, kbytes
 
 
@@ -322,7 +327,7 @@ def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=5, bias=None, pmc_f
     total_flops, total_bytes, kflops, kbytes = prefill_work(cfg, fmts, T, U)
     d_us = kern.get("gate_up", float("nan"))
     tfs = kflops["gate_up"] / (d_us * 1e-6) / 1e12
-    roof = {"bound": "mfma", "kernel": "gate_up (" + PREFILL_KERNELS["gate_up"] + ")", "achieved": round(tfs, 1),
+    roof = {"bound": "mfma", "kernel": "routed gate_up (" + PREFILL_KERNELS["gate_up"] + ")", "achieved": round(tfs, 1),
             "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s", "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4),
             "algorithmic_flops_per_launch": kflops["gate_up"], "algorithmic_bytes_per_launch": kbytes["gate_up"],
             "avg_launch_us": round(d_us, 2),

@@ -215,9 +215,12 @@ HX_DEV f16x8_t frag(const uint16_t* base) { return __builtin_bit_cast(f16x8_t, *
 
 // the M tile of a workgroup (expert, first permuted row, rows): from the
 // dispatch list, or for a shared-expert-only launch computed from T; false if
-// the workgroup has no tile (past the end, or a tile the launch skips)
+// the workgroup has no tile (past the end, or a tile the launch skips). TS is
+// the launch's tile selection (HX_TILES_*), a template parameter so that each
+// selection is a kernel of its own name in traces and counter runs.
+template <int TS>
 HX_DEV bool get_tile(const ExpertArgs& a, int tile, int& e, int& p0, int& rows) {
-  if (a.tsel == HX_TILES_SHARED) {
+  if (TS == HX_TILES_SHARED) {
     const int m0 = tile * PM;
     if (m0 >= a.T) return false;
     e = a.E;
@@ -229,7 +232,7 @@ HX_DEV bool get_tile(const ExpertArgs& a, int tile, int& e, int& p0, int& rows) 
   e = a.tiles[4 * tile + 1];
   p0 = a.tiles[4 * tile + 2];
   rows = a.tiles[4 * tile + 3];
-  return !(a.tsel == HX_TILES_ROUTED && e == a.E);
+  return !(TS == HX_TILES_ROUTED && e == a.E);
 }
 
 // ---------------------------------------------------------------- Q4_K gate/up, streamed
@@ -490,7 +493,7 @@ HX_DEV void q4k_main(const ExpertArgs& a, uint8_t* ring, const Q4kSrc<Q>& src, i
 
 // grid (I / COLS, tiles rounded up to 8), mapped by xcd_tile
 // (the second bound is waves per SIMD: 3 workgroups of 4 waves per CU)
-template <int FPW, int NW>
+template <int FPW, int NW, int TS>
 __global__ __launch_bounds__(64 * NW, 3) void k_gate_up_q4k(ExpertArgs a) {
   using Q = Q4k<FPW, NW>;
   __shared__ __attribute__((aligned(16))) uint8_t ring[Q::NST * Q::STAGE];
@@ -498,7 +501,7 @@ __global__ __launch_bounds__(64 * NW, 3) void k_gate_up_q4k(ExpertArgs a) {
   int nt, tile;
   xcd_tile(nt, tile);
   int e, p0, rows;
-  if (!get_tile(a, tile, e, p0, rows)) return;
+  if (!get_tile<TS>(a, tile, e, p0, rows)) return;
   const bool sh = e == a.E;
   const int n0 = nt * Q::COLS;
   const uint8_t* G = sh ? a.sgate.base : a.gate.mat(e);
@@ -709,13 +712,14 @@ HX_DEV void dq_main(const ExpertArgs& a, uint8_t* ring, float* rws, const DqSrc&
   }
 }
 
+template <int TS>
 __global__ __launch_bounds__(256, 3) void k_down_q6k(ExpertArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[DQ_NST * DQ_STAGE + 128 * 4];
   __shared__ float rws[PM];
   int nt, tile;
   xcd_tile(nt, tile);
   int e, p0, rows;
-  if (!get_tile(a, tile, e, p0, rows)) return;
+  if (!get_tile<TS>(a, tile, e, p0, rows)) return;
   const bool sh = e == a.E;
   const int n0 = nt * 128;
   const uint8_t* W = sh ? a.sdown.base : a.down.mat(e);
@@ -742,7 +746,7 @@ __global__ __launch_bounds__(256, 3) void k_down_q6k(ExpertArgs a) {
 // intermediate columns; wave w owns columns
 // 16w .. 16w+15 of gate and of up for all 64 rows. h = silu(gate) * up is
 // written as f16 in the swizzled order.
-template <int FMT>
+template <int FMT, int TS>
 __global__ __launch_bounds__(256) void k_gate_up_mfma(ExpertArgs a) {
   __shared__ uint16_t As[PM * PLD];
   __shared__ uint16_t Bs[128 * PLD];
@@ -750,7 +754,7 @@ __global__ __launch_bounds__(256) void k_gate_up_mfma(ExpertArgs a) {
   int nt, tile;
   xcd_tile(nt, tile);
   int e, p0, rows;
-  if (!get_tile(a, tile, e, p0, rows)) return;
+  if (!get_tile<TS>(a, tile, e, p0, rows)) return;
   const bool sh = e == a.E;
   const int I = sh ? a.Is : a.I, n0 = nt * 64;
   if (n0 >= I) return;
@@ -815,7 +819,7 @@ __global__ __launch_bounds__(256) void k_gate_up_mfma(ExpertArgs a) {
 // output columns; wave w owns columns
 // 32w .. 32w+31. Rows are scaled by their routing weight (shared expert: the
 // sigmoid gate) and written to the per-assignment output rows.
-template <int FMT>
+template <int FMT, int TS>
 __global__ __launch_bounds__(256) void k_down_mfma(ExpertArgs a) {
   __shared__ uint16_t As[PM * PLD];
   __shared__ uint16_t Bs[128 * PLD];
@@ -824,7 +828,7 @@ __global__ __launch_bounds__(256) void k_down_mfma(ExpertArgs a) {
   int nt, tile;
   xcd_tile(nt, tile);
   int e, p0, rows;
-  if (!get_tile(a, tile, e, p0, rows)) return;
+  if (!get_tile<TS>(a, tile, e, p0, rows)) return;
   const bool sh = e == a.E;
   const int K = sh ? a.Is : a.I, n0 = nt * 128, nk = K / PKC;
   const uint8_t* W = sh ? a.sdown.base : a.down.mat(e);
@@ -921,29 +925,47 @@ static int grid_tiles(const ExpertArgs& a) {
 }
 
 // reads the f16 tokens launch_x_to_f16 wrote
-hipError_t launch_gate_up_mfma(const ExpertArgs& a, hipStream_t s) {
+template <int TS>
+static hipError_t gate_up_mfma_ts(const ExpertArgs& a, hipStream_t s) {
   const dim3 grid(a.I / 64, grid_tiles(a));
   switch (a.gate.fmt) {
-    case HX_Q4_K: hx_launch(k_gate_up_q4k<1, 4>, grid, dim3(256), 0, s, a); break;
-    case HX_Q8_0: hx_launch(k_gate_up_mfma<HX_Q8_0>, grid, dim3(256), 0, s, a); break;
-    case HX_Q6_K: hx_launch(k_gate_up_mfma<HX_Q6_K>, grid, dim3(256), 0, s, a); break;
+    case HX_Q4_K: hx_launch(k_gate_up_q4k<1, 4, TS>, grid, dim3(256), 0, s, a); break;
+    case HX_Q8_0: hx_launch(k_gate_up_mfma<HX_Q8_0, TS>, grid, dim3(256), 0, s, a); break;
+    case HX_Q6_K: hx_launch(k_gate_up_mfma<HX_Q6_K, TS>, grid, dim3(256), 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gate_up_mfma(const ExpertArgs& a, hipStream_t s) {
+  switch (a.tsel) {
+    case HX_TILES_ROUTED: return gate_up_mfma_ts<HX_TILES_ROUTED>(a, s);
+    case HX_TILES_SHARED: return gate_up_mfma_ts<HX_TILES_SHARED>(a, s);
+    default: return gate_up_mfma_ts<HX_TILES_ALL>(a, s);
+  }
+}
+
+template <int TS>
+static hipError_t down_mfma_ts(const ExpertArgs& a, hipStream_t s) {
+  const dim3 grid(a.H / 128, grid_tiles(a));
+  switch (a.down.fmt) {
+    case HX_Q4_K: hx_launch(k_down_mfma<HX_Q4_K, TS>, grid, dim3(256), 0, s, a); break;
+    case HX_Q8_0: hx_launch(k_down_mfma<HX_Q8_0, TS>, grid, dim3(256), 0, s, a); break;
+    case HX_Q6_K:
+      if (a.I == DQ_K && (a.wpos || TS == HX_TILES_SHARED)) hx_launch(k_down_q6k<TS>, grid, dim3(256), 0, s, a);
+      else hx_launch(k_down_mfma<HX_Q6_K, TS>, grid, dim3(256), 0, s, a);
+      break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
 hipError_t launch_down_mfma(const ExpertArgs& a, hipStream_t s) {
-  const dim3 grid(a.H / 128, grid_tiles(a));
-  switch (a.down.fmt) {
-    case HX_Q4_K: hx_launch(k_down_mfma<HX_Q4_K>, grid, dim3(256), 0, s, a); break;
-    case HX_Q8_0: hx_launch(k_down_mfma<HX_Q8_0>, grid, dim3(256), 0, s, a); break;
-    case HX_Q6_K:
-      if (a.I == DQ_K && a.wpos) hx_launch(k_down_q6k, grid, dim3(256), 0, s, a);
-      else hx_launch(k_down_mfma<HX_Q6_K>, grid, dim3(256), 0, s, a);
-      break;
-    default: return hipErrorInvalidValue;
+  switch (a.tsel) {
+    case HX_TILES_ROUTED: return down_mfma_ts<HX_TILES_ROUTED>(a, s);
+    case HX_TILES_SHARED: return down_mfma_ts<HX_TILES_SHARED>(a, s);
+    default: return down_mfma_ts<HX_TILES_ALL>(a, s);
   }
-  return hipGetLastError();
 }
 
 }  // namespace hx
