@@ -489,7 +489,8 @@ def bench_c5(T=4096, target_share=0.40, reps=5, cpu_runs=0):
     blk.close()
     del blk
     out = prefill_run(cfg, fmts, 4243, 78, T, f"C5: {T}-token prefill, Q4_K_M, Zipf(1.1) router bias", reps,
-                      bias=base * alpha, mfma_file="c5_prefill_mfma.txt", trace_file="c5_prefill_kernels.txt",
+                      bias=base * alpha, pmc_file="c5_prefill_pmc.txt", mfma_file="c5_prefill_mfma.txt",
+                      trace_file="c5_prefill_kernels.txt",
                       cpu_runs=cpu_runs)
     out.update({"alpha": round(alpha, 4), "top8_share": round(achieved, 4)})
     return out

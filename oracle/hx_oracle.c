@@ -62,10 +62,13 @@
  *   - hxo_quantize restates candle's from_float rules from the published
  *     algorithms; byte parity with candle itself is unpinned (forward parity
  *     never depends on it: both sides are fed the same GGUF bytes).
- *   - candle's quantised-matmul arithmetic (QMatMul activation quantisation to
- *     Q8_K / Q8_0 at m <= 64, the f16 path at m > 64) is not restated; the
- *     forward here accumulates dequantised weights in double, and agreement
- *     with candle is only to the tolerance the tests state.
+ *   - two forward modes: hxo_moe_forward (exact: dequantised weights, products
+ *     accumulated in double) and hxo_moe_forward_candle (candle's CPU
+ *     quantised-matmul arithmetic, restated in its own section below). The
+ *     candle mode is pinned bit for bit against an independent numpy
+ *     restatement of the integer vec_dot and against the f64 dot of the
+ *     dequantised operands, but not against candle itself (its CPU build is
+ *     not available here).
  */
 #include <immintrin.h>
 #include <math.h>
