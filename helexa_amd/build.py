@@ -4,7 +4,10 @@
     python -m helexa_amd.build --jobs 8
 
 Flags: -ffp-contract=off keeps every multiply-add explicit (the routing contract
-spells out its fmaf chains); packed fp32 instructions are disabled.
+spells out its fmaf chains); packed fp32 instructions are disabled. The MFMA
+router (hx_route_mfma.hip) is compiled with MFMA results in VGPRs: it adds every
+MFMA's result to its running sums with VALU instructions, which would otherwise
+first copy each result out of the accumulation registers.
 """
 from __future__ import annotations
 
@@ -19,7 +22,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libhxmoe.so")
-SOURCES = ["hx_route.hip", "hx_experts.hip", "hx_decode.hip", "hx_prefill.hip", "hx_weights.hip", "hx_moe.hip"]
+SOURCES = ["hx_route.hip", "hx_route_mfma.hip", "hx_experts.hip", "hx_decode.hip", "hx_prefill.hip", "hx_weights.hip", "hx_moe.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 CFLAGS = [
@@ -30,9 +33,12 @@ CFLAGS = [
 ]
 
 
+EXTRA = {"hx_route_mfma.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [HIPCC, *CFLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [HIPCC, *CFLAGS, *EXTRA.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     out = "\n".join(l for l in (r.stdout + r.stderr).splitlines() if "packed-fp32-ops" not in l)
     if r.returncode != 0:

@@ -79,6 +79,9 @@ struct RouterArgs {
   const float* norm_w = nullptr;
   float eps = 0.f;
   uint16_t* xn_out = nullptr;
+  // |r_e| rounded up, per router row (bf16 router rows): the MFMA prefill
+  // routing bounds each logit with it
+  const float* rnorm = nullptr;
 };
 
 // One projection stack: E matrices of [rows][K] in the internal layout.
@@ -147,6 +150,12 @@ void launch_router(const RouterArgs& a, bool xbf, bool rbf, hipStream_t s);
 void launch_route_small(const RouterArgs& a, hipStream_t s);   // T <= HX_DECODE_MAX_T, one workgroup
 void launch_route_tokens(const RouterArgs& a, hipStream_t s);
 void launch_dispatch(const DispatchArgs& d, hipStream_t s);
+// prefill routing with the router GEMM on MFMA (bf16 tokens and router rows,
+// renormalised top-k): approximate logits, then per token the exact top-k
+bool route_mfma_ok(const RouterArgs& a, bool xbf, bool rbf);
+void launch_router_mfma(const RouterArgs& a, hipStream_t s);
+void launch_route_mfma(const RouterArgs& a, hipStream_t s);
+hipError_t launch_row_norms(const void* R, int E1, int H, float* out, hipStream_t s);
 
 // decode (T <= HX_DECODE_MAX_T)
 bool decode_fast_ok(const ExpertArgs& a);   // bf16 activations, GGUF weights: f16 dot2 kernels

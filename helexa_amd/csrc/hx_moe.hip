@@ -104,6 +104,7 @@ struct hx_moe {
   int E1 = 0;
   int rdt = HX_F32;   // dtype of the combined router rows
   void* router = nullptr;
+  float* rnorm = nullptr;   // [E1] |router row| rounded up (bf16 router rows only)
   WMat gate, up, down, sgate, sup, sdown;
   void* own_ws = nullptr;
   size_t own_ws_bytes = 0;
@@ -235,6 +236,7 @@ extern "C" int hx_moe_destroy(hx_moe* m) {
   free_mat(m->gate); free_mat(m->up); free_mat(m->down);
   free_mat(m->sgate); free_mat(m->sup); free_mat(m->sdown);
   if (m->router) (void)hipFree(m->router);
+  if (m->rnorm) (void)hipFree(m->rnorm);
   if (m->own_ws) (void)hipFree(m->own_ws);
   for (hipEvent_t e : m->tm.ev) (void)hipEventDestroy(e);
   if (m->ev_fork) (void)hipEventDestroy(m->ev_fork);
@@ -278,6 +280,12 @@ static int build_router(hx_moe* m, const hx_moe_weights* w) {
   if (sh && (rc = fetch(w->shared_expert_gate, sd, 1, host.data() + (size_t)E * H * es))) return rc;
   if (hipMalloc(&m->router, host.size()) != hipSuccess) return fail(HX_ERR_OUT_OF_MEMORY, "router allocation");
   HX_HIP(hipMemcpy(m->router, host.data(), host.size(), hipMemcpyHostToDevice));
+  if (m->rdt == HX_BF16) {
+    if (hipMalloc((void**)&m->rnorm, sizeof(float) * m->E1) != hipSuccess)
+      return fail(HX_ERR_OUT_OF_MEMORY, "router norm allocation");
+    HX_HIP(launch_row_norms(m->router, m->E1, H, m->rnorm, 0));
+    HX_HIP(hipDeviceSynchronize());
+  }
   return HX_OK;
 }
 
@@ -404,6 +412,7 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
   r.norm = c.norm_topk_prob != 0;
   r.has_shared = c.shared_expert_intermediate_size > 0;
   r.bias = bias;
+  r.rnorm = m->rnorm;
   r.logits = (float*)(ws + L.logits);
   r.topk_w = (float*)(ws + L.topk_w);
   r.sgw = (float*)(ws + L.sgw);
@@ -502,10 +511,16 @@ static void tm_ext_done(hx_moe* m, int slot) {
   t.used[(size_t)t.calls * N_SLOTS + slot] = 1;
 }
 
+// the prefill routing on MFMA (approximate logits, exact top-k per token)
+static bool route_mfma(const hx_moe* m, const Plan& p) {
+  return route_mfma_ok(p.ra, m->cfg.act_dtype == HX_BF16, m->rdt == HX_BF16);
+}
+
 static int run_router(hx_moe* m, Plan& p, hipStream_t s) {
   const bool xbf = m->cfg.act_dtype == HX_BF16, rbf = m->rdt == HX_BF16;
   tm_ext(m, SLOT_ROUTER, s);
-  launch_router(p.ra, xbf, rbf, s);
+  if (route_mfma(m, p)) launch_router_mfma(p.ra, s);
+  else launch_router(p.ra, xbf, rbf, s);
   tm_ext_done(m, SLOT_ROUTER);
   HX_HIP(hipGetLastError());
   return HX_OK;
@@ -520,7 +535,8 @@ static int run_route_dispatch(hx_moe* m, Plan& p, hipStream_t s) {
     HX_HIP(hipGetLastError());
   } else {
     tm_ext(m, SLOT_ROUTE_TOKENS, s);
-    launch_route_tokens(p.ra, s);
+    if (route_mfma(m, p)) launch_route_mfma(p.ra, s);
+    else launch_route_tokens(p.ra, s);
     tm_ext_done(m, SLOT_ROUTE_TOKENS);
     HX_HIP(hipGetLastError());
     tm_mark(m, SLOT_DISPATCH, 0, s);

@@ -179,11 +179,13 @@ HX_DEV int route_round(uint32_t* h, uint32_t* l, uint32_t& pend, uint32_t& m) {
 // chosen lane pops. The pop is split: the head is replaced at once (the next
 // reduction needs it); the rest of the shift is applied during the next
 // round's reduction, which does not depend on it.
+// v: this lane's logits (expert lane + 64 j in v[j], padding -inf); mx: their
+// wave-wide maximum.
 template <int EPL>
-HX_DEV void route_token_core(const float* lg, int E, int k, bool norm, int& out_e, float& out_w) {
+HX_DEV void route_token_regs(float* v, float mx, int k, bool norm, int& out_e, float& out_w) {
   const int lane = lane_id();
   uint32_t h[EPL], l[EPL];
-  route_keys<EPL>(lg, E, h, l);
+  route_keys_from<EPL>(v, mx, h, l);
   float my_p = 0.0f, tot = 0.0f;
   int my_e = 0;
   uint32_t pend = 0u;   // all-ones in the lane popped by the previous round
@@ -197,6 +199,14 @@ HX_DEV void route_token_core(const float* lg, int E, int k, bool norm, int& out_
   }
   out_e = my_e;
   out_w = norm ? my_p / tot : my_p;
+}
+
+// the same from the token's logits row lg (E values) in memory
+template <int EPL>
+HX_DEV void route_token_core(const float* lg, int E, int k, bool norm, int& out_e, float& out_w) {
+  float v[EPL];
+  const float mx = route_logits<EPL>(lg, E, v);
+  route_token_regs<EPL>(v, mx, k, norm, out_e, out_w);
 }
 
 // route_token_core with K rounds unrolled and hook(r, e) called right after

@@ -86,3 +86,25 @@ def report(tag, got, ref):
     print(f"[err] {tag}: normwise {e['normwise']:.3e} cosine {e['cosine']:.7f} elementwise {e['elementwise']:.3e}",
           flush=True)
     return e
+
+
+def mfma_routing(T, H, E, k, norm, act_bf16, router_bf16):
+    """whether a route / forward of T tokens takes the prefill routing whose
+    router GEMM runs on MFMA: ids and permutation bit-exact, the renormalised
+    weights exp(l_r - max) / sum over the selected (the softmax denominator
+    cancels) within a few ulps of the reference's p_r / sum p"""
+    return (T > 8 and act_bf16 and router_bf16 and norm and H % 32 == 0 and 32 <= H <= 4096
+            and E <= 1024 and k <= 64)
+
+
+def assert_topk_w(got, ref, k, exact):
+    """routing weights: bit-exact, or (MFMA routing) within (4k + 8) u of the
+    reference relative to each weight, u = 2^-24 -- twice the rounding steps
+    of the two formulas"""
+    got = np.asarray(got, np.float32)
+    ref = np.asarray(ref, np.float32)
+    if exact:
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+        return
+    rel = np.abs(got.astype(np.float64) - ref) / np.maximum(np.abs(ref.astype(np.float64)), 1e-30)
+    assert float(rel.max()) <= (4 * k + 8) * 2.0 ** -24, float(rel.max())
