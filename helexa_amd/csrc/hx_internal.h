@@ -149,11 +149,15 @@ __host__ __device__ inline int down_groups(int F, int T) { return (F + T + HX_DO
 void launch_router(const RouterArgs& a, bool xbf, bool rbf, hipStream_t s);
 void launch_route_small(const RouterArgs& a, hipStream_t s);   // T <= HX_DECODE_MAX_T, one workgroup
 void launch_route_tokens(const RouterArgs& a, hipStream_t s);
-void launch_dispatch(const DispatchArgs& d, hipStream_t s);
+// hist_ready: the per-chunk histogram is already in d.hist (the MFMA routing
+// fills it)
+void launch_dispatch(const DispatchArgs& d, hipStream_t s, bool hist_ready = false);
 // prefill routing with the router GEMM on MFMA (bf16 tokens and router rows,
 // renormalised top-k): approximate logits, then per token the exact top-k
 bool route_mfma_ok(const RouterArgs& a, bool xbf, bool rbf);
-void launch_router_mfma(const RouterArgs& a, hipStream_t s);
+// also writes the f16 tokens for the MFMA expert kernels when xh is not null,
+// and clears the dispatch histogram that launch_route_mfma fills
+void launch_router_mfma(const RouterArgs& a, uint16_t* xh, hipStream_t s);
 void launch_route_mfma(const RouterArgs& a, hipStream_t s);
 hipError_t launch_row_norms(const void* R, int E1, int H, float* out, hipStream_t s);
 

@@ -334,9 +334,13 @@ extern "C" int hx_moe_create(const hx_moe_config* cfg, const hx_moe_weights* w, 
   hx_moe* m = new hx_moe();
   m->cfg = c;
   m->device = device;
+  // the fork / join events order work of two streams on this one device: a
+  // device-scope release / acquire is enough (no system-scope fence, which
+  // writes back and invalidates the caches for the host at every record)
+  const unsigned evf = hipEventDisableTiming | hipEventDisableSystemFence;
   if (hipStreamCreateWithFlags(&m->side, hipStreamNonBlocking) != hipSuccess ||
-      hipEventCreateWithFlags(&m->ev_fork, hipEventDisableTiming) != hipSuccess ||
-      hipEventCreateWithFlags(&m->ev_join, hipEventDisableTiming) != hipSuccess) {
+      hipEventCreateWithFlags(&m->ev_fork, evf) != hipSuccess ||
+      hipEventCreateWithFlags(&m->ev_join, evf) != hipSuccess) {
     hx_moe_destroy(m);
     return fail(HX_ERR_DEVICE, "cannot create the handle's side stream / events");
   }
@@ -516,10 +520,11 @@ static bool route_mfma(const hx_moe* m, const Plan& p) {
   return route_mfma_ok(p.ra, m->cfg.act_dtype == HX_BF16, m->rdt == HX_BF16);
 }
 
-static int run_router(hx_moe* m, Plan& p, hipStream_t s) {
+// xh: where the MFMA router also writes the f16 tokens (or null)
+static int run_router(hx_moe* m, Plan& p, hipStream_t s, uint16_t* xh = nullptr) {
   const bool xbf = m->cfg.act_dtype == HX_BF16, rbf = m->rdt == HX_BF16;
   tm_ext(m, SLOT_ROUTER, s);
-  if (route_mfma(m, p)) launch_router_mfma(p.ra, s);
+  if (route_mfma(m, p)) launch_router_mfma(p.ra, xh, s);
   else launch_router(p.ra, xbf, rbf, s);
   tm_ext_done(m, SLOT_ROUTER);
   HX_HIP(hipGetLastError());
@@ -540,7 +545,7 @@ static int run_route_dispatch(hx_moe* m, Plan& p, hipStream_t s) {
     tm_ext_done(m, SLOT_ROUTE_TOKENS);
     HX_HIP(hipGetLastError());
     tm_mark(m, SLOT_DISPATCH, 0, s);
-    launch_dispatch(p.ra.d, s);
+    launch_dispatch(p.ra.d, s, route_mfma(m, p));
     tm_mark(m, SLOT_DISPATCH, 1, s);
     HX_HIP(hipGetLastError());
   }
@@ -629,12 +634,14 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
     // sigmoid gate the routing computes); the routed GEMMs follow the dispatch
     // on the caller's stream and the combine waits for both.
     const bool split = mfma && m->cfg.shared_expert_intermediate_size > 0;
-    if (mfma) {
+    // the MFMA router writes the f16 tokens itself
+    const bool xh_in_router = mfma && route_mfma(m, p);
+    if (mfma && !xh_in_router) {
       tm_ext(m, SLOT_X_F16, s);
       HX_HIP(launch_x_to_f16(p.ea, s));
       tm_ext_done(m, SLOT_X_F16);
     }
-    if ((rc = run_router(m, p, s))) return rc;
+    if ((rc = run_router(m, p, s, xh_in_router ? p.ea.xh : nullptr))) return rc;
     if (split) {
       ExpertArgs sa = p.ea;
       sa.tsel = HX_TILES_SHARED;

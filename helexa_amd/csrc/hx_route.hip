@@ -175,7 +175,17 @@ __global__ __launch_bounds__(256) void k_disp_hist(DispatchArgs a) {
   for (int e = threadIdx.x; e < E; e += 256) cnt[e] = 0;
   __syncthreads();
   const int f0 = b * HX_DISPATCH_CHUNK, f1 = min(a.F, f0 + HX_DISPATCH_CHUNK);
-  for (int f = f0 + threadIdx.x; f < f1; f += 256) atomicAdd(&cnt[a.topk_idx[f]], 1);
+  // all of this thread's loads before the first atomic
+  constexpr int PER = HX_DISPATCH_CHUNK / 256;
+  int ev[PER];
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int f = f0 + threadIdx.x + 256 * i;
+    ev[i] = f < f1 ? a.topk_idx[f] : -1;
+  }
+#pragma unroll
+  for (int i = 0; i < PER; i++)
+    if (ev[i] >= 0) atomicAdd(&cnt[ev[i]], 1);
   __syncthreads();
   for (int e = threadIdx.x; e < E; e += 256) a.hist[(int64_t)b * E + e] = cnt[e];
 }
@@ -280,7 +290,8 @@ __global__ __launch_bounds__(1024) void k_disp_scan(DispatchArgs a) {
 // (from a per-wave histogram), then 64 entries at a time in order, the rank of
 // an entry among the equal experts of its 64 from bitwise ballots. Each wave
 // keeps its own running bases, so the waves never wait for each other after
-// the bases are set.
+// the bases are set. A wave's experts and weights are loaded into registers
+// before anything else (one memory round trip).
 __global__ __launch_bounds__(256) void k_disp_scatter(DispatchArgs a) {
   constexpr int NWV = 4, SUB = HX_DISPATCH_CHUNK / NWV;
   __shared__ int wbase[NWV][HX_MAX_EXPERTS];
@@ -293,7 +304,18 @@ __global__ __launch_bounds__(256) void k_disp_scatter(DispatchArgs a) {
   __syncthreads();
   const int f0 = b * HX_DISPATCH_CHUNK, f1 = min(a.F, f0 + HX_DISPATCH_CHUNK);
   const int s0 = min(f1, f0 + SUB * wave), s1 = min(f1, s0 + SUB);
-  for (int f = s0 + lane; f < s1; f += 64) atomicAdd(&wbase[wave][a.topk_idx[f]], 1);
+  constexpr int PER = SUB / 64;
+  int ev[PER];
+  float wv[PER];
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int f = s0 + lane + 64 * i;
+    ev[i] = f < s1 ? a.topk_idx[f] : -1;
+    wv[i] = f < s1 && a.wpos ? a.topk_w[f] : 0.0f;
+  }
+#pragma unroll
+  for (int i = 0; i < PER; i++)
+    if (ev[i] >= 0) atomicAdd(&wbase[wave][ev[i]], 1);
   __syncthreads();
   for (int e = tid; e < E; e += 256) {
     int run = a.hist[(int64_t)b * E + e];
@@ -308,10 +330,12 @@ __global__ __launch_bounds__(256) void k_disp_scatter(DispatchArgs a) {
   const int nbits = 32 - __clz(E);
   const unsigned long long lt = (1ull << lane) - 1ull;
   int* base = wbase[wave];
-  for (int g = s0; g < s1; g += 64) {
-    const int f = g + lane;
+#pragma unroll
+  for (int i = 0; i < PER; i++) {
+    const int f = s0 + lane + 64 * i;
+    if (s0 + 64 * i >= s1) break;   // wave-uniform
     const bool valid = f < s1;
-    const int e = valid ? a.topk_idx[f] : 0;
+    const int e = valid ? ev[i] : 0;
     unsigned long long mask = __ballot(valid);
     for (int bit = 0; bit < nbits; bit++) {
       const int v = (e >> bit) & 1;
@@ -323,7 +347,7 @@ __global__ __launch_bounds__(256) void k_disp_scatter(DispatchArgs a) {
       const int pos = base[e] + rank;
       a.perm[pos] = f;
       if (a.inv) a.inv[f] = pos;
-      if (a.wpos) a.wpos[pos] = a.topk_w[f];
+      if (a.wpos) a.wpos[pos] = wv[i];
     }
     __builtin_amdgcn_wave_barrier();   // every lane has read base[] before the leaders move it
     if (valid && rank == 0) base[e] += cnt;
@@ -426,13 +450,13 @@ void launch_route_tokens(const RouterArgs& a, hipStream_t s) {
 #undef RT
 }
 
-void launch_dispatch(const DispatchArgs& d, hipStream_t s) {
+void launch_dispatch(const DispatchArgs& d, hipStream_t s, bool hist_ready) {
   const int nb = dispatch_blocks(d.F);
   if (nb <= 1 || !d.hist || d.E > 1024) {
     hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, d);
     return;
   }
-  hipLaunchKernelGGL(k_disp_hist, dim3(nb), dim3(256), 0, s, d);
+  if (!hist_ready) hipLaunchKernelGGL(k_disp_hist, dim3(nb), dim3(256), 0, s, d);
   hipLaunchKernelGGL(k_disp_scan, dim3(1), dim3(1024), 0, s, d);
   hipLaunchKernelGGL(k_disp_scatter, dim3(nb), dim3(256), 0, s, d);
 }

@@ -71,16 +71,25 @@ constexpr int RM_AHEAD = 8;
 // rows a fragment read touches then fall in 16 distinct bank groups. The K
 // loop is unrolled (NST is a template argument), so the compiler's waits
 // count exactly the loads in flight.
+//
+// Two jobs ride along (each a null pointer when not wanted): the workgroups of
+// expert block 0 write the f16 copy of the tokens the MFMA expert kernels read
+// (xh: each group of 8 elements converted exactly and stored in the swizzled
+// order (e0,e2)(e1,e3)(e4,e6)(e5,e7) at its own place), and the per-chunk
+// dispatch histogram the routing kernel fills is cleared (nhist ints).
 template <int NST>
 __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict__ x, const uint16_t* __restrict__ R,
-                                                     int T, int E, int E1, float* __restrict__ m) {
+                                                     int T, int E, int E1, float* __restrict__ m,
+                                                     uint16_t* __restrict__ xh, int32_t* __restrict__ hist, int nhist) {
   constexpr int H = 64 * NST;
   static_assert(NST % 2 == 0, "K steps come in pairs");
   __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][64 * 128];   // [buffer][A / B][row * 128 + slot * 16]
   const int NX = gridDim.x, L = blockIdx.y * NX + blockIdx.x;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  if (hist)
+    for (int i = L * 256 + tid; i < nhist; i += NX * gridDim.y * 256) hist[i] = 0;
   const int eb = (L >> 3) % NX, tb = (L / (8 * NX)) * 8 + (L & 7);
   if (tb * 64 >= T) return;   // whole workgroups
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   // loads: this thread's two 16-byte slots of each operand tile per step
   // (slot u = q * 256 + tid: row u / 8, 16-byte slot u % 8) as buffer loads
   // (a 32-bit byte offset and the step's scalar offset) from descriptors over
@@ -106,11 +115,34 @@ __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict_
       st[b][1][q] = __builtin_amdgcn_raw_buffer_load_b128(rsb, goff[1][q], step * 128, 0);
     }
   };
-  auto store = [&](int b, int buf) {
+  const bool wxh = xh && eb == 0;
+  auto store = [&](int b, int buf, int step) {
 #pragma unroll
     for (int o = 0; o < 2; o++)
 #pragma unroll
       for (int q = 0; q < 2; q++) *(u32x4_t*)(&lds[buf][o][soff[q]]) = st[b][o][q];
+    if (wxh) {
+#pragma unroll
+      for (int q = 0; q < 2; q++) {
+        const int u = q * 256 + tid, r = u >> 3, sl = u & 7;
+        if (r < nrows) {
+          const u32x4_t v = st[b][0][q];
+          uint32_t h[4];
+#pragma unroll
+          for (int j2 = 0; j2 < 4; j2++) {
+            const _Float16 lo16 = (_Float16)__uint_as_float(v[j2] << 16);
+            const _Float16 hi16 = (_Float16)__uint_as_float(v[j2] & 0xffff0000u);
+            h[j2] = (uint32_t)__builtin_bit_cast(uint16_t, lo16) | ((uint32_t)__builtin_bit_cast(uint16_t, hi16) << 16);
+          }
+          u32x4_t o;
+          o[0] = __builtin_amdgcn_perm(h[1], h[0], 0x05040100u);
+          o[1] = __builtin_amdgcn_perm(h[1], h[0], 0x07060302u);
+          o[2] = __builtin_amdgcn_perm(h[3], h[2], 0x05040100u);
+          o[3] = __builtin_amdgcn_perm(h[3], h[2], 0x07060302u);
+          *(u32x4_t*)(xh + ((int64_t)tb * 64 + r) * H + 64 * step + 8 * sl) = o;
+        }
+      }
+    }
   };
   // fragment reads: row rowbase + l % 16, logical slot c * 4 + l / 16
   const int r16 = lane & 15, kq = lane >> 4;
@@ -155,13 +187,13 @@ __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict_
   constexpr int NB = RM_AHEAD + 1;
 #pragma unroll
   for (int s = 0; s < RM_AHEAD && s < NST; s++) load(s, s);
-  store(0, 0);
+  store(0, 0, 0);
   __syncthreads();
 #pragma unroll
   for (int s = 0; s < NST; s++) {
     // slot (s + RM_AHEAD) % NB last held step s - 1, stored to LDS before now
     if (s + RM_AHEAD < NST) load(s + RM_AHEAD, (s + RM_AHEAD) % NB);
-    if (s + 1 < NST) store((s + 1) % NB, (s + 1) & 1);
+    if (s + 1 < NST) store((s + 1) % NB, (s + 1) & 1, s + 1);
     compute(s & 1);
     __syncthreads();
   }
@@ -434,8 +466,11 @@ __global__ __launch_bounds__(256) void k_route_mfma(RouterArgs a) {
     route_token_regs<EPL>(v, mx, k, a.norm, out_e, out_w);
   }
   if (lane < k) {
-    a.d.topk_idx[(int64_t)t * k + lane] = out_e;
-    a.topk_w[(int64_t)t * k + lane] = out_w;
+    const int64_t f = (int64_t)t * k + lane;
+    a.d.topk_idx[f] = out_e;
+    a.topk_w[f] = out_w;
+    // the dispatch histogram of entry f's chunk (cleared by k_router_mfma)
+    if (a.d.hist && dispatch_blocks(a.d.F) > 1) atomicAdd(&a.d.hist[(f / HX_DISPATCH_CHUNK) * E + out_e], 1);
   }
   if (a.has_shared && lane == 0) a.sgw[t] = sigmoidf_(lsh);
 }
@@ -462,13 +497,15 @@ bool route_mfma_ok(const RouterArgs& a, bool xbf, bool rbf) {
          a.E >= 1 && a.E <= 1024 && a.k >= 1 && a.k <= 64 && a.k <= a.E;
 }
 
-void launch_router_mfma(const RouterArgs& a, hipStream_t s) {
+void launch_router_mfma(const RouterArgs& a, uint16_t* xh, hipStream_t s) {
+  int32_t* hist = a.d.hist && dispatch_blocks(a.d.F) > 1 ? a.d.hist : nullptr;
+  const int nhist = hist ? dispatch_blocks(a.d.F) * a.E : 0;
   const int NX = (a.E + 63) / 64;
   const dim3 grid(NX, ((a.T + 63) / 64 + 7) / 8 * 8);
 #define RM(N)                                                                                                   \
   case N:                                                                                                       \
     hx_launch(k_router_mfma<2 * N>, grid, dim3(256), 0, s, (const uint16_t*)a.x, (const uint16_t*)a.R, a.T, a.E, a.E1, \
-              a.logits);                                                                                        \
+              a.logits, xh, hist, nhist);                                                                       \
     break;
   switch (a.H / (32 * RM_GROUP)) {
     RM(1) RM(2) RM(3) RM(4) RM(6) RM(8) RM(12) RM(16) RM(24) RM(32)
