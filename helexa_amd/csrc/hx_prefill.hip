@@ -289,8 +289,10 @@ struct Q4k {
   static constexpr int NA = 1024 / NT;                   // A DMA rounds
   static constexpr int BPIECES = 5 * BROWS;              // 16-byte pieces of B per chunk
   static constexpr int NBI = (BPIECES + NT - 1) / NT;    // B DMA rounds
-  // DMA instructions per chunk of wave w
-  HX_DEV static int per_wave(int w) { return NA + (BPIECES - NT * (NBI - 1) > 64 * w ? NBI : NBI - 1); }
+  // DMA instructions per chunk of wave w for a tile of MT sub-tiles
+  HX_DEV static int per_wave(int w, int MT) {
+    return (MT < NA ? MT : NA) + (BPIECES - NT * (NBI - 1) > 64 * w ? NBI : NBI - 1);
+  }
 };
 
 // Per-thread DMA sources of chunk 0; chunk kc adds 256 kc bytes to the A
@@ -326,12 +328,14 @@ HX_DEV Q4kSrc<Q> q4k_sources(const uint16_t* xh, int H, const int* rowsrc, const
   return src;
 }
 
-// DMA of chunk kc into stage st
-template <class Q>
+// DMA of chunk kc into stage st; A round i moves token rows 16 i .. 16 i + 15
+// (sub-tile i), so a tile of MT sub-tiles needs the first MT rounds only
+template <class Q, int MT>
 HX_DEV void q4k_issue(uint32_t lds0, int st, const Q4kSrc<Q>& src, int kc, int wave_u) {
+  static_assert(Q::NT == 256, "A round i = rows 16 i .. 16 i + 15");
   const uint32_t sbase = lds0 + (uint32_t)(st * Q::STAGE + wave_u * 64 * 16);
 #pragma unroll
-  for (int i = 0; i < Q::NA; i++) dma16(src.a[i] + 256 * kc, sbase + (uint32_t)(i * Q::NT * 16));
+  for (int i = 0; i < (MT < Q::NA ? MT : Q::NA); i++) dma16(src.a[i] + 256 * kc, sbase + (uint32_t)(i * Q::NT * 16));
   const int hdr_off = (kc >> 1) * 144, qs_off = hdr_off + 64 * (kc & 1);
 #pragma unroll
   for (int i = 0; i < Q::NBI; i++) {
@@ -422,10 +426,11 @@ HX_DEV void q4k_compute(const lds_u8* st, f32x4_t (*accg)[Q::FPW_], f32x4_t (*ac
 
 // wait until at most `ahead` chunks of this wave's DMAs are outstanding;
 // `ahead` and the count are wave-uniform, so the branches are scalar
-template <class Q>
+template <class Q, int MT>
 HX_DEV void q4k_wait(int ahead, int wave_u) {
-  const int n = ahead * Q::per_wave(wave_u);
-  switch (n) {
+  const int n = ahead * Q::per_wave(wave_u, MT);
+  switch (n) {   // counts not listed wait for everything (correct, only later)
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
     case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
     case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
     case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
@@ -439,9 +444,7 @@ HX_DEV void q4k_wait(int ahead, int wave_u) {
 }
 
 // the K loop and epilogue of k_gate_up_q4k for tiles of at most 16 MT rows:
-// MFMAs and activation-fragment reads only for the sub-tiles in use (the DMAs
-// still move all 64 rows, so every wave's DMA count, which the waits rely on,
-// does not depend on the tile)
+// DMAs, activation-fragment reads and MFMAs only for the sub-tiles in use
 template <class Q, int MT>
 HX_DEV void q4k_main(const ExpertArgs& a, uint8_t* ring, const Q4kSrc<Q>& src, int nk, int rows, int p0, int n0,
                      int wave, int wave_u, int l16, int kq, uint32_t knib, uint32_t kbyte, uint32_t kmagic) {
@@ -457,12 +460,12 @@ HX_DEV void q4k_main(const ExpertArgs& a, uint8_t* ring, const Q4kSrc<Q>& src, i
     }
 #pragma unroll
   for (int c = 0; c < Q::NST - 1; c++)
-    if (c < nk) q4k_issue<Q>(lds0, c, src, c, wave_u);
+    if (c < nk) q4k_issue<Q, MT>(lds0, c, src, c, wave_u);
   for (int kc = 0; kc < nk; kc++) {
     const int ahead = min(Q::NST - 2, nk - 1 - kc);
-    q4k_wait<Q>(ahead, wave_u);
+    q4k_wait<Q, MT>(ahead, wave_u);
     __syncthreads();   // chunk kc is in LDS for every wave; stage (kc - 1) % NST is free
-    if (kc + Q::NST - 1 < nk) q4k_issue<Q>(lds0, (kc + Q::NST - 1) % Q::NST, src, kc + Q::NST - 1, wave_u);
+    if (kc + Q::NST - 1 < nk) q4k_issue<Q, MT>(lds0, (kc + Q::NST - 1) % Q::NST, src, kc + Q::NST - 1, wave_u);
     const lds_u8* st = (const lds_u8*)ring + (kc % Q::NST) * Q::STAGE;
     if (kc & 1) q4k_compute<Q, 1, MT>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
     else q4k_compute<Q, 0, MT>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
