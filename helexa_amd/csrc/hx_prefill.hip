@@ -605,13 +605,15 @@ HX_DEV DqSrc dq_sources(const uint16_t* hbf, int hstride, int p0, int rows, cons
   return src;
 }
 
-// 5 DMA instructions per wave and chunk
+// NA + 3 DMA instructions per wave and chunk: A round i moves rows
+// 32 i .. 32 i + 31 of h, so tiles of at most 32 rows (NA = 1) skip round 1
+template <int NA>
 HX_DEV void dq_issue(uint32_t lds0, int st, const DqSrc& src, int c, int wave_u) {
   const uint32_t sbase = lds0 + (uint32_t)(st * DQ_STAGE);
   const int sb = c >> 2, n = (c >> 1) & 1;
   const int aoff = 2 * dq_col(c), qloff = 128 * sb + 64 * n + 32 * (c & 1), qhoff = 64 * sb + 32 * n;
 #pragma unroll
-  for (int i = 0; i < 2; i++) dma16(src.a[i] + aoff, sbase + (uint32_t)(i * 4096 + wave_u * 1024));
+  for (int i = 0; i < NA; i++) dma16(src.a[i] + aoff, sbase + (uint32_t)(i * 4096 + wave_u * 1024));
 #pragma unroll
   for (int i = 0; i < 2; i++)
     dma16(src.b[i] + ((src.bqh >> i) & 1 ? qhoff : qloff), sbase + (uint32_t)(DQ_A + i * 4096 + wave_u * 1024));
@@ -661,15 +663,16 @@ HX_DEV void dq_compute(const lds_u8* st, const uint16_t* dl, int sb, f32x4_t (*a
 }
 
 // grid (H / 128, tiles rounded up to 8), mapped by xcd_tile
-// the K loop and epilogue of k_down_q6k for tiles of at most 16 MT rows (MFMAs
-// and activation-fragment reads for the sub-tiles in use; DMAs unchanged)
+// the K loop and epilogue of k_down_q6k for tiles of at most 16 MT rows (MFMAs,
+// activation-fragment reads and A DMA rounds for the sub-tiles in use)
 template <int MT>
 HX_DEV void dq_main(const ExpertArgs& a, uint8_t* ring, float* rws, const DqSrc& src, float rw, int rows, int p0,
                     int n0, int wave, int wave_u, int l16, int kq) {
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)ring;
   const uint16_t* dl = (const uint16_t*)(ring + DQ_NST * DQ_STAGE);
+  constexpr int NA = MT <= 2 ? 1 : 2;   // A rounds (32 rows each) the tile needs
 #pragma unroll
-  for (int c = 0; c < DQ_NST - 1; c++) dq_issue(lds0, c, src, c, wave_u);
+  for (int c = 0; c < DQ_NST - 1; c++) dq_issue<NA>(lds0, c, src, c, wave_u);
   const uint32_t knib = __builtin_amdgcn_readfirstlane(0x000F000Fu), k30 = __builtin_amdgcn_readfirstlane(0x00300030u);
   uint32_t kmagic;
   asm("v_mov_b32 %0, 0x64006400" : "=v"(kmagic));
@@ -680,11 +683,15 @@ HX_DEV void dq_main(const ExpertArgs& a, uint8_t* ring, float* rws, const DqSrc&
     for (int i = 0; i < MT; i++) acc[j][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   for (int c = 0; c < DQ_NC; c++) {
     // chunk c (and, before chunk 0, the d dwords) has landed once at most the
-    // 5 DMAs of chunk c + 1 are outstanding
-    if (c + 1 < DQ_NC) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // NA + 3 DMAs of chunk c + 1 are outstanding
+    if (c + 1 < DQ_NC) {
+      if (NA == 1) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+      else asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+    } else {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    }
     __syncthreads();   // chunk c is in LDS for every wave; stage (c - 1) % NST is free
-    if (c + DQ_NST - 1 < DQ_NC) dq_issue(lds0, (c + DQ_NST - 1) % DQ_NST, src, c + DQ_NST - 1, wave_u);
+    if (c + DQ_NST - 1 < DQ_NC) dq_issue<NA>(lds0, (c + DQ_NST - 1) % DQ_NST, src, c + DQ_NST - 1, wave_u);
     const lds_u8* st = (const lds_u8*)ring + (c % DQ_NST) * DQ_STAGE;
     if (c & 1) dq_compute<1, MT>(st, dl, c >> 2, acc, wave, l16, kq, knib, kmagic, k30);
     else dq_compute<0, MT>(st, dl, c >> 2, acc, wave, l16, kq, knib, kmagic, k30);
