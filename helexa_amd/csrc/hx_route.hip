@@ -190,75 +190,116 @@ __global__ __launch_bounds__(256) void k_disp_hist(DispatchArgs a) {
   for (int e = threadIdx.x; e < E; e += 256) a.hist[(int64_t)b * E + e] = cnt[e];
 }
 
-// exclusive scan of one value per thread over a 1024-thread block; *total gets
-// the sum (sh: 17 ints of LDS)
-HX_DEV int block_scan_1024(int v, int* sh, int* total) {
+// exclusive scans of three values per thread over a 1024-thread block in one
+// pass (three barriers); tot[i] gets the sums (sh: 3 x 17 ints of LDS)
+HX_DEV void block_scan3_1024(const int (&v)[3], int (&r)[3], int (&tot)[3], int (*sh)[17]) {
   const int lane = lane_id(), wave = threadIdx.x >> 6;
-  int x = v;
+  int x[3] = {v[0], v[1], v[2]};
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    const int y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const int y = __shfl_up(x[i], off, 64);
+      if (lane >= off) x[i] += y;
+    }
   }
-  if (lane == 63) sh[wave] = x;
+  if (lane == 63)
+#pragma unroll
+    for (int i = 0; i < 3; i++) sh[i][wave] = x[i];
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (threadIdx.x < 3) {
     int run = 0;
     for (int w = 0; w < 16; w++) {
-      const int c = sh[w];
-      sh[w] = run;
+      const int c = sh[threadIdx.x][w];
+      sh[threadIdx.x][w] = run;
       run += c;
     }
-    sh[16] = run;
+    sh[threadIdx.x][16] = run;
   }
   __syncthreads();
-  const int r = sh[wave] + x - v;
-  *total = sh[16];
-  __syncthreads();
-  return r;
+#pragma unroll
+  for (int i = 0; i < 3; i++) {
+    r[i] = sh[i][wave] + x[i] - v[i];
+    tot[i] = sh[i][16];
+  }
 }
 
+// k_disp_scan: one block, thread e = expert e. The per-block bases are
+// written once (prefix over blocks + the expert's offset) when the block
+// count is at most SCAN_REG (registers), else in a second pass; the M tiles
+// are written in parallel, tile i's expert found by an upper-bound search
+// over the experts' first tiles (experts without tiles share the next one's
+// first tile, so the largest e with first[e] <= i is the owner).
+constexpr int SCAN_REG = 32;
 __global__ __launch_bounds__(1024) void k_disp_scan(DispatchArgs a) {
-  __shared__ int sh[17];
+  __shared__ int sh[3][17];
+  __shared__ int s_first[HX_MAX_EXPERTS], s_slot[HX_MAX_EXPERTS], s_off[HX_MAX_EXPERTS], s_cnt[HX_MAX_EXPERTS];
   const int e = threadIdx.x, E = a.E, nb = dispatch_blocks(a.F);
   int count = 0;
+  int pre[SCAN_REG];   // entries of e in blocks before b (nb <= SCAN_REG)
   if (e < E) {
-    // the expert's per-block counts, PB at a time: all loads of a batch
-    // issued before the first is used (one memory round trip per batch)
-    constexpr int PB = 16;
-    for (int b0 = 0; b0 < nb; b0 += PB) {
-      int h[PB];
+    if (nb <= SCAN_REG) {
+      int h[SCAN_REG];
 #pragma unroll
-      for (int i = 0; i < PB; i++) h[i] = b0 + i < nb ? a.hist[(int64_t)(b0 + i) * E + e] : 0;
+      for (int i = 0; i < SCAN_REG; i++) h[i] = i < nb ? a.hist[(int64_t)i * E + e] : 0;
 #pragma unroll
-      for (int i = 0; i < PB; i++) {
-        if (b0 + i < nb) a.hist[(int64_t)(b0 + i) * E + e] = count;
+      for (int i = 0; i < SCAN_REG; i++) {
+        pre[i] = count;
         count += h[i];
+      }
+    } else {
+      // the expert's per-block counts, PB at a time: all loads of a batch
+      // issued before the first is used (one memory round trip per batch)
+      constexpr int PB = 16;
+      for (int b0 = 0; b0 < nb; b0 += PB) {
+        int h[PB];
+#pragma unroll
+        for (int i = 0; i < PB; i++) h[i] = b0 + i < nb ? a.hist[(int64_t)(b0 + i) * E + e] : 0;
+#pragma unroll
+        for (int i = 0; i < PB; i++) {
+          if (b0 + i < nb) a.hist[(int64_t)(b0 + i) * E + e] = count;
+          count += h[i];
+        }
       }
     }
   }
-  int tot;
-  const int off = block_scan_1024(e < E ? count : 0, sh, &tot);
-  const int slot = block_scan_1024(e < E && count > 0 ? 1 : 0, sh, &tot);
-  const int nslot = tot;
-  const int ntile_e = e < E ? (count + a.tile_m - 1) / a.tile_m : 0;
-  const int tile0 = block_scan_1024(ntile_e, sh, &tot);
-  const int ntile = tot;
+  const int in[3] = {e < E ? count : 0, e < E && count > 0 ? 1 : 0, e < E ? (count + a.tile_m - 1) / a.tile_m : 0};
+  int ex[3], tot[3];
+  block_scan3_1024(in, ex, tot, sh);
+  const int off = ex[0], slot = ex[1], nslot = tot[1], ntile = tot[2];
   if (e < E) {
     a.offsets[e] = off;
+    s_first[e] = ex[2];
+    s_slot[e] = slot;
+    s_off[e] = off;
+    s_cnt[e] = count;
     // per-block bases: offsets[e] + entries of e in earlier blocks
-    for (int b = 0; b < nb; b++) a.hist[(int64_t)b * E + e] += off;
+    if (nb <= SCAN_REG) {
+#pragma unroll
+      for (int i = 0; i < SCAN_REG; i++)
+        if (i < nb) a.hist[(int64_t)i * E + e] = pre[i] + off;
+    } else {
+      for (int b = 0; b < nb; b++) a.hist[(int64_t)b * E + e] += off;
+    }
     if (count > 0) {
       a.slots[3 * slot + 0] = e;
       a.slots[3 * slot + 1] = off;
       a.slots[3 * slot + 2] = count;
-      for (int m0 = 0, i = 0; m0 < count; m0 += a.tile_m, i++) {
-        a.tiles[4 * (tile0 + i) + 0] = slot;
-        a.tiles[4 * (tile0 + i) + 1] = e;
-        a.tiles[4 * (tile0 + i) + 2] = off + m0;
-        a.tiles[4 * (tile0 + i) + 3] = count - m0 < a.tile_m ? count - m0 : a.tile_m;
-      }
     }
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < ntile; t += 1024) {
+    int lo = 0, hi = E - 1;   // the largest e with s_first[e] <= t
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_first[mid] <= t) lo = mid;
+      else hi = mid - 1;
+    }
+    const int m0 = (t - s_first[lo]) * a.tile_m, c = s_cnt[lo];
+    a.tiles[4 * t + 0] = s_slot[lo];
+    a.tiles[4 * t + 1] = lo;
+    a.tiles[4 * t + 2] = s_off[lo] + m0;
+    a.tiles[4 * t + 3] = c - m0 < a.tile_m ? c - m0 : a.tile_m;
   }
   if (e == 0) a.offsets[E] = a.F;
   int ns = nslot, nt = ntile;
@@ -298,6 +339,14 @@ __global__ __launch_bounds__(256) void k_disp_scatter(DispatchArgs a) {
   const int b = blockIdx.x, E = a.E, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
   if (b == 0 && a.wpos && a.has_shared)
     for (int t = tid; t < a.T; t += 256) a.wpos[a.F + t] = a.sgw[t];
+  // this block's per-expert bases, loaded before anything waits on memory
+  constexpr int EPT = HX_MAX_EXPERTS / 256;
+  int bb[EPT];
+#pragma unroll
+  for (int i = 0; i < EPT; i++) {
+    const int e = tid + 256 * i;
+    bb[i] = e < E ? a.hist[(int64_t)b * E + e] : 0;
+  }
   for (int e = tid; e < E; e += 256)
 #pragma unroll
     for (int w = 0; w < NWV; w++) wbase[w][e] = 0;
@@ -317,8 +366,11 @@ __global__ __launch_bounds__(256) void k_disp_scatter(DispatchArgs a) {
   for (int i = 0; i < PER; i++)
     if (ev[i] >= 0) atomicAdd(&wbase[wave][ev[i]], 1);
   __syncthreads();
-  for (int e = tid; e < E; e += 256) {
-    int run = a.hist[(int64_t)b * E + e];
+#pragma unroll
+  for (int i = 0; i < EPT; i++) {
+    const int e = tid + 256 * i;
+    if (e >= E) break;
+    int run = bb[i];
 #pragma unroll
     for (int w = 0; w < NWV; w++) {
       const int c = wbase[w][e];
