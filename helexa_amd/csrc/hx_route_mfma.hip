@@ -405,9 +405,9 @@ __global__ __launch_bounds__(256) void k_route_mfma(RouterArgs a) {
     const float li = lane < nc ? sm.cl[wave][lane] : -__builtin_inff();
     const int ei = lane < nc ? sm.ce[wave][lane] : 0x7fffffff;
     int rank = 0;
-    for (int j = 0; j < nc; j++) {
-      const float lj = __shfl(li, j, 64);
-      const int ej = __shfl(ei, j, 64);
+    for (int j = 0; j < nc; j++) {   // wave-uniform j: readlane, not a permute through LDS
+      const float lj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(li), j));
+      const int ej = __builtin_amdgcn_readlane(ei, j);
       rank += (lj > li || (lj == li && ej < ei)) ? 1 : 0;
     }
     if (lane < nc) {
@@ -435,7 +435,7 @@ __global__ __launch_bounds__(256) void k_route_mfma(RouterArgs a) {
     ok = __all(good);
     if (ok) {
       float tot = 0.0f;
-      for (int r = 0; r < k; r++) tot = tot + __shfl(ex, r, 64);
+      for (int r = 0; r < k; r++) tot = tot + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ex), r));
       out_e = er;
       out_w = ex / tot;
     }
