@@ -265,8 +265,9 @@ def cpu_baseline_c2(cfg, host0, x0, runs=50):
 
 # the routed gate/up launch is the dominant prefill kernel; the shared expert's
 # GEMMs are separate launches (template argument 2) on the handle's side stream
-PREFILL_KERNELS = {"gate_up": "k_gate_up_q4k<1, 4, 1>", "down": "k_down_q6k<1>", "router": "k_router88",
-                   "shared_gate_up": "k_gate_up_q4k<1, 4, 2>", "shared_down": "k_down_q6k<2>"}
+PREFILL_KERNELS = {"gate_up": "k_gate_up_q4k<1, 4, 1>", "down": "k_down_q6k<1>", "router": "k_router_mfma",
+                   "route_tokens": "k_route_mfma", "shared_gate_up": "k_gate_up_q4k<1, 4, 2>",
+                   "shared_down": "k_down_q6k<2>"}
 
 
 def prefill_work(cfg, fmts, T, U):
@@ -280,11 +281,13 @@ def prefill_work(cfg, fmts, T, U):
     F = T * k
     gu_w, sgu_w = U * 2 * gguf_bytes(fmts["gate"], I, H), 2 * gguf_bytes(fmts["sgate"], Is, H)
     dn_w, sdn_w = U * gguf_bytes(fmts["down"], H, I), gguf_bytes(fmts["sdown"], H, Is)
+    # router: the MFMA logits of the E routed experts over bf16 tokens, which
+    # also writes the f16 copy of the tokens the expert kernels read
     flops = {"gate_up": 2 * F * 2 * H * I, "down": 2 * F * H * I, "shared_gate_up": 2 * T * 2 * H * Is,
-             "shared_down": 2 * T * H * Is, "router": 2 * T * H * (E + 1)}
+             "shared_down": 2 * T * H * Is, "router": 2 * T * H * E}
     kbytes = {"gate_up": gu_w + T * H * 2 + F * I * 2, "down": dn_w + F * I * 2 + F * H * 2,
               "shared_gate_up": sgu_w + T * H * 2 + T * Is * 2, "shared_down": sdn_w + T * Is * 2 + T * H * 2,
-              "router": (E + 1) * H * 2 + T * H * 2}
+              "router": E * H * 2 + T * H * 2 + T * H * 2}
     total_flops = 2 * T * k * 3 * H * I + 2 * T * 3 * H * Is + 2 * T * H * E
     total_bytes = gu_w + sgu_w + dn_w + sdn_w + (E + 1) * H * 2 + 2 * T * H * 2
     return total_flops, total_bytes, flops, kbytes
