@@ -82,7 +82,13 @@ struct RouterArgs {
   // |r_e| rounded up, per router row (bf16 router rows): the MFMA prefill
   // routing bounds each logit with it
   const float* rnorm = nullptr;
+  // MFMA prefill routing: logit planes (split K) the routing kernel adds;
+  // plane 0 is `logits`, plane z >= 1 at mplanes + (z - 1) T (E + 1)
+  int msplit = 1;
+  float* mplanes = nullptr;
 };
+// most logit planes of the MFMA prefill router
+#define HX_RM_SPLITS 4
 
 // One projection stack: E matrices of [rows][K] in the internal layout.
 struct WMat {
@@ -155,9 +161,10 @@ void launch_dispatch(const DispatchArgs& d, hipStream_t s, bool hist_ready = fal
 // prefill routing with the router GEMM on MFMA (bf16 tokens and router rows,
 // renormalised top-k): approximate logits, then per token the exact top-k
 bool route_mfma_ok(const RouterArgs& a, bool xbf, bool rbf);
+int route_mfma_splits(const RouterArgs& a);
 // also writes the f16 tokens for the MFMA expert kernels when xh is not null,
 // and clears the dispatch histogram that launch_route_mfma fills
-void launch_router_mfma(const RouterArgs& a, uint16_t* xh, hipStream_t s);
+hipError_t launch_router_mfma(const RouterArgs& a, uint16_t* xh, hipStream_t s);
 void launch_route_mfma(const RouterArgs& a, hipStream_t s);
 hipError_t launch_row_norms(const void* R, int E1, int H, float* out, hipStream_t s);
 

@@ -417,6 +417,10 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
   r.has_shared = c.shared_expert_intermediate_size > 0;
   r.bias = bias;
   r.rnorm = m->rnorm;
+  // logit planes 1.. of the MFMA router live at the start of the weighted-rows
+  // buffer, which nothing writes before the down kernels (the shared expert's
+  // rows, written beside the routing, start at row F, far past them)
+  r.mplanes = L.obuf ? (float*)(ws + L.obuf) : nullptr;
   r.logits = (float*)(ws + L.logits);
   r.topk_w = (float*)(ws + L.topk_w);
   r.sgw = (float*)(ws + L.sgw);
@@ -524,7 +528,7 @@ static bool route_mfma(const hx_moe* m, const Plan& p) {
 static int run_router(hx_moe* m, Plan& p, hipStream_t s, uint16_t* xh = nullptr) {
   const bool xbf = m->cfg.act_dtype == HX_BF16, rbf = m->rdt == HX_BF16;
   tm_ext(m, SLOT_ROUTER, s);
-  if (route_mfma(m, p)) launch_router_mfma(p.ra, xh, s);
+  if (route_mfma(m, p)) HX_HIP(launch_router_mfma(p.ra, xh, s));
   else launch_router(p.ra, xbf, rbf, s);
   tm_ext_done(m, SLOT_ROUTER);
   HX_HIP(hipGetLastError());

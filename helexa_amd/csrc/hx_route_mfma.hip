@@ -72,24 +72,37 @@ constexpr int RM_AHEAD = 8;
 // loop is unrolled (NST is a template argument), so the compiler's waits
 // count exactly the loads in flight.
 //
-// Two jobs ride along (each a null pointer when not wanted): the workgroups of
-// expert block 0 write the f16 copy of the tokens the MFMA expert kernels read
+// Two jobs ride along (each a null pointer when not wanted): the workgroups
+// write the f16 copy of the tokens the MFMA expert kernels read, K step s by
+// the workgroup of expert block s % (expert blocks)
 // (xh: each group of 8 elements converted exactly and stored in the swizzled
 // order (e0,e2)(e1,e3)(e4,e6)(e5,e7) at its own place), and the per-chunk
 // dispatch histogram the routing kernel fills is cleared (nhist ints).
+//
+// Split K: grid z = s < S takes K steps s NST .. s NST + NST - 1 (NST steps of
+// 64 per workgroup, H = 64 NST S) and writes its sums to logit plane s (plane
+// 0: m, plane s >= 1: mp + (s - 1) T E1); the routing kernel adds the planes
+// in order.
+// With S planes each running sum covers H / (32 S) chunks and the planes add
+// S - 1 roundings: fewer than the H / 32 of one running sum, so the bound
+// below holds as stated.
 template <int NST>
 __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict__ x, const uint16_t* __restrict__ R,
-                                                     int T, int E, int E1, float* __restrict__ m,
-                                                     uint16_t* __restrict__ xh, int32_t* __restrict__ hist, int nhist) {
-  constexpr int H = 64 * NST;
+                                                     int T, int H, int E, int E1, float* __restrict__ m,
+                                                     float* __restrict__ mp, uint16_t* __restrict__ xh,
+                                                     int32_t* __restrict__ hist, int nhist) {
   static_assert(NST % 2 == 0, "K steps come in pairs");
   __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][64 * 128];   // [buffer][A / B][row * 128 + slot * 16]
-  const int NX = gridDim.x, L = blockIdx.y * NX + blockIdx.x;
+  const int NX = gridDim.x, L = blockIdx.y * NX + blockIdx.x, z = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  if (hist)
-    for (int i = L * 256 + tid; i < nhist; i += NX * gridDim.y * 256) hist[i] = 0;
+  if (hist) {
+    const int nwg = NX * gridDim.y * gridDim.z, lz = z * NX * gridDim.y + L;
+    for (int i = lz * 256 + tid; i < nhist; i += nwg * 256) hist[i] = 0;
+  }
   const int eb = (L >> 3) % NX, tb = (L / (8 * NX)) * 8 + (L & 7);
   if (tb * 64 >= T) return;   // whole workgroups
+  const int ks0 = z * NST;     // this workgroup's first K step
+  if (z > 0) m = mp + (int64_t)(z - 1) * T * E1;
   // loads: this thread's two 16-byte slots of each operand tile per step
   // (slot u = q * 256 + tid: row u / 8, 16-byte slot u % 8) as buffer loads
   // (a 32-bit byte offset and the step's scalar offset) from descriptors over
@@ -111,17 +124,18 @@ __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict_
   auto load = [&](int step, int b) {
 #pragma unroll
     for (int q = 0; q < 2; q++) {
-      st[b][0][q] = __builtin_amdgcn_raw_buffer_load_b128(rsa, goff[0][q], step * 128, 0);
-      st[b][1][q] = __builtin_amdgcn_raw_buffer_load_b128(rsb, goff[1][q], step * 128, 0);
+      st[b][0][q] = __builtin_amdgcn_raw_buffer_load_b128(rsa, goff[0][q], (ks0 + step) * 128, 0);
+      st[b][1][q] = __builtin_amdgcn_raw_buffer_load_b128(rsb, goff[1][q], (ks0 + step) * 128, 0);
     }
   };
-  const bool wxh = xh && eb == 0;
   auto store = [&](int b, int buf, int step) {
 #pragma unroll
     for (int o = 0; o < 2; o++)
 #pragma unroll
       for (int q = 0; q < 2; q++) *(u32x4_t*)(&lds[buf][o][soff[q]]) = st[b][o][q];
-    if (wxh) {
+    // the f16 tokens of K step s are written by the token block's workgroup of
+    // expert block s % NX (every one of them loads every step of its K range)
+    if (xh && (ks0 + step) % NX == eb) {
 #pragma unroll
       for (int q = 0; q < 2; q++) {
         const int u = q * 256 + tid, r = u >> 3, sl = u & 7;
@@ -139,7 +153,7 @@ __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict_
           o[1] = __builtin_amdgcn_perm(h[1], h[0], 0x07060302u);
           o[2] = __builtin_amdgcn_perm(h[3], h[2], 0x05040100u);
           o[3] = __builtin_amdgcn_perm(h[3], h[2], 0x07060302u);
-          *(u32x4_t*)(xh + ((int64_t)tb * 64 + r) * H + 64 * step + 8 * sl) = o;
+          *(u32x4_t*)(xh + ((int64_t)tb * 64 + r) * H + 64 * (ks0 + step) + 8 * sl) = o;
         }
       }
     }
@@ -292,7 +306,9 @@ __global__ __launch_bounds__(256) void k_route_mfma(RouterArgs a) {
     const uint4 v = *(const uint4*)((const uint16_t*)a.x + (int64_t)t * H + 8 * g);
     xr[i][0] = v.x; xr[i][1] = v.y; xr[i][2] = v.z; xr[i][3] = v.w;
   }
+  // the MFMA logits: the sum of the split-K planes, in plane order
   const float* mrow = a.logits + (int64_t)t * a.E1;
+  const int64_t plane = (int64_t)a.T * a.E1;   // floats per logit plane
   float mv[EPL], nw[EPL], bv[EPL];
 #pragma unroll
   for (int j = 0; j < EPL; j++) {
@@ -300,6 +316,21 @@ __global__ __launch_bounds__(256) void k_route_mfma(RouterArgs a) {
     mv[j] = mrow[e];
     nw[j] = a.rnorm[e];
     bv[j] = a.bias ? a.bias[e] : 0.0f;
+  }
+  {
+    // every plane's loads first (one memory round trip), then the sums in plane order
+    float pv[HX_RM_SPLITS - 1][EPL];
+#pragma unroll
+    for (int z = 1; z < HX_RM_SPLITS; z++) {
+      const float* prow = a.mplanes + (z - 1) * plane + (int64_t)t * a.E1;
+#pragma unroll
+      for (int j = 0; j < EPL; j++) pv[z - 1][j] = z < a.msplit ? prow[min(lane + 64 * j, E - 1)] : 0.0f;
+    }
+#pragma unroll
+    for (int z = 1; z < HX_RM_SPLITS; z++)
+#pragma unroll
+      for (int j = 0; j < EPL; j++)
+        if (z < a.msplit) mv[j] = mv[j] + pv[z - 1][j];
   }
   // |x| from above: the f32 sum of squares is within 40 u of the exact one
   float ss = 0.0f;
@@ -497,25 +528,39 @@ bool route_mfma_ok(const RouterArgs& a, bool xbf, bool rbf) {
          a.E >= 1 && a.E <= 1024 && a.k >= 1 && a.k <= 64 && a.k <= a.E;
 }
 
-void launch_router_mfma(const RouterArgs& a, uint16_t* xh, hipStream_t s) {
+// K splits of the MFMA router (logit planes): HX_RM_SPLITS when the K steps
+// of 64 divide into that many runs of at least 4 and planes 1.. fit in front of
+// the shared expert's rows of the weighted-rows buffer (row F of bf16 rows of
+// H: 2 k H bytes per token), else 1
+int route_mfma_splits(const RouterArgs& a) {
+  const int nst = a.H / 64, S = HX_RM_SPLITS;
+  const bool fit = a.mplanes && (int64_t)4 * (S - 1) * a.E1 <= (int64_t)2 * a.k * a.H;
+  return nst % S == 0 && nst >= 4 * S && fit ? S : 1;
+}
+
+hipError_t launch_router_mfma(const RouterArgs& a, uint16_t* xh, hipStream_t s) {
   int32_t* hist = a.d.hist && dispatch_blocks(a.d.F) > 1 ? a.d.hist : nullptr;
   const int nhist = hist ? dispatch_blocks(a.d.F) * a.E : 0;
+  const int S = route_mfma_splits(a), nsw = a.H / 64 / S;
   const int NX = (a.E + 63) / 64;
-  const dim3 grid(NX, ((a.T + 63) / 64 + 7) / 8 * 8);
-#define RM(N)                                                                                                   \
-  case N:                                                                                                       \
-    hx_launch(k_router_mfma<2 * N>, grid, dim3(256), 0, s, (const uint16_t*)a.x, (const uint16_t*)a.R, a.T, a.E, a.E1, \
-              a.logits, xh, hist, nhist);                                                                       \
+  const dim3 grid(NX, ((a.T + 63) / 64 + 7) / 8 * 8, S);
+#define RM(N)                                                                                                    \
+  case N:                                                                                                        \
+    hx_launch(k_router_mfma<N>, grid, dim3(256), 0, s, (const uint16_t*)a.x, (const uint16_t*)a.R, a.T, a.H, a.E, \
+              a.E1, a.logits, a.mplanes, xh, hist, nhist);                                                       \
     break;
-  switch (a.H / (32 * RM_GROUP)) {
-    RM(1) RM(2) RM(3) RM(4) RM(6) RM(8) RM(12) RM(16) RM(24) RM(32)
-    default: break;   // route_mfma_ok admits only the sizes above
+  switch (nsw) {   // steps per workgroup: every size route_mfma_ok admits, split or not
+    RM(2) RM(4) RM(6) RM(8) RM(12) RM(16) RM(24) RM(32) RM(48) RM(64)
+    default: return hipErrorInvalidValue;   // route_mfma_ok admits only the sizes above
   }
 #undef RM
+  return hipGetLastError();
 }
 
 template <int EPL>
-static void route_mfma_ng(const RouterArgs& a, hipStream_t s) {
+static void route_mfma_ng(const RouterArgs& a0, hipStream_t s) {
+  RouterArgs a = a0;
+  a.msplit = route_mfma_splits(a);
   const dim3 g(((a.T + 63) / 64 + 7) / 8 * 8 * 16), b(256);   // 16 workgroups per token block of 64
   if (a.H <= 512) hx_launch(k_route_mfma<EPL, 1>, g, b, 0, s, a);
   else if (a.H <= 1024) hx_launch(k_route_mfma<EPL, 2>, g, b, 0, s, a);

@@ -191,6 +191,29 @@ def test_mfma_routing_all_tied_tokens_mixed_with_others(E):
     assert np.array_equal(r["offsets"].cpu().numpy(), offs)
 
 
+@pytest.mark.parametrize("H,E,k", [(1024, 64, 4), (1024, 1024, 1)])
+def test_mfma_routing_split_planes(H, E, k):
+    """the MFMA router's K split: H = 1024, E = 64, k = 4 sums four logit planes
+    (4 K steps of 64 per workgroup); H = 1024, E = 1024, k = 1 has no room for
+    the extra planes in front of the shared rows and runs one plane of 16 steps"""
+    hx, synth = _hx()
+    cfg = hx.TextConfig(hidden_size=H, num_experts=E, num_experts_per_tok=k, moe_intermediate_size=32,
+                        shared_expert_intermediate_size=32, norm_topk_prob=True)
+    w = synth.make_weights(cfg, synth.FMT_BF16, 23)
+    blk = hx.Qwen3_5MoeBlock.load(cfg, w, act_dtype=hx.BF16)
+    o = oracle_for(cfg, synth.to_numpy(w), O.BF16)
+    for T in (9, 200):
+        x = synth.make_x(cfg, T, 23 + T)
+        r = blk.route(x)
+        _, _, ix, wt = o.route(x_np(x))
+        assert np.array_equal(r["topk_idx"].cpu().numpy(), ix), (H, E, k, T)
+        assert_topk_w(r["topk_w"].cpu().numpy(), wt, k, exact=False)
+        perm, offs, inv = O.dispatch(ix, E)
+        assert np.array_equal(r["perm"].cpu().numpy(), perm)
+        got = blk.forward(x).float().cpu().numpy()
+        assert rel_err(got, o.forward(x_np(x))) <= TOL_BF16
+
+
 def test_mfma_routing_underflowing_probabilities():
     """a bias of -150 on 12 of 16 experts: their probabilities underflow to 0
     and the top 8 takes them by id; the MFMA routing must notice (selected exps
