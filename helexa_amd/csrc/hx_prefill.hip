@@ -542,8 +542,15 @@ __global__ __launch_bounds__(64 * NW, 3) void k_gate_up_q4k(ExpertArgs a) {
 // bytes (low and high nibbles) and the half's qh bytes, so a chunk needs per
 // weight row 32 ql + 32 qh bytes, with the half's 8 scales beside them.
 //   stage: A = 64 rows x 64 K (8 KB; the row's 8 16-byte pieces stored at
-//          slot piece ^ (row % 8)); B = 64 B per weight row; S = 8 B per row;
+//          slot piece ^ ((row >> 1) & 7)); B = 64 B per weight row (its four
+//          16-byte parts stored at slot part ^ ((row >> 2) & 3)); S = 8 B per row;
 //   once per tile: d of both superblocks of each weight row (4 B).
+// The two swizzles make the fragment reads conflict-free: the 16 rows of an
+// A fragment (128 B apart, so rows 2 apart share banks) read 16 different
+// 16-byte bank groups, and the 32 lanes of a B read (16 rows 64 B apart, two
+// 8-byte halves) cover the 64 banks once. (With slot piece ^ (row % 8) and
+// unswizzled B rows, bank conflicts took 2/3 of the kernel's LDS cycles and
+// the kernel 5-8 % longer.)
 // Dequantisation in registers: q = ql nibble | (qh bits << 4) under the 0x6400
 // f16 pattern (1024 + q, exact), (x - 1056) * (d * sc) with packed f16 ops.
 // Rows are scaled by their routing weight by position (the shared expert's
@@ -570,9 +577,10 @@ HX_DEV int dq_col(int c) { return 256 * (c >> 2) + 128 * ((c >> 1) & 1) + 32 * (
 // sources, dq_col(c) / 2 (the ql offset 128 sb + 64 n + 32 p) to ql pieces,
 // 64 sb + 32 n to qh pieces and 16 sb + 8 n to the scales.
 // A piece q = 256 i + t: row q / 8, slot q % 8 holding segment
-// (q % 8) ^ (row % 8): segments 0..3 are K columns 8 s .. of quarter p, 4..7 of
-// quarter p + 2 (64 columns further). B piece q = 256 i + t: part q % 4 of
-// weight row q / 4 (ql bytes 16 part for parts 0, 1; qh bytes 16 (part - 2)).
+// (q % 8) ^ ((row / 2) % 8): segments 0..3 are K columns 8 s .. of quarter p,
+// 4..7 of quarter p + 2 (64 columns further). B piece q = 256 i + t: slot q % 4
+// of weight row q / 4, holding part (q % 4) ^ ((row / 4) % 4) (ql bytes
+// 16 part for parts 0, 1; qh bytes 16 (part - 2)).
 // Scale dword t: row t / 2, half t % 2.
 struct DqSrc {
   const uint8_t* a[2];
@@ -586,7 +594,7 @@ HX_DEV DqSrc dq_sources(const uint16_t* hbf, int hstride, int p0, int rows, cons
   DqSrc src;
 #pragma unroll
   for (int i = 0; i < 2; i++) {
-    const int q = i * 256 + tid, row = q >> 3, seg = (q & 7) ^ (row & 7);
+    const int q = i * 256 + tid, row = q >> 3, seg = (q & 7) ^ ((row >> 1) & 7);
     const int r = min(row, rows - 1);   // padding rows repeat the last row
     src.a[i] = (const uint8_t*)(hbf + (int64_t)(p0 + r) * hstride + 64 * (seg >> 2) + 8 * (seg & 3));
   }
@@ -596,7 +604,7 @@ HX_DEV DqSrc dq_sources(const uint16_t* hbf, int hstride, int p0, int rows, cons
   src.bqh = 0;
 #pragma unroll
   for (int i = 0; i < 2; i++) {
-    const int q = i * 256 + tid, row = q >> 2, part = q & 3;
+    const int q = i * 256 + tid, row = q >> 2, part = (q & 3) ^ ((row >> 2) & 3);
     src.b[i] = part < 2 ? ql + (int64_t)(n0 + row) * (DQ_K / 2) + 16 * part
                         : qh + (int64_t)(n0 + row) * (DQ_K / 4) + 16 * (part - 2);
     src.bqh |= (part >= 2 ? 1u : 0u) << i;
@@ -634,7 +642,9 @@ HX_DEV void dq_compute(const lds_u8* st, const uint16_t* dl, int sb, f32x4_t (*a
   for (int j = 0; j < 2; j++) {
     const int brow = 32 * wave + 16 * j + l16;
     const lds_u8* B = st + DQ_A + brow * DQ_BROW;
-    const uint2 ql = lds_ld8(B + 8 * kq), qh = lds_ld8(B + 32 + 8 * kq);
+    // ql bytes 8 kq .. (part kq / 2) and qh bytes 8 kq .. (part 2 + kq / 2); brow / 4 % 4 = l16 / 4
+    const int sw = (l16 >> 2) & 3, hk = 8 * (kq & 1);
+    const uint2 ql = lds_ld8(B + 16 * ((kq >> 1) ^ sw) + hk), qh = lds_ld8(B + 16 * ((2 + (kq >> 1)) ^ sw) + hk);
     const uint2 sc = lds_ld8(st + DQ_A + DQ_B + brow * 8);
     const float d = f16_to_f32(dl[2 * brow + sb]);
     const int sh = 8 * (kq >> 1);
@@ -655,7 +665,7 @@ HX_DEV void dq_compute(const lds_u8* st, const uint16_t* dl, int sb, f32x4_t (*a
       for (int mt = 0; mt < MT; mt++) {
         const int row = 16 * mt + l16, seg = 4 * t + kq;
         const f16x8_t av = __builtin_bit_cast(
-            f16x8_t, *(const __attribute__((address_space(3))) u32x4_t*)(st + row * 128 + ((seg ^ (l16 & 7)) << 4)));
+            f16x8_t, *(const __attribute__((address_space(3))) u32x4_t*)(st + row * 128 + ((seg ^ ((l16 >> 1) & 7)) << 4)));
         acc[j][mt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bf, acc[j][mt], 0, 0, 0);
       }
     }
