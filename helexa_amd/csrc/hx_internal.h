@@ -38,7 +38,14 @@ struct DispatchArgs {
   // the decode routing tail writes the plan only (a forward reads nothing else;
   // topk_idx, perm, inv, offsets, slots and counts are left as they were)
   bool plan_only = false;
-  int32_t* hist;       // [dispatch_blocks(F)][E] per-block expert counts (multi-block dispatch)
+  // multi-block dispatch (F > HX_DISPATCH_SMALL): hist[c][e] = entries of
+  // expert e among the tokens of chunk c (HX_DISPATCH_TOK tokens), which the
+  // scan turns into the position in perm of the chunk's first such entry; bit
+  // j of bits[w][e] is set when token 32 w + j has expert e among its top k.
+  // The two are one block of (dispatch_chunks(T) + dispatch_words(T)) E ints,
+  // hist first.
+  int32_t* hist;       // [dispatch_chunks(T)][E]
+  uint32_t* bits;      // [dispatch_words(T)][E]
   // prefill: routing weight by permuted position, wpos[p] = topk_w[perm[p]],
   // and the shared expert's sigmoid gate at wpos[F + t]
   const float* topk_w = nullptr;
@@ -46,9 +53,14 @@ struct DispatchArgs {
   float* wpos = nullptr;
 };
 
-// Multi-block dispatch: entries per block and block count.
-#define HX_DISPATCH_CHUNK 2048
-__host__ __device__ inline int dispatch_blocks(int F) { return (F + HX_DISPATCH_CHUNK - 1) / HX_DISPATCH_CHUNK; }
+// Dispatch: up to HX_DISPATCH_SMALL entries sorted by one workgroup in LDS,
+// more by the multi-block dispatch (per-chunk histogram + token bitmap, 32
+// tokens a word, HX_DISPATCH_TOK tokens a chunk).
+#define HX_DISPATCH_SMALL 2048
+#define HX_DISPATCH_TOK 256
+__host__ __device__ inline bool dispatch_multi(int F) { return F > HX_DISPATCH_SMALL; }
+__host__ __device__ inline int dispatch_words(int T) { return (T + 31) / 32; }
+__host__ __device__ inline int dispatch_chunks(int T) { return (T + HX_DISPATCH_TOK - 1) / HX_DISPATCH_TOK; }
 
 // Decode plan: everything the decode expert kernels need about the routing, in
 // one contiguous int32 block they pull into LDS with a single coalesced load.
@@ -155,15 +167,14 @@ __host__ __device__ inline int down_groups(int F, int T) { return (F + T + HX_DO
 void launch_router(const RouterArgs& a, bool xbf, bool rbf, hipStream_t s);
 void launch_route_small(const RouterArgs& a, hipStream_t s);   // T <= HX_DECODE_MAX_T, one workgroup
 void launch_route_tokens(const RouterArgs& a, hipStream_t s);
-// hist_ready: the per-chunk histogram is already in d.hist (the MFMA routing
-// fills it)
-void launch_dispatch(const DispatchArgs& d, hipStream_t s, bool hist_ready = false);
+// maps_ready: d.hist and d.bits are already filled (the MFMA routing does it)
+void launch_dispatch(const DispatchArgs& d, hipStream_t s, bool maps_ready = false);
 // prefill routing with the router GEMM on MFMA (bf16 tokens and router rows,
 // renormalised top-k): approximate logits, then per token the exact top-k
 bool route_mfma_ok(const RouterArgs& a, bool xbf, bool rbf);
 int route_mfma_splits(const RouterArgs& a);
 // also writes the f16 tokens for the MFMA expert kernels when xh is not null,
-// and clears the dispatch histogram that launch_route_mfma fills
+// and clears the dispatch histogram and bitmap that launch_route_mfma fills
 hipError_t launch_router_mfma(const RouterArgs& a, uint16_t* xh, hipStream_t s);
 void launch_route_mfma(const RouterArgs& a, hipStream_t s);
 hipError_t launch_row_norms(const void* R, int E1, int H, float* out, hipStream_t s);

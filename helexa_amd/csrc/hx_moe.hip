@@ -122,7 +122,7 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 #define HX_MAX_TOKENS ((int64_t)1 << 24)
 
 struct WsLayout {
-  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, hist, hbuf, hbf, xh, xcv, obuf, xn, ym, dpart,
+  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, dmap, hbuf, hbf, xh, xcv, obuf, xn, ym, dpart,
       wpos, total;
   int hstride, max_slots, max_tiles;
 };
@@ -153,7 +153,7 @@ static WsLayout ws_layout(const hx_moe* m, int64_t T) {
   L.tiles = take(sizeof(int32_t) * 4 * L.max_tiles);
   L.counts = take(sizeof(int32_t) * 4);
   L.plan = take(sizeof(int32_t) * plan_ints(L.max_slots, (int)F, (int)T));
-  L.hist = decode ? 0 : take(sizeof(int32_t) * (size_t)dispatch_blocks((int)F) * E);
+  L.dmap = decode ? 0 : take(sizeof(int32_t) * (size_t)(dispatch_chunks((int)T) + dispatch_words((int)T)) * E);
   L.hbuf = take(sizeof(float) * (F + T) * L.hstride);
   L.hbf = take(sizeof(uint16_t) * (F + T) * L.hstride);
   const size_t act = m->cfg.act_dtype == HX_BF16 ? 2 : 4;
@@ -440,7 +440,8 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
   d.counts = (int32_t*)(ws + L.counts);
   d.plan = (int32_t*)(ws + L.plan);
   d.max_slots = L.max_slots;
-  d.hist = L.hist ? (int32_t*)(ws + L.hist) : nullptr;
+  d.hist = L.dmap ? (int32_t*)(ws + L.dmap) : nullptr;
+  d.bits = L.dmap ? (uint32_t*)(ws + L.dmap) + (size_t)dispatch_chunks((int)T) * E : nullptr;
   d.topk_w = r.topk_w;
   d.sgw = r.sgw;
   d.wpos = L.wpos ? (float*)(ws + L.wpos) : nullptr;

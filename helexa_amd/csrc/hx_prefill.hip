@@ -386,8 +386,14 @@ HX_DEV void q4k_compute(const lds_u8* st, f32x4_t (*accg)[Q::FPW_], f32x4_t (*ac
   for (int f = 0; f < NB; f++) {
     const int row = (f < NF ? 0 : Q::COLS) + 16 * (NF * wave + f % NF) + l16;
     hdr[f] = lds_ld16(B + row * QB_ROW);
-#pragma unroll
-    for (int g = 0; g < 2; g++) qs[f][g] = lds_ld8(B + row * QB_ROW + 16 + 32 * g + 8 * kq);
+    // two 8-byte reads: the compiler would merge them into one ds_read2_b64,
+    // whose two addresses 32 B apart in rows 80 B apart conflict in the LDS
+    // banks (measured ~3x the cycles of the two reads); the empty asm hides
+    // the relation between the addresses
+    uint32_t q0 = row * QB_ROW + 16 + 8 * kq, q1 = q0 + 32;
+    asm volatile("" : "+v"(q1));
+    qs[f][0] = lds_ld8(B + q0);
+    qs[f][1] = lds_ld8(B + q1);
   }
   h2_t a[NB][4], nb[NB][4];
 #pragma unroll

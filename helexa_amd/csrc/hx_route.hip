@@ -162,32 +162,42 @@ __global__ __launch_bounds__(1024) void k_dispatch(DispatchArgs a) {
 
 // ----------------------------------------------------------------------------
 // Multi-block dispatch for large F (prefill): the same outputs as k_dispatch.
-//   k_disp_hist    block b counts the experts of entries [2048 b, 2048 b + 2048)
-//   k_disp_scan    one block: per expert, the exclusive prefix over blocks and
+// The order is by expert, then token (each token's experts are distinct, so
+// this is the stable order by entry index).
+//   k_disp_maps    (routing paths other than the MFMA one, which fills both
+//                  maps itself) block c counts the experts of the tokens of
+//                  chunk c (HX_DISPATCH_TOK tokens) and sets their bits
+//   k_disp_scan    one block: per expert, the exclusive prefix over chunks and
 //                  the total; offsets = exclusive scan of the totals; slots and
 //                  M-tiles as in dispatch_block
-//   k_disp_scatter block b places its entries stably: position = offsets[e] +
-//                  (entries of e in earlier blocks) + (rank within the block)
+//   k_disp_scatter one thread per entry (token t, expert e): position = the
+//                  base of e in t's chunk + the set bits of e's bitmap words
+//                  from the chunk's first token up to t
 // ----------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_disp_hist(DispatchArgs a) {
+__global__ __launch_bounds__(256) void k_disp_maps(DispatchArgs a) {
+  constexpr int WPC = HX_DISPATCH_TOK / 32;   // bitmap words a chunk
   __shared__ int cnt[HX_MAX_EXPERTS];
-  const int b = blockIdx.x, E = a.E;
-  for (int e = threadIdx.x; e < E; e += 256) cnt[e] = 0;
-  __syncthreads();
-  const int f0 = b * HX_DISPATCH_CHUNK, f1 = min(a.F, f0 + HX_DISPATCH_CHUNK);
-  // all of this thread's loads before the first atomic
-  constexpr int PER = HX_DISPATCH_CHUNK / 256;
-  int ev[PER];
+  __shared__ uint32_t row[WPC][HX_MAX_EXPERTS];
+  const int c = blockIdx.x, E = a.E, k = a.k, W = dispatch_words(a.T);
+  for (int e = threadIdx.x; e < E; e += 256) {
+    cnt[e] = 0;
 #pragma unroll
-  for (int i = 0; i < PER; i++) {
-    const int f = f0 + threadIdx.x + 256 * i;
-    ev[i] = f < f1 ? a.topk_idx[f] : -1;
+    for (int i = 0; i < WPC; i++) row[i][e] = 0u;
   }
-#pragma unroll
-  for (int i = 0; i < PER; i++)
-    if (ev[i] >= 0) atomicAdd(&cnt[ev[i]], 1);
   __syncthreads();
-  for (int e = threadIdx.x; e < E; e += 256) a.hist[(int64_t)b * E + e] = cnt[e];
+  const int t0 = c * HX_DISPATCH_TOK, n = min(HX_DISPATCH_TOK, a.T - t0) * k;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const int e = a.topk_idx[(int64_t)t0 * k + i], t = i / k;
+    atomicAdd(&cnt[e], 1);
+    atomicOr(&row[t >> 5][e], 1u << (t & 31));
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 256) {
+    a.hist[(int64_t)c * E + e] = cnt[e];
+#pragma unroll
+    for (int i = 0; i < WPC; i++)
+      if (c * WPC + i < W) a.bits[(int64_t)(c * WPC + i) * E + e] = row[i][e];
+  }
 }
 
 // exclusive scans of three values per thread over a 1024-thread block in one
@@ -224,8 +234,8 @@ HX_DEV void block_scan3_1024(const int (&v)[3], int (&r)[3], int (&tot)[3], int 
   }
 }
 
-// k_disp_scan: one block, thread e = expert e. The per-block bases are
-// written once (prefix over blocks + the expert's offset) when the block
+// k_disp_scan: one block, thread e = expert e. The per-chunk bases are
+// written once (prefix over chunks + the expert's offset) when the chunk
 // count is at most SCAN_REG (registers), else in a second pass; the M tiles
 // are written in parallel, tile i's expert found by an upper-bound search
 // over the experts' first tiles (experts without tiles share the next one's
@@ -234,9 +244,9 @@ constexpr int SCAN_REG = 32;
 __global__ __launch_bounds__(1024) void k_disp_scan(DispatchArgs a) {
   __shared__ int sh[3][17];
   __shared__ int s_first[HX_MAX_EXPERTS], s_slot[HX_MAX_EXPERTS], s_off[HX_MAX_EXPERTS], s_cnt[HX_MAX_EXPERTS];
-  const int e = threadIdx.x, E = a.E, nb = dispatch_blocks(a.F);
+  const int e = threadIdx.x, E = a.E, nb = dispatch_chunks(a.T);
   int count = 0;
-  int pre[SCAN_REG];   // entries of e in blocks before b (nb <= SCAN_REG)
+  int pre[SCAN_REG];   // entries of e in chunks before c (nb <= SCAN_REG)
   if (e < E) {
     if (nb <= SCAN_REG) {
       int h[SCAN_REG];
@@ -248,7 +258,7 @@ __global__ __launch_bounds__(1024) void k_disp_scan(DispatchArgs a) {
         count += h[i];
       }
     } else {
-      // the expert's per-block counts, PB at a time: all loads of a batch
+      // the expert's per-chunk counts, PB at a time: all loads of a batch
       // issued before the first is used (one memory round trip per batch)
       constexpr int PB = 16;
       for (int b0 = 0; b0 < nb; b0 += PB) {
@@ -273,7 +283,7 @@ __global__ __launch_bounds__(1024) void k_disp_scan(DispatchArgs a) {
     s_slot[e] = slot;
     s_off[e] = off;
     s_cnt[e] = count;
-    // per-block bases: offsets[e] + entries of e in earlier blocks
+    // per-chunk bases: offsets[e] + entries of e in earlier chunks
     if (nb <= SCAN_REG) {
 #pragma unroll
       for (int i = 0; i < SCAN_REG; i++)
@@ -326,85 +336,26 @@ __global__ __launch_bounds__(1024) void k_disp_scan(DispatchArgs a) {
   }
 }
 
-// wave w places the entries [f0 + 512 w, f0 + 512 w + 512) of block b's
-// chunk: its per-expert base = the block's base + the counts of waves 0..w-1
-// (from a per-wave histogram), then 64 entries at a time in order, the rank of
-// an entry among the equal experts of its 64 from bitwise ballots. Each wave
-// keeps its own running bases, so the waves never wait for each other after
-// the bases are set. A wave's experts and weights are loaded into registers
-// before anything else (one memory round trip).
+// one thread per entry: the chunk's base and the (at most HX_DISPATCH_TOK / 32)
+// bitmap words from the chunk's first token to t, all loaded before the first
+// is used; threads t < T also copy the shared expert's sigmoid gate to its
+// rows' weights (wpos[F + t])
 __global__ __launch_bounds__(256) void k_disp_scatter(DispatchArgs a) {
-  constexpr int NWV = 4, SUB = HX_DISPATCH_CHUNK / NWV;
-  __shared__ int wbase[NWV][HX_MAX_EXPERTS];
-  const int b = blockIdx.x, E = a.E, tid = threadIdx.x, lane = lane_id(), wave = tid >> 6;
-  if (b == 0 && a.wpos && a.has_shared)
-    for (int t = tid; t < a.T; t += 256) a.wpos[a.F + t] = a.sgw[t];
-  // this block's per-expert bases, loaded before anything waits on memory
-  constexpr int EPT = HX_MAX_EXPERTS / 256;
-  int bb[EPT];
+  constexpr int WPC = HX_DISPATCH_TOK / 32;
+  const int f = blockIdx.x * 256 + threadIdx.x;
+  if (a.wpos && a.has_shared && f < a.T) a.wpos[a.F + f] = a.sgw[f];
+  if (f >= a.F) return;
+  const int E = a.E, e = a.topk_idx[f], t = f / a.k, w = t >> 5, w0 = (t / HX_DISPATCH_TOK) * WPC;
+  const float wv = a.wpos ? a.topk_w[f] : 0.0f;
+  int pos = a.hist[(int64_t)(t / HX_DISPATCH_TOK) * E + e];
+  uint32_t b[WPC];
 #pragma unroll
-  for (int i = 0; i < EPT; i++) {
-    const int e = tid + 256 * i;
-    bb[i] = e < E ? a.hist[(int64_t)b * E + e] : 0;
-  }
-  for (int e = tid; e < E; e += 256)
+  for (int i = 0; i < WPC; i++) b[i] = w0 + i <= w ? a.bits[(int64_t)(w0 + i) * E + e] : 0u;
 #pragma unroll
-    for (int w = 0; w < NWV; w++) wbase[w][e] = 0;
-  __syncthreads();
-  const int f0 = b * HX_DISPATCH_CHUNK, f1 = min(a.F, f0 + HX_DISPATCH_CHUNK);
-  const int s0 = min(f1, f0 + SUB * wave), s1 = min(f1, s0 + SUB);
-  constexpr int PER = SUB / 64;
-  int ev[PER];
-  float wv[PER];
-#pragma unroll
-  for (int i = 0; i < PER; i++) {
-    const int f = s0 + lane + 64 * i;
-    ev[i] = f < s1 ? a.topk_idx[f] : -1;
-    wv[i] = f < s1 && a.wpos ? a.topk_w[f] : 0.0f;
-  }
-#pragma unroll
-  for (int i = 0; i < PER; i++)
-    if (ev[i] >= 0) atomicAdd(&wbase[wave][ev[i]], 1);
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < EPT; i++) {
-    const int e = tid + 256 * i;
-    if (e >= E) break;
-    int run = bb[i];
-#pragma unroll
-    for (int w = 0; w < NWV; w++) {
-      const int c = wbase[w][e];
-      wbase[w][e] = run;
-      run += c;
-    }
-  }
-  __syncthreads();
-  const int nbits = 32 - __clz(E);
-  const unsigned long long lt = (1ull << lane) - 1ull;
-  int* base = wbase[wave];
-#pragma unroll
-  for (int i = 0; i < PER; i++) {
-    const int f = s0 + lane + 64 * i;
-    if (s0 + 64 * i >= s1) break;   // wave-uniform
-    const bool valid = f < s1;
-    const int e = valid ? ev[i] : 0;
-    unsigned long long mask = __ballot(valid);
-    for (int bit = 0; bit < nbits; bit++) {
-      const int v = (e >> bit) & 1;
-      const unsigned long long m = __ballot(v);
-      mask &= v ? m : ~m;
-    }
-    const int rank = __popcll(mask & lt), cnt = __popcll(mask);
-    if (valid) {
-      const int pos = base[e] + rank;
-      a.perm[pos] = f;
-      if (a.inv) a.inv[f] = pos;
-      if (a.wpos) a.wpos[pos] = wv[i];
-    }
-    __builtin_amdgcn_wave_barrier();   // every lane has read base[] before the leaders move it
-    if (valid && rank == 0) base[e] += cnt;
-    __builtin_amdgcn_wave_barrier();
-  }
+  for (int i = 0; i < WPC; i++) pos += __popc(w0 + i < w ? b[i] : w0 + i == w ? b[i] & ((1u << (t & 31)) - 1u) : 0u);
+  a.perm[pos] = f;
+  if (a.inv) a.inv[f] = pos;
+  if (a.wpos) a.wpos[pos] = wv;
 }
 
 // per-token routing for any T: one wave per token
@@ -502,15 +453,14 @@ void launch_route_tokens(const RouterArgs& a, hipStream_t s) {
 #undef RT
 }
 
-void launch_dispatch(const DispatchArgs& d, hipStream_t s, bool hist_ready) {
-  const int nb = dispatch_blocks(d.F);
-  if (nb <= 1 || !d.hist || d.E > 1024) {
+void launch_dispatch(const DispatchArgs& d, hipStream_t s, bool maps_ready) {
+  if (!dispatch_multi(d.F) || !d.hist || d.E > 1024) {
     hipLaunchKernelGGL(k_dispatch, dim3(1), dim3(1024), 0, s, d);
     return;
   }
-  if (!hist_ready) hipLaunchKernelGGL(k_disp_hist, dim3(nb), dim3(256), 0, s, d);
+  if (!maps_ready) hipLaunchKernelGGL(k_disp_maps, dim3(dispatch_chunks(d.T)), dim3(256), 0, s, d);
   hipLaunchKernelGGL(k_disp_scan, dim3(1), dim3(1024), 0, s, d);
-  hipLaunchKernelGGL(k_disp_scatter, dim3(nb), dim3(256), 0, s, d);
+  hipLaunchKernelGGL(k_disp_scatter, dim3((d.F + 255) / 256), dim3(256), 0, s, d);
 }
 
 }  // namespace hx

@@ -76,8 +76,8 @@ constexpr int RM_AHEAD = 8;
 // write the f16 copy of the tokens the MFMA expert kernels read, K step s by
 // the workgroup of expert block s % (expert blocks)
 // (xh: each group of 8 elements converted exactly and stored in the swizzled
-// order (e0,e2)(e1,e3)(e4,e6)(e5,e7) at its own place), and the per-chunk
-// dispatch histogram the routing kernel fills is cleared (nhist ints).
+// order (e0,e2)(e1,e3)(e4,e6)(e5,e7) at its own place), and the dispatch
+// histogram and token bitmap the routing kernel fills are cleared (ndmap ints).
 //
 // Split K: grid z = s < S takes K steps s NST .. s NST + NST - 1 (NST steps of
 // 64 per workgroup, H = 64 NST S) and writes its sums to logit plane s (plane
@@ -90,14 +90,14 @@ template <int NST>
 __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict__ x, const uint16_t* __restrict__ R,
                                                      int T, int H, int E, int E1, float* __restrict__ m,
                                                      float* __restrict__ mp, uint16_t* __restrict__ xh,
-                                                     int32_t* __restrict__ hist, int nhist) {
+                                                     int32_t* __restrict__ dmap, int ndmap) {
   static_assert(NST % 2 == 0, "K steps come in pairs");
   __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][64 * 128];   // [buffer][A / B][row * 128 + slot * 16]
   const int NX = gridDim.x, L = blockIdx.y * NX + blockIdx.x, z = blockIdx.z;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  if (hist) {
+  if (dmap) {
     const int nwg = NX * gridDim.y * gridDim.z, lz = z * NX * gridDim.y + L;
-    for (int i = lz * 256 + tid; i < nhist; i += nwg * 256) hist[i] = 0;
+    for (int i = lz * 256 + tid; i < ndmap; i += nwg * 256) dmap[i] = 0;
   }
   const int eb = (L >> 3) % NX, tb = (L / (8 * NX)) * 8 + (L & 7);
   if (tb * 64 >= T) return;   // whole workgroups
@@ -500,8 +500,12 @@ __global__ __launch_bounds__(256) void k_route_mfma(RouterArgs a) {
     const int64_t f = (int64_t)t * k + lane;
     a.d.topk_idx[f] = out_e;
     a.topk_w[f] = out_w;
-    // the dispatch histogram of entry f's chunk (cleared by k_router_mfma)
-    if (a.d.hist && dispatch_blocks(a.d.F) > 1) atomicAdd(&a.d.hist[(f / HX_DISPATCH_CHUNK) * E + out_e], 1);
+    // the dispatch histogram of token t's chunk and t's bit of its expert in
+    // the bitmap (both cleared by k_router_mfma)
+    if (a.d.hist && dispatch_multi(a.d.F)) {
+      atomicAdd(&a.d.hist[(int64_t)(t / HX_DISPATCH_TOK) * E + out_e], 1);
+      atomicOr(&a.d.bits[(int64_t)(t >> 5) * E + out_e], 1u << (t & 31));
+    }
   }
   if (a.has_shared && lane == 0) a.sgw[t] = sigmoidf_(lsh);
 }
@@ -539,15 +543,15 @@ int route_mfma_splits(const RouterArgs& a) {
 }
 
 hipError_t launch_router_mfma(const RouterArgs& a, uint16_t* xh, hipStream_t s) {
-  int32_t* hist = a.d.hist && dispatch_blocks(a.d.F) > 1 ? a.d.hist : nullptr;
-  const int nhist = hist ? dispatch_blocks(a.d.F) * a.E : 0;
+  int32_t* dmap = a.d.hist && dispatch_multi(a.d.F) ? a.d.hist : nullptr;
+  const int ndmap = dmap ? (dispatch_chunks(a.T) + dispatch_words(a.T)) * a.E : 0;
   const int S = route_mfma_splits(a), nsw = a.H / 64 / S;
   const int NX = (a.E + 63) / 64;
   const dim3 grid(NX, ((a.T + 63) / 64 + 7) / 8 * 8, S);
 #define RM(N)                                                                                                    \
   case N:                                                                                                        \
     hx_launch(k_router_mfma<N>, grid, dim3(256), 0, s, (const uint16_t*)a.x, (const uint16_t*)a.R, a.T, a.H, a.E, \
-              a.E1, a.logits, a.mplanes, xh, hist, nhist);                                                       \
+              a.E1, a.logits, a.mplanes, xh, dmap, ndmap);                                                       \
     break;
   switch (nsw) {   // steps per workgroup: every size route_mfma_ok admits, split or not
     RM(2) RM(4) RM(6) RM(8) RM(12) RM(16) RM(24) RM(32) RM(48) RM(64)
