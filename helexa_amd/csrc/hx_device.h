@@ -50,12 +50,12 @@ HX_DEV uint32_t vconst() {
 
 HX_DEV float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
-HX_DEV uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// f32 -> bf16, round to nearest even, a NaN kept with its sign and upper
+// payload and quieted (bit 6 of the bf16 set): one v_cvt_pk_bf16_f32, whose
+// result equals that bit-level rule (u + 0x7fff + ((u >> 16) & 1)) >> 16 for
+// every one of the 2^32 f32 inputs (checked exhaustively on MI355X); two
+// conversions packed into one word compile to a single instruction
+HX_DEV uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 // exact for every f16 value (normal, subnormal, inf, nan): v_cvt_f32_f16 with
 // f16 denormals kept (the default mode of HIP kernels)

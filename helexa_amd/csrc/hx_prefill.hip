@@ -719,15 +719,16 @@ HX_DEV void dq_main(const ExpertArgs& a, uint8_t* ring, float* rws, const DqSrc&
   constexpr int OP = 136;   // pitch in bf16
   uint16_t* ot = (uint16_t*)ring;
 #pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const int col = 32 * wave + 16 * j + l16;
+  for (int mt = 0; mt < MT; mt++) {
+    // the weights of this lane's rows 16 mt + 4 kq .. + 3, one 16-byte read
+    const float4 w4 = *(const float4*)(rws + 16 * mt + 4 * kq);
+    const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
 #pragma unroll
-    for (int mt = 0; mt < MT; mt++)
+    for (int j = 0; j < 2; j++) {
+      const int col = 32 * wave + 16 * j + l16;
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const int m = 16 * mt + 4 * kq + i;
-        ot[m * OP + col] = f32_to_bf16(rws[m] * acc[j][mt][i]);
-      }
+      for (int i = 0; i < 4; i++) ot[(16 * mt + 4 * kq + i) * OP + col] = f32_to_bf16(wv[i] * acc[j][mt][i]);
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -741,7 +742,7 @@ HX_DEV void dq_main(const ExpertArgs& a, uint8_t* ring, float* rws, const DqSrc&
 template <int TS>
 __global__ __launch_bounds__(256, 3) void k_down_q6k(ExpertArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t ring[DQ_NST * DQ_STAGE + 128 * 4];
-  __shared__ float rws[PM];
+  __shared__ __attribute__((aligned(16))) float rws[PM];
   int nt, tile;
   xcd_tile(nt, tile);
   int e, p0, rows;
