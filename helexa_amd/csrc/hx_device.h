@@ -143,6 +143,10 @@ HX_DEV void expf_route_n(float* x) {
 
 HX_DEV float sigmoidf_(float v) { return 1.0f / (1.0f + __expf(-v)); }
 HX_DEV float siluf_(float g) { return g / (1.0f + __expf(-g)); }
+// the same with the division by one v_rcp_f32 (1 ulp): g -> -inf gives
+// rcp(inf) = 0, so -0 as the quotient; for the prefill SwiGLU epilogue, whose
+// result is rounded to f16
+HX_DEV float silu_rcp(float g) { return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)); }
 
 // Xor butterfly over aligned groups of WIDTH lanes (WIDTH a power of two <= 64):
 // for off = WIDTH/2 .. 1, every lane adds the value of lane (lane ^ off). Float

@@ -489,15 +489,18 @@ HX_DEV void q4k_main(const ExpertArgs& a, uint8_t* ring, const Q4kSrc<Q>& src, i
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int m = 16 * mt + 4 * kq + i;
-        ot[m * OP + col] = (_Float16)(siluf_(accg[mt][j][i]) * accu[mt][j][i]);
+        ot[m * OP + col] = (_Float16)(silu_rcp(accg[mt][j][i]) * accu[mt][j][i]);
       }
   }
   __syncthreads();
   constexpr int PER_ROW = Q::COLS / 8;
-  for (int q = threadIdx.x; q < 16 * MT * PER_ROW; q += Q::NT) {
-    const int m = q / PER_ROW, c8 = (q % PER_ROW) * 8;
-    if (m < rows) *(uint4*)(a.hbf + (int64_t)(p0 + m) * a.hstride + n0 + c8) = *(const uint4*)(ot + m * OP + c8);
-  }
+  static_assert(Q::NT % PER_ROW == 0, "a thread keeps its column piece");
+  constexpr int RSTEP = Q::NT / PER_ROW;   // rows one pass of the workgroup stores
+  const int m0 = threadIdx.x / PER_ROW, c8 = (threadIdx.x % PER_ROW) * 8;
+  _Float16* hrow = (_Float16*)a.hbf + (int64_t)(p0 + m0) * a.hstride + n0 + c8;
+#pragma unroll
+  for (int m = m0; m < 16 * MT; m += RSTEP, hrow += (int64_t)RSTEP * a.hstride)
+    if (m < rows) *(uint4*)hrow = *(const uint4*)(ot + m * OP + c8);
 }
 
 // grid (I / COLS, tiles rounded up to 8), mapped by xcd_tile
@@ -732,10 +735,11 @@ HX_DEV void dq_main(const ExpertArgs& a, uint8_t* ring, float* rws, const DqSrc&
   }
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < MT; i++) {
-    const int q = i * 256 + threadIdx.x, m = q >> 4, c8 = (q & 15) * 8;
+  for (int i = 0, m = threadIdx.x >> 4; i < MT; i++, m += 16) {
+    const int c8 = (threadIdx.x & 15) * 8;
     if (m < rows)
-      *(uint4*)((uint16_t*)a.obuf + (int64_t)(p0 + m) * a.H + n0 + c8) = *(const uint4*)(ot + m * OP + c8);
+      *(uint4*)((uint16_t*)a.obuf + (int64_t)(p0 + (threadIdx.x >> 4)) * a.H + (int64_t)(16 * i) * a.H + n0 + c8) =
+          *(const uint4*)(ot + m * OP + c8);
   }
 }
 
