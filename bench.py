@@ -30,7 +30,9 @@ Method
     tokens: C2 per layer here; C3, the 512-token chunk and C5 full forwards in
     their lines, C4 B = 1 (one layer x 48) in the C3 line.
   * `prefill` (secondary): C3, 2048 tokens of the same layer in Q4_K_M (gate/up
-    Q4_K, down Q6_K), tokens/s with its MFMA and HBM fractions, and a roofline
+    Q4_K, down Q6_K), tokens/s with its MFMA and HBM fractions (`us`: 20
+    back-to-back forwards timed by HIP events on the stream; `wall_us`: the
+    host clock around the same forwards, synchronised on both sides), and a roofline
     object for the gate/up MFMA kernel (event-timed; traced average, HBM traffic
     and MFMA counters from profiles/). `prefill_512`: the same at the
     reference's production prefill chunk of 512 tokens.
@@ -293,11 +295,14 @@ def prefill_work(cfg, fmts, T, U):
     return total_flops, total_bytes, flops, kbytes
 
 
-def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=5, bias=None, pmc_file=None, mfma_file=None,
+def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=20, bias=None, pmc_file=None, mfma_file=None,
                 trace_file=None, cpu_runs=0, c4_layer=False):
-    """One prefill line: wall-clock time of `reps` forwards, then the same forwards
-    again with every kernel timed by its own dispatch's HIP events, queued behind
-    a sleep kernel; roofline of the gate/up MFMA kernel (the largest)."""
+    """One prefill line: `reps` back-to-back forwards timed by HIP events on the
+    stream (GPU time per forward, `us`) and by the host clock around them with a
+    synchronisation on both sides (`wall_us`, which adds the host's launch of the
+    first forward); then `kern_reps` forwards again with every kernel timed by
+    its own dispatch's HIP events, queued behind a sleep kernel; roofline of the
+    gate/up MFMA kernel (the largest)."""
     import torch
     import helexa_amd as hx
     from helexa_amd import synth
@@ -315,14 +320,19 @@ def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=5, bias=None, pmc_f
     for _ in range(2):
         blk.forward(x, router_bias=bias, workspace=ws, out=y)
     torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
     t0 = time.perf_counter()
+    ev[0].record()
     for _ in range(reps):
         blk.forward(x, router_bias=bias, workspace=ws, out=y)
+    ev[1].record()
     torch.cuda.synchronize()
-    dt = (time.perf_counter() - t0) / reps
-    blk.timing_begin(reps)
+    wall = (time.perf_counter() - t0) / reps
+    dt = ev[0].elapsed_time(ev[1]) * 1e-3 / reps
+    kern_reps = 5
+    blk.timing_begin(kern_reps)
     torch.cuda._sleep(int(2.4e9 * 0.05))
-    for _ in range(reps):
+    for _ in range(kern_reps):
         blk.forward(x, router_bias=bias, workspace=ws, out=y)
     torch.cuda.synchronize()
     kern = {k: v[0] / v[1] * 1e3 for k, v in blk.timing_end().items() if v[1]}
@@ -351,7 +361,8 @@ def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=5, bias=None, pmc_f
               "mfma_frac": round(kflops[k] / (v * 1e-6) / (MFMA_BF16_PEAK_TFS * 1e12), 4) if k in kflops else None,
               "hbm_frac": round(kbytes[k] / (v * 1e-6) / (HBM_PEAK_GBS * 1e9), 4) if k in kbytes else None}
           for k, v in kern.items()}
-    out = {"workload": workload, "tokens": T, "us": round(dt * 1e6, 1), "tok_per_s": round(T / dt, 1),
+    out = {"workload": workload, "tokens": T, "forwards": reps, "us": round(dt * 1e6, 1),
+           "wall_us": round(wall * 1e6, 1), "tok_per_s": round(T / dt, 1),
            "mfma_frac": round(total_flops / dt / (MFMA_BF16_PEAK_TFS * 1e12), 4),
            "hbm_frac": round(total_bytes / dt / (HBM_PEAK_GBS * 1e9), 4),
            "algorithmic_flops": total_flops, "algorithmic_bytes": total_bytes, "unique_experts": U,
@@ -374,7 +385,7 @@ def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=5, bias=None, pmc_f
     return out
 
 
-def bench_prefill(T=2048, reps=5, cpu_runs=0):
+def bench_prefill(T=2048, reps=20, cpu_runs=0):
     """C3 (T = 2048) and the production chunk (T = 512): Q4_K_M prefill, seeded
     near-uniform routing"""
     from helexa_amd import synth
@@ -460,7 +471,7 @@ def b_rms(x, w, eps=1e-6):
     return y.to(x.dtype)
 
 
-def bench_c5(T=4096, target_share=0.40, reps=5, cpu_runs=0):
+def bench_c5(T=4096, target_share=0.40, reps=20, cpu_runs=0):
     """C5: 4096-token prefill of the Q4_K_M layer with a seeded Zipf(1.1) router
     bias (router_bias[e] = alpha ln p_{pi(e)}), alpha calibrated on this layer so
     the top 8 experts take about 40% of the assignments."""
