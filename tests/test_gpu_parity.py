@@ -214,6 +214,32 @@ def test_mfma_routing_split_planes(H, E, k):
         assert rel_err(got, o.forward(x_np(x))) <= TOL_BF16
 
 
+@pytest.mark.parametrize("fmt,act,norm", [("FMT_F32", O.F32, True), ("FMT_BF16", O.BF16, False)])
+def test_multi_block_dispatch_after_generic_routing(fmt, act, norm):
+    """more than 2048 entries routed by the per-token kernel (f32 tokens, or no
+    renormalisation): the dispatch's own kernel builds the chunk counts and the
+    token bitmap; T = 300 and 1000 leave the last bitmap word and the last
+    256-token chunk partly filled"""
+    hx, synth = _hx()
+    cfg = hx.TextConfig(hidden_size=256, num_experts=96, num_experts_per_tok=8, moe_intermediate_size=32,
+                        shared_expert_intermediate_size=32, norm_topk_prob=norm)
+    w = synth.make_weights(cfg, getattr(synth, fmt), 41)
+    blk = hx.Qwen3_5MoeBlock.load(cfg, w, act_dtype=act)
+    o = oracle_for(cfg, synth.to_numpy(w), act)
+    for T in (300, 1000):
+        x = synth.make_x(cfg, T, 41 + T, act)
+        r = blk.route(x)
+        _, _, ix, wt = o.route(x_np(x))
+        assert np.array_equal(r["topk_idx"].cpu().numpy(), ix), (fmt, norm, T)
+        assert_topk_w(r["topk_w"].cpu().numpy(), wt, cfg.num_experts_per_tok, exact=True)
+        perm, offs, inv = O.dispatch(ix, cfg.num_experts)
+        assert np.array_equal(r["perm"].cpu().numpy(), perm), (fmt, norm, T)
+        assert np.array_equal(r["offsets"].cpu().numpy(), offs)
+        assert np.array_equal(r["inv"].cpu().numpy(), inv)
+        got = blk.forward(x).float().cpu().numpy()
+        assert rel_err(got, o.forward(x_np(x))) <= (TOL_F32 if act == O.F32 else TOL_BF16), (fmt, norm, T)
+
+
 def test_mfma_routing_underflowing_probabilities():
     """a bias of -150 on 12 of 16 experts: their probabilities underflow to 0
     and the top 8 takes them by id; the MFMA routing must notice (selected exps
