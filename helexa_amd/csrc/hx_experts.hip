@@ -276,7 +276,9 @@ __global__ __launch_bounds__(256) void k_down_rows(ExpertArgs a) {
 // 8 per thread. Wave 0 sorts the token's k positions once (rank of each among
 // the k, into LDS); every thread then issues all k + 1 row loads together.
 // ----------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_combine(ExpertArgs a) {
+// (the bound of 8 workgroups per CU holds it to 64 registers, so the T
+// workgroups of a prefill are all resident at once instead of in two rounds)
+__global__ __launch_bounds__(256, 8) void k_combine(ExpertArgs a) {
   __shared__ int spos[HX_MAX_TOPK + 1];
   const int t = blockIdx.x, k = a.k;
   if (threadIdx.x < 64) {
