@@ -295,6 +295,17 @@ struct Q4k {
   }
 };
 
+// Ring layout for tiles of MT sub-tiles: tiles of at most 16 rows (most of
+// them at the 512-token prefill chunk) need 4 KB of A per stage, so their ring
+// has 3 stages, two chunks ahead, in the LDS of the 2-stage ring of the rest.
+template <class Q, int MT>
+struct QStage {
+  static constexpr int A = MT == 1 ? 16 * 128 * 2 : QA_BYTES;
+  static constexpr int SIZE = A + Q::BROWS * QB_ROW;
+  static constexpr int NST = MT == 1 ? 3 : 2;
+  static_assert(NST * SIZE <= Q::NST * Q::STAGE, "the stages fit the ring");
+};
+
 // Per-thread DMA sources of chunk 0; chunk kc adds 256 kc bytes to the A
 // sources and (kc / 2) 144 bytes (+ 64 for odd kc on qs pieces) to the B ones.
 // A: thread t moves piece t % 16 (stored at slot t % 16, holding K segment
@@ -333,14 +344,15 @@ HX_DEV Q4kSrc<Q> q4k_sources(const uint16_t* xh, int H, const int* rowsrc, const
 template <class Q, int MT>
 HX_DEV void q4k_issue(uint32_t lds0, int st, const Q4kSrc<Q>& src, int kc, int wave_u) {
   static_assert(Q::NT == 256, "A round i = rows 16 i .. 16 i + 15");
-  const uint32_t sbase = lds0 + (uint32_t)(st * Q::STAGE + wave_u * 64 * 16);
+  using S = QStage<Q, MT>;
+  const uint32_t sbase = lds0 + (uint32_t)(st * S::SIZE + wave_u * 64 * 16);
 #pragma unroll
   for (int i = 0; i < (MT < Q::NA ? MT : Q::NA); i++) dma16(src.a[i] + 256 * kc, sbase + (uint32_t)(i * Q::NT * 16));
   const int hdr_off = (kc >> 1) * 144, qs_off = hdr_off + 64 * (kc & 1);
 #pragma unroll
   for (int i = 0; i < Q::NBI; i++) {
     if (i * Q::NT + 64 * wave_u >= Q::BPIECES) break;   // the last round may cover fewer waves
-    dma16(src.b[i] + ((src.bq >> i) & 1 ? qs_off : hdr_off), sbase + (uint32_t)(QA_BYTES + i * Q::NT * 16));
+    dma16(src.b[i] + ((src.bq >> i) & 1 ? qs_off : hdr_off), sbase + (uint32_t)(S::A + i * Q::NT * 16));
   }
 }
 
@@ -378,7 +390,7 @@ template <class Q, int PAR, int MT>   // chunk parity: sub-blocks 4 PAR .. 4 PAR
 HX_DEV void q4k_compute(const lds_u8* st, f32x4_t (*accg)[Q::FPW_], f32x4_t (*accu)[Q::FPW_], int wave, int l16, int kq,
                         uint32_t knib, uint32_t kbyte, uint32_t kmagic) {
   constexpr int NF = Q::FPW_;
-  const lds_u8* B = st + QA_BYTES;
+  const lds_u8* B = st + QStage<Q, MT>::A;
   constexpr int NB = 2 * NF;   // B fragments of the wave: gate j, then up j
   uint4 hdr[NB];
   uint2 qs[NB][2];
@@ -464,15 +476,16 @@ HX_DEV void q4k_main(const ExpertArgs& a, uint8_t* ring, const Q4kSrc<Q>& src, i
       accg[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       accu[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
+  using S = QStage<Q, MT>;
 #pragma unroll
-  for (int c = 0; c < Q::NST - 1; c++)
+  for (int c = 0; c < S::NST - 1; c++)
     if (c < nk) q4k_issue<Q, MT>(lds0, c, src, c, wave_u);
   for (int kc = 0; kc < nk; kc++) {
-    const int ahead = min(Q::NST - 2, nk - 1 - kc);
+    const int ahead = min(S::NST - 2, nk - 1 - kc);
     q4k_wait<Q, MT>(ahead, wave_u);
     __syncthreads();   // chunk kc is in LDS for every wave; stage (kc - 1) % NST is free
-    if (kc + Q::NST - 1 < nk) q4k_issue<Q, MT>(lds0, (kc + Q::NST - 1) % Q::NST, src, kc + Q::NST - 1, wave_u);
-    const lds_u8* st = (const lds_u8*)ring + (kc % Q::NST) * Q::STAGE;
+    if (kc + S::NST - 1 < nk) q4k_issue<Q, MT>(lds0, (kc + S::NST - 1) % S::NST, src, kc + S::NST - 1, wave_u);
+    const lds_u8* st = (const lds_u8*)ring + (kc % S::NST) * S::SIZE;
     if (kc & 1) q4k_compute<Q, 1, MT>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
     else q4k_compute<Q, 0, MT>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
   }
