@@ -38,7 +38,7 @@ struct DispatchArgs {
   // the decode routing tail writes the plan only (a forward reads nothing else;
   // topk_idx, perm, inv, offsets, slots and counts are left as they were)
   bool plan_only = false;
-  // multi-block dispatch (F > HX_DISPATCH_SMALL): hist[c][e] = entries of
+  // prefill dispatch: hist[c][e] = entries of
   // expert e among the tokens of chunk c (HX_DISPATCH_TOK tokens), which the
   // scan turns into the position in perm of the chunk's first such entry; bit
   // j of bits[w][e] is set when token 32 w + j has expert e among its top k.
@@ -53,12 +53,9 @@ struct DispatchArgs {
   float* wpos = nullptr;
 };
 
-// Dispatch: up to HX_DISPATCH_SMALL entries sorted by one workgroup in LDS,
-// more by the multi-block dispatch (per-chunk histogram + token bitmap, 32
-// tokens a word, HX_DISPATCH_TOK tokens a chunk).
-#define HX_DISPATCH_SMALL 2048
+// Prefill dispatch maps: the per-chunk histogram (HX_DISPATCH_TOK tokens a
+// chunk) and the token bitmap (32 tokens a word).
 #define HX_DISPATCH_TOK 256
-__host__ __device__ inline bool dispatch_multi(int F) { return F > HX_DISPATCH_SMALL; }
 __host__ __device__ inline int dispatch_words(int T) { return (T + 31) / 32; }
 __host__ __device__ inline int dispatch_chunks(int T) { return (T + HX_DISPATCH_TOK - 1) / HX_DISPATCH_TOK; }
 
@@ -168,7 +165,7 @@ void launch_router(const RouterArgs& a, bool xbf, bool rbf, hipStream_t s);
 void launch_route_small(const RouterArgs& a, hipStream_t s);   // T <= HX_DECODE_MAX_T, one workgroup
 void launch_route_tokens(const RouterArgs& a, hipStream_t s);
 // maps_ready: d.hist and d.bits are already filled (the MFMA routing does it)
-void launch_dispatch(const DispatchArgs& d, hipStream_t s, bool maps_ready = false);
+hipError_t launch_dispatch(const DispatchArgs& d, hipStream_t s, bool maps_ready = false);
 // prefill routing with the router GEMM on MFMA (bf16 tokens and router rows,
 // renormalised top-k): approximate logits, then per token the exact top-k
 bool route_mfma_ok(const RouterArgs& a, bool xbf, bool rbf);

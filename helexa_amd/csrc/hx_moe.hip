@@ -550,9 +550,8 @@ static int run_route_dispatch(hx_moe* m, Plan& p, hipStream_t s) {
     tm_ext_done(m, SLOT_ROUTE_TOKENS);
     HX_HIP(hipGetLastError());
     tm_mark(m, SLOT_DISPATCH, 0, s);
-    launch_dispatch(p.ra.d, s, route_mfma(m, p));
+    HX_HIP(launch_dispatch(p.ra.d, s, route_mfma(m, p)));
     tm_mark(m, SLOT_DISPATCH, 1, s);
-    HX_HIP(hipGetLastError());
   }
   return HX_OK;
 }

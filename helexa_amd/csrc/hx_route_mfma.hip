@@ -502,7 +502,7 @@ __global__ __launch_bounds__(256) void k_route_mfma(RouterArgs a) {
     a.topk_w[f] = out_w;
     // the dispatch histogram of token t's chunk and t's bit of its expert in
     // the bitmap (both cleared by k_router_mfma)
-    if (a.d.hist && dispatch_multi(a.d.F)) {
+    if (a.d.hist) {
       atomicAdd(&a.d.hist[(int64_t)(t / HX_DISPATCH_TOK) * E + out_e], 1);
       atomicOr(&a.d.bits[(int64_t)(t >> 5) * E + out_e], 1u << (t & 31));
     }
@@ -543,7 +543,7 @@ int route_mfma_splits(const RouterArgs& a) {
 }
 
 hipError_t launch_router_mfma(const RouterArgs& a, uint16_t* xh, hipStream_t s) {
-  int32_t* dmap = a.d.hist && dispatch_multi(a.d.F) ? a.d.hist : nullptr;
+  int32_t* dmap = a.d.hist;
   const int ndmap = dmap ? (dispatch_chunks(a.T) + dispatch_words(a.T)) * a.E : 0;
   const int S = route_mfma_splits(a), nsw = a.H / 64 / S;
   const int NX = (a.E + 63) / 64;
