@@ -216,7 +216,7 @@ def test_mfma_routing_split_planes(H, E, k):
 
 @pytest.mark.parametrize("fmt,act,norm", [("FMT_F32", O.F32, True), ("FMT_BF16", O.BF16, False)])
 def test_multi_block_dispatch_after_generic_routing(fmt, act, norm):
-    """more than 2048 entries routed by the per-token kernel (f32 tokens, or no
+    """prefills routed by the per-token kernel (f32 tokens, or no
     renormalisation): the dispatch's own kernel builds the chunk counts and the
     token bitmap; T = 300 and 1000 leave the last bitmap word and the last
     256-token chunk partly filled"""
