@@ -16,16 +16,16 @@ namespace hx {
 // GEMMs. The order is by expert, then token (each token's experts are
 // distinct, so this is the stable order by entry index). (One workgroup
 // sorting the entries in LDS took ~35 µs at any size from 90 to 5,120
-// entries, against 10-15 µs for these three kernels.)
+// entries.)
 //   k_disp_maps    (routing paths other than the MFMA one, which fills both
 //                  maps itself) block c counts the experts of the tokens of
 //                  chunk c (HX_DISPATCH_TOK tokens) and sets their bits
-//   k_disp_scan    one block: per expert, the exclusive prefix over chunks and
-//                  the total; offsets = exclusive scan of the totals; slots and
-//                  M-tiles
-//   k_disp_scatter one thread per entry (token t, expert e): position = the
-//                  base of e in t's chunk + the set bits of e's bitmap words
-//                  from the chunk's first token up to t
+//   k_disp_fused   one workgroup per 1024 entries: per expert, the prefix over
+//                  chunks and the total; offsets = exclusive scan of the totals;
+//                  slots and M-tiles (workgroup 0); then one thread per entry
+//                  (token t, expert e): position = offset of e + the prefix of e
+//                  at t's chunk + the set bits of e's bitmap words from the
+//                  chunk's first token up to t
 // ----------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void k_disp_maps(DispatchArgs a) {
   constexpr int WPC = HX_DISPATCH_TOK / 32;   // bitmap words a chunk
@@ -87,128 +87,125 @@ HX_DEV void block_scan3_1024(const int (&v)[3], int (&r)[3], int (&tot)[3], int 
   }
 }
 
-// k_disp_scan: one block, thread e = expert e. The per-chunk bases are
-// written once (prefix over chunks + the expert's offset) when the chunk
-// count is at most SCAN_REG (registers), else in a second pass; the M tiles
-// are written in parallel, tile i's expert found by an upper-bound search
-// over the experts' first tiles (experts without tiles share the next one's
-// first tile, so the largest e with first[e] <= i is the owner).
-constexpr int SCAN_REG = 32;
-__global__ __launch_bounds__(1024) void k_disp_scan(DispatchArgs a) {
+// k_disp_fused: the scan and the scatter in one launch, one workgroup per
+// DISP_EPB entries. The per-chunk counts are complete before it starts, so
+// every workgroup scans them itself: thread e sums expert e's counts over all
+// chunks, keeping the prefix at the (at most DISP_MAXC) chunks its own entries
+// come from; the three-value block scan gives the offsets, slots and M tiles.
+// Workgroup 0 writes offsets, slots, tiles and counts; every workgroup places
+// its own entries (one thread each). The entry's expert and its bitmap words
+// are loaded before the scan, so their latency overlaps it. (A one-block scan
+// kernel followed by a per-entry scatter kernel took 6.0 + 4.6 us at 2048
+// tokens, plus the gap between the two launches.)
+constexpr int DISP_EPB = 1024;
+constexpr int DISP_MAXC = DISP_EPB / HX_DISPATCH_TOK + 2;
+__global__ __launch_bounds__(1024) void k_disp_fused(DispatchArgs a) {
+  constexpr int WPC = HX_DISPATCH_TOK / 32, PB = 16;
   __shared__ int sh[3][17];
   __shared__ int s_first[HX_MAX_EXPERTS], s_slot[HX_MAX_EXPERTS], s_off[HX_MAX_EXPERTS], s_cnt[HX_MAX_EXPERTS];
-  const int e = threadIdx.x, E = a.E, nb = dispatch_chunks(a.T);
+  __shared__ int s_base[DISP_MAXC][HX_MAX_EXPERTS];
+  const int e = threadIdx.x, E = a.E, nb = dispatch_chunks(a.T), k = a.k;
+  const int f0 = blockIdx.x * DISP_EPB, f1 = min(a.F, f0 + DISP_EPB);
+  const int c_lo = (f0 / k) / HX_DISPATCH_TOK, c_hi = ((f1 - 1) / k) / HX_DISPATCH_TOK;
+  // this thread's entry, then its bitmap words (the chunk's first word up to t's)
+  const int f = f0 + (int)threadIdx.x;
+  const bool has_f = f < f1;
+  const int fe = has_f ? a.topk_idx[f] : 0;
+  const float wv = has_f && a.wpos ? a.topk_w[f] : 0.0f;
+  const int t = f / k, w = t >> 5, w0 = (t / HX_DISPATCH_TOK) * WPC;
+  uint32_t b[WPC];
+#pragma unroll
+  for (int i = 0; i < WPC; i++) b[i] = has_f && w0 + i <= w ? a.bits[(int64_t)(w0 + i) * E + fe] : 0u;
+  // expert e's total and its prefix at chunks c_lo .. c_hi, PB counts per memory round trip
   int count = 0;
-  int pre[SCAN_REG];   // entries of e in chunks before c (nb <= SCAN_REG)
+  int pre[DISP_MAXC];
+#pragma unroll
+  for (int j = 0; j < DISP_MAXC; j++) pre[j] = 0;
   if (e < E) {
-    if (nb <= SCAN_REG) {
-      int h[SCAN_REG];
+    for (int c0 = 0; c0 < nb; c0 += PB) {
+      int h[PB];
 #pragma unroll
-      for (int i = 0; i < SCAN_REG; i++) h[i] = i < nb ? a.hist[(int64_t)i * E + e] : 0;
+      for (int i = 0; i < PB; i++) h[i] = c0 + i < nb ? a.hist[(int64_t)(c0 + i) * E + e] : 0;
 #pragma unroll
-      for (int i = 0; i < SCAN_REG; i++) {
-        pre[i] = count;
+      for (int i = 0; i < PB; i++) {
+#pragma unroll
+        for (int j = 0; j < DISP_MAXC; j++)
+          if (c0 + i == c_lo + j) pre[j] = count;
         count += h[i];
-      }
-    } else {
-      // the expert's per-chunk counts, PB at a time: all loads of a batch
-      // issued before the first is used (one memory round trip per batch)
-      constexpr int PB = 16;
-      for (int b0 = 0; b0 < nb; b0 += PB) {
-        int h[PB];
-#pragma unroll
-        for (int i = 0; i < PB; i++) h[i] = b0 + i < nb ? a.hist[(int64_t)(b0 + i) * E + e] : 0;
-#pragma unroll
-        for (int i = 0; i < PB; i++) {
-          if (b0 + i < nb) a.hist[(int64_t)(b0 + i) * E + e] = count;
-          count += h[i];
-        }
       }
     }
   }
   const int in[3] = {e < E ? count : 0, e < E && count > 0 ? 1 : 0, e < E ? (count + a.tile_m - 1) / a.tile_m : 0};
   int ex[3], tot[3];
   block_scan3_1024(in, ex, tot, sh);
-  const int off = ex[0], slot = ex[1], nslot = tot[1], ntile = tot[2];
+  const int off = ex[0], nslot = tot[1], ntile = tot[2];
   if (e < E) {
-    a.offsets[e] = off;
-    s_first[e] = ex[2];
-    s_slot[e] = slot;
-    s_off[e] = off;
-    s_cnt[e] = count;
-    // per-chunk bases: offsets[e] + entries of e in earlier chunks
-    if (nb <= SCAN_REG) {
 #pragma unroll
-      for (int i = 0; i < SCAN_REG; i++)
-        if (i < nb) a.hist[(int64_t)i * E + e] = pre[i] + off;
-    } else {
-      for (int b = 0; b < nb; b++) a.hist[(int64_t)b * E + e] += off;
-    }
-    if (count > 0) {
-      a.slots[3 * slot + 0] = e;
-      a.slots[3 * slot + 1] = off;
-      a.slots[3 * slot + 2] = count;
+    for (int j = 0; j < DISP_MAXC; j++)
+      if (c_lo + j <= c_hi) s_base[j][e] = off + pre[j];
+    if (blockIdx.x == 0) {
+      a.offsets[e] = off;
+      s_first[e] = ex[2];
+      s_slot[e] = ex[1];
+      s_off[e] = off;
+      s_cnt[e] = count;
+      if (count > 0) {
+        a.slots[3 * ex[1] + 0] = e;
+        a.slots[3 * ex[1] + 1] = off;
+        a.slots[3 * ex[1] + 2] = count;
+      }
     }
   }
   __syncthreads();
-  for (int t = threadIdx.x; t < ntile; t += 1024) {
-    int lo = 0, hi = E - 1;   // the largest e with s_first[e] <= t
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_first[mid] <= t) lo = mid;
-      else hi = mid - 1;
+  if (blockIdx.x == 0) {
+    for (int i = threadIdx.x; i < ntile; i += 1024) {
+      int lo = 0, hi = E - 1;   // the largest e with s_first[e] <= i
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_first[mid] <= i) lo = mid;
+        else hi = mid - 1;
+      }
+      const int m0 = (i - s_first[lo]) * a.tile_m, c = s_cnt[lo];
+      a.tiles[4 * i + 0] = s_slot[lo];
+      a.tiles[4 * i + 1] = lo;
+      a.tiles[4 * i + 2] = s_off[lo] + m0;
+      a.tiles[4 * i + 3] = c - m0 < a.tile_m ? c - m0 : a.tile_m;
     }
-    const int m0 = (t - s_first[lo]) * a.tile_m, c = s_cnt[lo];
-    a.tiles[4 * t + 0] = s_slot[lo];
-    a.tiles[4 * t + 1] = lo;
-    a.tiles[4 * t + 2] = s_off[lo] + m0;
-    a.tiles[4 * t + 3] = c - m0 < a.tile_m ? c - m0 : a.tile_m;
-  }
-  if (e == 0) a.offsets[E] = a.F;
-  int ns = nslot, nt = ntile;
-  if (a.has_shared) {
-    const int nst = (a.T + a.tile_m - 1) / a.tile_m;
-    for (int i = threadIdx.x; i < nst; i += 1024) {
-      const int m0 = i * a.tile_m;
-      a.tiles[4 * (ntile + i) + 0] = nslot;
-      a.tiles[4 * (ntile + i) + 1] = E;
-      a.tiles[4 * (ntile + i) + 2] = a.F + m0;
-      a.tiles[4 * (ntile + i) + 3] = a.T - m0 < a.tile_m ? a.T - m0 : a.tile_m;
+    if (threadIdx.x == 0) a.offsets[E] = a.F;
+    int ns = nslot, nt = ntile;
+    if (a.has_shared) {
+      const int nst = (a.T + a.tile_m - 1) / a.tile_m;
+      for (int i = threadIdx.x; i < nst; i += 1024) {
+        const int m0 = i * a.tile_m;
+        a.tiles[4 * (ntile + i) + 0] = nslot;
+        a.tiles[4 * (ntile + i) + 1] = E;
+        a.tiles[4 * (ntile + i) + 2] = a.F + m0;
+        a.tiles[4 * (ntile + i) + 3] = a.T - m0 < a.tile_m ? a.T - m0 : a.tile_m;
+      }
+      if (threadIdx.x == 0) {
+        a.slots[3 * nslot + 0] = E;
+        a.slots[3 * nslot + 1] = a.F;
+        a.slots[3 * nslot + 2] = a.T;
+      }
+      ns++;
+      nt += nst;
     }
     if (threadIdx.x == 0) {
-      a.slots[3 * nslot + 0] = E;
-      a.slots[3 * nslot + 1] = a.F;
-      a.slots[3 * nslot + 2] = a.T;
+      a.counts[0] = ns;
+      a.counts[1] = nt;
     }
-    ns++;
-    nt += nst;
   }
-  if (threadIdx.x == 0) {
-    a.counts[0] = ns;
-    a.counts[1] = nt;
-  }
-}
-
-// one thread per entry: the chunk's base and the (at most HX_DISPATCH_TOK / 32)
-// bitmap words from the chunk's first token to t, all loaded before the first
-// is used; threads t < T also copy the shared expert's sigmoid gate to its
-// rows' weights (wpos[F + t])
-__global__ __launch_bounds__(256) void k_disp_scatter(DispatchArgs a) {
-  constexpr int WPC = HX_DISPATCH_TOK / 32;
-  const int f = blockIdx.x * 256 + threadIdx.x;
+  // the shared expert's rows take its sigmoid gate as their weight
   if (a.wpos && a.has_shared && f < a.T) a.wpos[a.F + f] = a.sgw[f];
-  if (f >= a.F) return;
-  const int E = a.E, e = a.topk_idx[f], t = f / a.k, w = t >> 5, w0 = (t / HX_DISPATCH_TOK) * WPC;
-  const float wv = a.wpos ? a.topk_w[f] : 0.0f;
-  int pos = a.hist[(int64_t)(t / HX_DISPATCH_TOK) * E + e];
-  uint32_t b[WPC];
+  const int cl = t / HX_DISPATCH_TOK - c_lo;
+  if (has_f && cl >= 0 && cl < DISP_MAXC) {
+    int pos = s_base[cl][fe];
 #pragma unroll
-  for (int i = 0; i < WPC; i++) b[i] = w0 + i <= w ? a.bits[(int64_t)(w0 + i) * E + e] : 0u;
-#pragma unroll
-  for (int i = 0; i < WPC; i++) pos += __popc(w0 + i < w ? b[i] : w0 + i == w ? b[i] & ((1u << (t & 31)) - 1u) : 0u);
-  a.perm[pos] = f;
-  if (a.inv) a.inv[f] = pos;
-  if (a.wpos) a.wpos[pos] = wv;
+    for (int i = 0; i < WPC; i++) pos += __popc(w0 + i < w ? b[i] : w0 + i == w ? b[i] & ((1u << (t & 31)) - 1u) : 0u);
+    a.perm[pos] = f;
+    if (a.inv) a.inv[f] = pos;
+    if (a.wpos) a.wpos[pos] = wv;
+  }
 }
 
 // per-token routing for any T: one wave per token
@@ -309,8 +306,7 @@ void launch_route_tokens(const RouterArgs& a, hipStream_t s) {
 hipError_t launch_dispatch(const DispatchArgs& d, hipStream_t s, bool maps_ready) {
   if (!d.hist || d.E > HX_MAX_EXPERTS) return hipErrorInvalidValue;   // a prefill workspace holds the maps
   if (!maps_ready) hipLaunchKernelGGL(k_disp_maps, dim3(dispatch_chunks(d.T)), dim3(256), 0, s, d);
-  hipLaunchKernelGGL(k_disp_scan, dim3(1), dim3(1024), 0, s, d);
-  hipLaunchKernelGGL(k_disp_scatter, dim3((d.F + 255) / 256), dim3(256), 0, s, d);
+  hipLaunchKernelGGL(k_disp_fused, dim3((d.F + DISP_EPB - 1) / DISP_EPB), dim3(1024), 0, s, d);
   return hipGetLastError();
 }
 
