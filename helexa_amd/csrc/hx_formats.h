@@ -105,6 +105,20 @@ struct Chunk<HX_Q8_0> {
 };
 
 // ---------------------------------------------------------------- Q4_K (GGUF)
+// Stored layout of a Q4_K matrix of R rows: the GGUF superblocks (144 B) in
+// groups of HX_Q4K_GROUP rows, superblock-major inside a group -- superblock
+// sb of row r at ((r / G) G nsb + sb Gr + r % G) 144, Gr = min(G, R - r / G G)
+// the rows of r's group. The same bytes as the GGUF rows, reordered at load so
+// that one superblock of a group's rows (what a prefill tile's K chunk reads
+// from its 64 weight rows) is one contiguous run: read row by row, the chunks
+// touched DRAM pages 80 bytes at a time (measured on MI355X: 4.6 against
+// 6.2 TB/s for the same bytes blocked).
+#define HX_Q4K_GROUP 64
+HX_DEV const uint8_t* q4k_sb(const uint8_t* mat, int R, int K, int row, int sb) {
+  const int nsb = K / 256, g0 = row & ~(HX_Q4K_GROUP - 1), gr = min(HX_Q4K_GROUP, R - g0);
+  return mat + ((int64_t)g0 * nsb + (int64_t)sb * gr + (row - g0)) * 144;
+}
+
 // Chunk c of a row: superblock sb = c / 8, cc = c % 8, pair p = cc / 2, half
 // h = cc % 2. It holds the 16 bytes qs[32p + 16h .. +15]: low nibbles are
 // elements 64p + 16h + i (sub-block 2p), high nibbles 64p + 32 + 16h + i
@@ -118,7 +132,7 @@ struct Chunk<HX_Q4_K> {
     return sb * 256 + 64 * p + 16 * h + (i < 16 ? i : 32 + (i - 16));
   }
   HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
-    const uint8_t* sb = mat + ((int64_t)row * (K / 256) + (c >> 3)) * 144;
+    const uint8_t* sb = q4k_sb(mat, R, K, row, c >> 3);
     int cc = c & 7;
     r.hdr = *(const uint4*)sb;
     r.q = *(const uint4*)(sb + 16 + 32 * (cc >> 1) + 16 * (cc & 1));

@@ -61,7 +61,7 @@ struct PRaw<HX_Q4_K> {
   uint4 hdr, q0, q1;
   int c;
   HX_DEV void load(const uint8_t* mat, int R, int K, int row, int kc, int pt) {
-    const uint8_t* p = mat + ((int64_t)row * (K / 256) + (kc >> 1)) * 144;
+    const uint8_t* p = q4k_sb(mat, R, K, row, kc >> 1);
     c = 2 * (kc & 1) + pt;
     hdr = *(const uint4*)p;
     q0 = *(const uint4*)(p + 16 + 32 * c);
@@ -307,7 +307,9 @@ struct QStage {
 };
 
 // Per-thread DMA sources of chunk 0; chunk kc adds 256 kc bytes to the A
-// sources and (kc / 2) 144 bytes (+ 64 for odd kc on qs pieces) to the B ones.
+// sources and (kc / 2) 64 * 144 bytes (+ 64 for odd kc on qs pieces) to the B
+// ones (the weight rows n0 .. n0 + 63 are one full group of the stored layout:
+// each superblock of the 64 rows one contiguous 9,216-byte run).
 // A: thread t moves piece t % 16 (stored at slot t % 16, holding K segment
 // (t % 16) ^ (row % 16)) of rows t / 16 + (NT / 16) i.  B: piece q = NT i + t
 // is part q % 5 of weight row q / 5: the header (part 0) or 16 qs bytes
@@ -321,7 +323,7 @@ struct Q4kSrc {
 
 template <class Q>
 HX_DEV Q4kSrc<Q> q4k_sources(const uint16_t* xh, int H, const int* rowsrc, const uint8_t* G, const uint8_t* U,
-                             int n0, int K) {
+                             int n0, int R, int K) {
   const int tid = threadIdx.x;
   Q4kSrc<Q> src;
   const int sl = tid & 15, r0 = tid >> 4, seg = sl ^ (r0 & 15);
@@ -332,7 +334,7 @@ HX_DEV Q4kSrc<Q> q4k_sources(const uint16_t* xh, int H, const int* rowsrc, const
   for (int i = 0; i < Q::NBI; i++) {
     const int q = i * Q::NT + tid < Q::BPIECES ? i * Q::NT + tid : 0, row = q / 5, part = q - 5 * row;
     const uint8_t* mat = row < Q::COLS ? G : U;
-    const uint8_t* sbp = mat + (int64_t)(n0 + (row < Q::COLS ? row : row - Q::COLS)) * (K / 256) * 144;
+    const uint8_t* sbp = q4k_sb(mat, R, K, n0 + (row < Q::COLS ? row : row - Q::COLS), 0);
     src.b[i] = part == 0 ? sbp : sbp + 16 * part;
     src.bq |= (part != 0 ? 1u : 0u) << i;
   }
@@ -348,7 +350,8 @@ HX_DEV void q4k_issue(uint32_t lds0, int st, const Q4kSrc<Q>& src, int kc, int w
   const uint32_t sbase = lds0 + (uint32_t)(st * S::SIZE + wave_u * 64 * 16);
 #pragma unroll
   for (int i = 0; i < (MT < Q::NA ? MT : Q::NA); i++) dma16(src.a[i] + 256 * kc, sbase + (uint32_t)(i * Q::NT * 16));
-  const int hdr_off = (kc >> 1) * 144, qs_off = hdr_off + 64 * (kc & 1);
+  static_assert(Q::COLS == HX_Q4K_GROUP, "a tile's weight rows are one group of the stored layout");
+  const int hdr_off = (kc >> 1) * (HX_Q4K_GROUP * 144), qs_off = hdr_off + 64 * (kc & 1);
 #pragma unroll
   for (int i = 0; i < Q::NBI; i++) {
     if (i * Q::NT + 64 * wave_u >= Q::BPIECES) break;   // the last round may cover fewer waves
@@ -539,7 +542,7 @@ __global__ __launch_bounds__(64 * NW, 3) void k_gate_up_q4k(ExpertArgs a) {
   __syncthreads();
   const int lane = lane_id(), wave = threadIdx.x >> 6, l16 = lane & 15, kq = lane >> 4;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  const Q4kSrc<Q> src = q4k_sources<Q>(a.xh, a.H, rowsrc, G, U, n0, K);
+  const Q4kSrc<Q> src = q4k_sources<Q>(a.xh, a.H, rowsrc, G, U, n0, sh ? a.Is : a.I, K);
   // dequantisation constants, kept in registers for v_and_or_b32
   const uint32_t knib = __builtin_amdgcn_readfirstlane(0x000F000Fu), kbyte = __builtin_amdgcn_readfirstlane(0x00FF00FFu);
   uint32_t kmagic;

@@ -401,6 +401,18 @@ __global__ __launch_bounds__(256) void k_repack_q6_k(const uint8_t* src, int64_t
   d[1] = s[209];
 }
 
+// GGUF Q4_K rows -> the stored layout of q4k_sb: one thread per superblock
+__global__ __launch_bounds__(256) void k_repack_q4_k(const uint8_t* src, int64_t count, int64_t rows, int64_t K,
+                                                     uint8_t* dst, int64_t dst_stride) {
+  const int64_t nb_row = K / 256, nb_mat = rows * nb_row;
+  const int64_t b = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (b >= count * nb_mat) return;
+  const int64_t m = b / nb_mat, r = (b % nb_mat) / nb_row, j = b % nb_row;
+  const uint8_t* s = src + b * 144;   // the caller's rows: any alignment
+  uint8_t* d = (uint8_t*)q4k_sb(dst + m * dst_stride, (int)rows, (int)K, (int)r, (int)j);
+  for (int i = 0; i < 144; i++) d[i] = s[i];
+}
+
 hipError_t launch_quantize(int fmt, const float* src, int64_t rows, int64_t cols, void* dst, hipStream_t s) {
   const int64_t nb = rows * (cols / gguf_block_elems(fmt));
   const dim3 grid((unsigned)((nb + 255) / 256));
@@ -443,6 +455,10 @@ hipError_t launch_repack(int fmt, const void* src, int64_t count, int64_t rows, 
   } else if (fmt == HX_Q6_K) {
     const int64_t nb = count * rows * (K / 256);
     hipLaunchKernelGGL(k_repack_q6_k, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, s, p, count, rows, K, d,
+                       dst_stride);
+  } else if (fmt == HX_Q4_K) {
+    const int64_t nb = count * rows * (K / 256);
+    hipLaunchKernelGGL(k_repack_q4_k, dim3((unsigned)((nb + 255) / 256)), dim3(256), 0, s, p, count, rows, K, d,
                        dst_stride);
   } else {
     const int64_t packed = rows * (K / gguf_block_elems(fmt)) * gguf_block_bytes(fmt);
