@@ -179,6 +179,30 @@ struct Chunk<HX_Q4_K> {
 };
 
 // ---------------------------------------------------------------- Q6_K (planar)
+// Stored layout of a Q6_K matrix of R rows and K columns: four planes, ql
+// (K / 2 bytes a row), qh (K / 4), scales (K / 16) and d (K / 128); the first
+// three in groups of HX_Q6K_GROUP rows, piece-major inside a group -- byte o
+// of row r's part of a plane whose rows hold Wp bytes in pieces of Sp at
+//   (r / G) G Wp + (o / Sp) Gr Sp + (r % G) Sp + o % Sp,
+// Gr = min(G, R - r / G G), so that the pieces a prefill down tile's K chunk
+// reads from its 128 weight rows (32 ql and 32 qh bytes, 8 scale bytes each)
+// are contiguous runs; Sp = 32 for ql and qh, 16 for the scales (every read
+// stays inside one piece). d is row-major.
+#define HX_Q6K_GROUP 128
+HX_DEV const uint8_t* q6k_at(const uint8_t* plane, int R, int Wp, int Sp, int row, int o) {
+  const int g0 = row & ~(HX_Q6K_GROUP - 1), gr = min(HX_Q6K_GROUP, R - g0);
+  return plane + (int64_t)g0 * Wp + (int64_t)(o / Sp) * gr * Sp + (int64_t)(row - g0) * Sp + o % Sp;
+}
+HX_DEV const uint8_t* q6k_ql(const uint8_t* mat, int R, int K, int row, int o) {
+  return q6k_at(mat, R, K / 2, 32, row, o);
+}
+HX_DEV const uint8_t* q6k_qh(const uint8_t* mat, int R, int K, int row, int o) {
+  return q6k_at(mat + (int64_t)R * (K / 2), R, K / 4, 32, row, o);
+}
+HX_DEV const uint8_t* q6k_sc(const uint8_t* mat, int R, int K, int row, int o) {
+  return q6k_at(mat + (int64_t)R * (K / 2 + K / 4), R, K / 16, 16, row, o);
+}
+
 // Chunk c: superblock sb = c / 8, cc = c % 8, half n = cc / 4, a = cc % 4.
 // It covers l = 8a .. 8a+7 of the four quarters s = 0..3 of half n: elements
 // 128n + 32s + l. Bytes: ql[64n + 8a ..] (quarters 0, 2), ql[64n + 32 + 8a ..]
@@ -194,14 +218,14 @@ struct Chunk<HX_Q6_K> {
   }
   HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
     int sb = c >> 3, cc = c & 7, n = cc >> 2, a = cc & 3;
-    const uint8_t* ql = mat + (int64_t)row * (K / 2) + sb * 128 + 64 * n + 8 * a;
-    const uint8_t* qh = mat + (int64_t)R * (K / 2) + (int64_t)row * (K / 4) + sb * 64 + 32 * n + 8 * a;
+    const int o = sb * 128 + 64 * n + 8 * a;
+    const uint8_t* qh = q6k_qh(mat, R, K, row, sb * 64 + 32 * n + 8 * a);
     // the half's 8 scales as one 8-byte load; the chunk's are bytes
     // (a >> 1) + 0, 2, 4, 6 of it
-    const uint2 sc8 = *(const uint2*)(mat + (int64_t)R * (K / 2 + K / 4) + (int64_t)row * (K / 16) + sb * 16 + 8 * n);
+    const uint2 sc8 = *(const uint2*)q6k_sc(mat, R, K, row, sb * 16 + 8 * n);
     const uint16_t* d = (const uint16_t*)(mat + (int64_t)R * (K / 2 + K / 4 + K / 16)) + (int64_t)row * (K / 256) + sb;
-    r.l0 = *(const uint2*)ql;
-    r.l1 = *(const uint2*)(ql + 32);
+    r.l0 = *(const uint2*)q6k_ql(mat, R, K, row, o);
+    r.l1 = *(const uint2*)q6k_ql(mat, R, K, row, o + 32);
     r.h = *(const uint2*)qh;
     r.sc = __builtin_amdgcn_perm(sc8.y, sc8.x, 0x06040200u + 0x01010101u * (uint32_t)(a >> 1));
     r.d = *d;

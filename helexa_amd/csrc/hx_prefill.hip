@@ -138,9 +138,9 @@ struct PRaw<HX_Q6_K> {
   HX_DEV void load(const uint8_t* mat, int R, int K, int row, int kc, int p) {
     const int sb = kc >> 1, n = kc & 1;
     pt = p;
-    const uint8_t* ql = mat + (int64_t)row * (K / 2) + sb * 128 + 64 * n + 32 * pt;
-    const uint8_t* qh = mat + (int64_t)R * (K / 2) + (int64_t)row * (K / 4) + sb * 64 + 32 * n;
-    const uint8_t* s = mat + (int64_t)R * (K / 2 + K / 4) + (int64_t)row * (K / 16) + sb * 16 + 8 * n;
+    const uint8_t* ql = q6k_ql(mat, R, K, row, sb * 128 + 64 * n + 32 * pt);
+    const uint8_t* qh = q6k_qh(mat, R, K, row, sb * 64 + 32 * n);
+    const uint8_t* s = q6k_sc(mat, R, K, row, sb * 16 + 8 * n);
     l0 = *(const uint4*)ql;
     l1 = *(const uint4*)(ql + 16);
     h0 = *(const uint4*)qh;
@@ -599,8 +599,10 @@ HX_DEV void dma4(const void* g, uint32_t lds_base) {
 HX_DEV int dq_col(int c) { return 256 * (c >> 2) + 128 * ((c >> 1) & 1) + 32 * (c & 1); }
 
 // Per-thread DMA sources of chunk 0. Chunk c adds 2 dq_col(c) bytes to the A
-// sources, dq_col(c) / 2 (the ql offset 128 sb + 64 n + 32 p) to ql pieces,
-// 64 sb + 32 n to qh pieces and 16 sb + 8 n to the scales.
+// sources; the 128 weight rows n0 .. n0 + 127 are one full group of the stored
+// layout, so chunk c's ql pieces (piece c of each row) are the 4 KB run c, its
+// qh pieces (piece c / 2) the run c / 2, and its scales 8 n bytes into the
+// 2 KB run sb of 16-byte pieces.
 // A piece q = 256 i + t: row q / 8, slot q % 8 holding segment
 // (q % 8) ^ ((row / 2) % 8): segments 0..3 are K columns 8 s .. of quarter p,
 // 4..7 of quarter p + 2 (64 columns further). B piece q = 256 i + t: slot q % 4
@@ -623,18 +625,14 @@ HX_DEV DqSrc dq_sources(const uint16_t* hbf, int hstride, int p0, int rows, cons
     const int r = min(row, rows - 1);   // padding rows repeat the last row
     src.a[i] = (const uint8_t*)(hbf + (int64_t)(p0 + r) * hstride + 64 * (seg >> 2) + 8 * (seg & 3));
   }
-  const uint8_t* ql = W;
-  const uint8_t* qh = W + (int64_t)R * (DQ_K / 2);
-  const uint8_t* sc = W + (int64_t)R * (DQ_K / 2 + DQ_K / 4);
   src.bqh = 0;
 #pragma unroll
   for (int i = 0; i < 2; i++) {
     const int q = i * 256 + tid, row = q >> 2, part = (q & 3) ^ ((row >> 2) & 3);
-    src.b[i] = part < 2 ? ql + (int64_t)(n0 + row) * (DQ_K / 2) + 16 * part
-                        : qh + (int64_t)(n0 + row) * (DQ_K / 4) + 16 * (part - 2);
+    src.b[i] = part < 2 ? q6k_ql(W, R, DQ_K, n0 + row, 16 * part) : q6k_qh(W, R, DQ_K, n0 + row, 16 * (part - 2));
     src.bqh |= (part >= 2 ? 1u : 0u) << i;
   }
-  src.s = sc + (int64_t)(n0 + (tid >> 1)) * (DQ_K / 16) + 4 * (tid & 1);
+  src.s = q6k_sc(W, R, DQ_K, n0 + (tid >> 1), 4 * (tid & 1));
   return src;
 }
 
@@ -644,13 +642,14 @@ template <int NA>
 HX_DEV void dq_issue(uint32_t lds0, int st, const DqSrc& src, int c, int wave_u) {
   const uint32_t sbase = lds0 + (uint32_t)(st * DQ_STAGE);
   const int sb = c >> 2, n = (c >> 1) & 1;
-  const int aoff = 2 * dq_col(c), qloff = 128 * sb + 64 * n + 32 * (c & 1), qhoff = 64 * sb + 32 * n;
+  static_assert(HX_Q6K_GROUP == 128, "a down tile's weight rows are one group of the stored layout");
+  const int aoff = 2 * dq_col(c), qloff = c * (HX_Q6K_GROUP * 32), qhoff = (c >> 1) * (HX_Q6K_GROUP * 32);
 #pragma unroll
   for (int i = 0; i < NA; i++) dma16(src.a[i] + aoff, sbase + (uint32_t)(i * 4096 + wave_u * 1024));
 #pragma unroll
   for (int i = 0; i < 2; i++)
     dma16(src.b[i] + ((src.bqh >> i) & 1 ? qhoff : qloff), sbase + (uint32_t)(DQ_A + i * 4096 + wave_u * 1024));
-  dma4(src.s + 16 * sb + 8 * n, sbase + (uint32_t)(DQ_A + DQ_B + wave_u * 256));
+  dma4(src.s + sb * (HX_Q6K_GROUP * 16) + 8 * n, sbase + (uint32_t)(DQ_A + DQ_B + wave_u * 256));
 }
 
 // (lo4 & 0x000F000F) | 0x64006400 | (hi2 & 0x00300030): two 6-bit codes as 1024 + q

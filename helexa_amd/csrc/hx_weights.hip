@@ -390,12 +390,18 @@ __global__ __launch_bounds__(256) void k_repack_q6_k(const uint8_t* src, int64_t
   const int64_t m = b / nb_mat, r = (b % nb_mat) / nb_row, j = b % nb_row;
   const uint8_t* s = src + b * 210;
   uint8_t* mat = dst + m * dst_stride;
-  uint8_t* ql = mat + r * (K / 2) + j * 128;
-  uint8_t* qh = mat + rows * (K / 2) + r * (K / 4) + j * 64;
-  uint8_t* sc = mat + rows * (K / 2 + K / 4) + r * (K / 16) + j * 16;
+  const int R = (int)rows, KK = (int)K, row = (int)r, o = (int)j;
   uint8_t* d = mat + rows * (K / 2 + K / 4 + K / 16) + (r * nb_row + j) * 2;
-  for (int i = 0; i < 128; i++) ql[i] = s[i];
-  for (int i = 0; i < 64; i++) qh[i] = s[128 + i];
+  // planes in the stored layout of q6k_at (pieces of 32, 32 and 16 bytes)
+  for (int p = 0; p < 4; p++) {
+    uint8_t* ql = (uint8_t*)q6k_ql(mat, R, KK, row, 128 * o + 32 * p);
+    for (int i = 0; i < 32; i++) ql[i] = s[32 * p + i];
+  }
+  for (int p = 0; p < 2; p++) {
+    uint8_t* qh = (uint8_t*)q6k_qh(mat, R, KK, row, 64 * o + 32 * p);
+    for (int i = 0; i < 32; i++) qh[i] = s[128 + 32 * p + i];
+  }
+  uint8_t* sc = (uint8_t*)q6k_sc(mat, R, KK, row, 16 * o);
   for (int i = 0; i < 16; i++) sc[i] = s[192 + i];
   d[0] = s[208];
   d[1] = s[209];
