@@ -106,17 +106,20 @@ struct Chunk<HX_Q8_0> {
 
 // ---------------------------------------------------------------- Q4_K (GGUF)
 // Stored layout of a Q4_K matrix of R rows: the GGUF superblocks (144 B) in
-// groups of HX_Q4K_GROUP rows, superblock-major inside a group -- superblock
-// sb of row r at ((r / G) G nsb + sb Gr + r % G) 144, Gr = min(G, R - r / G G)
-// the rows of r's group. The same bytes as the GGUF rows, reordered at load so
-// that one superblock of a group's rows (what a prefill tile's K chunk reads
-// from its 64 weight rows) is one contiguous run: read row by row, the chunks
-// touched DRAM pages 80 bytes at a time (measured on MI355X: 4.6 against
-// 6.2 TB/s for the same bytes blocked).
+// groups of G rows, superblock-major inside a group -- superblock sb of row r
+// at ((r / G) G nsb + sb G + r % G) 144, G = the largest power of two up to
+// HX_Q4K_GROUP that divides R (64 for every shape the prefill MFMA kernels
+// take; every group full, so the offsets are shifts). The same bytes as the
+// GGUF rows, reordered at load so that one superblock of a group's rows (what
+// a prefill tile's K chunk reads from its 64 weight rows) is one contiguous
+// run: read row by row, the chunks touched DRAM pages 80 bytes at a time
+// (measured on MI355X: 4.6 against 6.2 TB/s for the same bytes blocked).
 #define HX_Q4K_GROUP 64
+HX_DEV int q4k_group_log2(int R) { return min(__builtin_ctz((unsigned)R), 6); }
 HX_DEV const uint8_t* q4k_sb(const uint8_t* mat, int R, int K, int row, int sb) {
-  const int nsb = K / 256, g0 = row & ~(HX_Q4K_GROUP - 1), gr = min(HX_Q4K_GROUP, R - g0);
-  return mat + ((int64_t)g0 * nsb + (int64_t)sb * gr + (row - g0)) * 144;
+  static_assert(HX_Q4K_GROUP == 64, "q4k_group_log2 caps at 2^6");
+  const int lg = q4k_group_log2(R), g0 = (row >> lg) << lg;
+  return mat + ((int64_t)g0 * (K / 256) + ((int64_t)sb << lg) + (row - g0)) * 144;
 }
 
 // Chunk c of a row: superblock sb = c / 8, cc = c % 8, pair p = cc / 2, half
@@ -181,17 +184,22 @@ struct Chunk<HX_Q4_K> {
 // ---------------------------------------------------------------- Q6_K (planar)
 // Stored layout of a Q6_K matrix of R rows and K columns: four planes, ql
 // (K / 2 bytes a row), qh (K / 4), scales (K / 16) and d (K / 128); the first
-// three in groups of HX_Q6K_GROUP rows, piece-major inside a group -- byte o
-// of row r's part of a plane whose rows hold Wp bytes in pieces of Sp at
-//   (r / G) G Wp + (o / Sp) Gr Sp + (r % G) Sp + o % Sp,
-// Gr = min(G, R - r / G G), so that the pieces a prefill down tile's K chunk
-// reads from its 128 weight rows (32 ql and 32 qh bytes, 8 scale bytes each)
-// are contiguous runs; Sp = 32 for ql and qh, 16 for the scales (every read
-// stays inside one piece). d is row-major.
+// three in groups of G rows, piece-major inside a group -- byte o of row r's
+// part of a plane whose rows hold Wp bytes in pieces of Sp at
+//   (r / G) G Wp + (o / Sp) G Sp + (r % G) Sp + o % Sp,
+// G = the largest power of two up to HX_Q6K_GROUP that divides R (128 for
+// every shape the prefill MFMA kernels take; every group full, so the piece
+// offset is a shift by a uniform amount -- a multiply per load there cost the
+// multi-token decode kernels 7-9 %), so that the pieces a prefill down tile's
+// K chunk reads from its 128 weight rows (32 ql and 32 qh bytes, 8 scale
+// bytes each) are contiguous runs; Sp = 32 for ql and qh, 16 for the scales
+// (every read stays inside one piece). d is row-major.
 #define HX_Q6K_GROUP 128
+HX_DEV int q6k_group_log2(int R) { return min(__builtin_ctz((unsigned)R), 7); }
 HX_DEV const uint8_t* q6k_at(const uint8_t* plane, int R, int Wp, int Sp, int row, int o) {
-  const int g0 = row & ~(HX_Q6K_GROUP - 1), gr = min(HX_Q6K_GROUP, R - g0);
-  return plane + (int64_t)g0 * Wp + (int64_t)(o / Sp) * gr * Sp + (int64_t)(row - g0) * Sp + o % Sp;
+  static_assert(HX_Q6K_GROUP == 128, "q6k_group_log2 caps at 2^7");
+  const int lg = q6k_group_log2(R), g0 = (row >> lg) << lg;
+  return plane + (int64_t)g0 * Wp + ((int64_t)(o / Sp) << lg) * Sp + (int64_t)(row - g0) * Sp + o % Sp;
 }
 HX_DEV const uint8_t* q6k_ql(const uint8_t* mat, int R, int K, int row, int o) {
   return q6k_at(mat, R, K / 2, 32, row, o);

@@ -599,10 +599,10 @@ HX_DEV void dma4(const void* g, uint32_t lds_base) {
 HX_DEV int dq_col(int c) { return 256 * (c >> 2) + 128 * ((c >> 1) & 1) + 32 * (c & 1); }
 
 // Per-thread DMA sources of chunk 0. Chunk c adds 2 dq_col(c) bytes to the A
-// sources; the 128 weight rows n0 .. n0 + 127 are one full group of the stored
-// layout, so chunk c's ql pieces (piece c of each row) are the 4 KB run c, its
-// qh pieces (piece c / 2) the run c / 2, and its scales 8 n bytes into the
-// 2 KB run sb of 16-byte pieces.
+// sources; the 128 weight rows n0 .. n0 + 127 are whole groups of G rows in the
+// stored layout, so in each group chunk c's ql pieces (piece c of each row) are
+// the run c of 32 G bytes, its qh pieces (piece c / 2) the run c / 2, and its
+// scales 8 n bytes into the run sb of 16-byte pieces.
 // A piece q = 256 i + t: row q / 8, slot q % 8 holding segment
 // (q % 8) ^ ((row / 2) % 8): segments 0..3 are K columns 8 s .. of quarter p,
 // 4..7 of quarter p + 2 (64 columns further). B piece q = 256 i + t: slot q % 4
@@ -642,7 +642,7 @@ template <int NA>
 HX_DEV void dq_issue(uint32_t lds0, int st, const DqSrc& src, int c, int wave_u) {
   const uint32_t sbase = lds0 + (uint32_t)(st * DQ_STAGE);
   const int sb = c >> 2, n = (c >> 1) & 1;
-  static_assert(HX_Q6K_GROUP == 128, "a down tile's weight rows are one group of the stored layout");
+  static_assert(128 % HX_Q6K_GROUP == 0, "a down tile's weight rows are whole groups of the stored layout");
   const int aoff = 2 * dq_col(c), qloff = c * (HX_Q6K_GROUP * 32), qhoff = (c >> 1) * (HX_Q6K_GROUP * 32);
 #pragma unroll
   for (int i = 0; i < NA; i++) dma16(src.a[i] + aoff, sbase + (uint32_t)(i * 4096 + wave_u * 1024));
