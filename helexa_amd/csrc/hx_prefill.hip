@@ -21,6 +21,7 @@
 // global loads are issued before the current chunk's MFMAs. 52 KB of LDS per
 // workgroup: three workgroups per CU.
 #include "hx_internal.h"
+#include <type_traits>
 
 namespace hx {
 
@@ -483,14 +484,21 @@ HX_DEV void q4k_main(const ExpertArgs& a, uint8_t* ring, const Q4kSrc<Q>& src, i
 #pragma unroll
   for (int c = 0; c < S::NST - 1; c++)
     if (c < nk) q4k_issue<Q, MT>(lds0, c, src, c, wave_u);
-  for (int kc = 0; kc < nk; kc++) {
+  // chunk kc: wait for its DMAs, issue chunk kc + NST - 1's, then its MFMAs;
+  // the loop takes the two chunks of a superblock per iteration (nk is even),
+  // so both parities are straight-line code and the accumulators stay in place
+  // (one parity branch per chunk made the compiler copy them back each time)
+  auto step = [&](int kc, auto par) __attribute__((always_inline)) {
     const int ahead = min(S::NST - 2, nk - 1 - kc);
     q4k_wait<Q, MT>(ahead, wave_u);
     __syncthreads();   // chunk kc is in LDS for every wave; stage (kc - 1) % NST is free
     if (kc + S::NST - 1 < nk) q4k_issue<Q, MT>(lds0, (kc + S::NST - 1) % S::NST, src, kc + S::NST - 1, wave_u);
     const lds_u8* st = (const lds_u8*)ring + (kc % S::NST) * S::SIZE;
-    if (kc & 1) q4k_compute<Q, 1, MT>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
-    else q4k_compute<Q, 0, MT>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
+    q4k_compute<Q, decltype(par)::value, MT>(st, accg, accu, wave, l16, kq, knib, kbyte, kmagic);
+  };
+  for (int kc = 0; kc < nk; kc += 2) {
+    step(kc, std::integral_constant<int, 0>{});
+    step(kc + 1, std::integral_constant<int, 1>{});
   }
   // the 16 MT x COLS f16 rows of h go through LDS (columns in the swizzled
   // order, row pitch COLS + 8) and out as 16-byte pieces
@@ -715,7 +723,9 @@ HX_DEV void dq_main(const ExpertArgs& a, uint8_t* ring, float* rws, const DqSrc&
   for (int j = 0; j < 2; j++)
 #pragma unroll
     for (int i = 0; i < MT; i++) acc[j][i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < DQ_NC; c++) {
+  // two chunks per iteration (DQ_NC is even), so both parities are
+  // straight-line code and the accumulators stay in place
+  auto step = [&](int c, auto par) __attribute__((always_inline)) {
     // chunk c (and, before chunk 0, the d dwords) has landed once at most the
     // NA + 3 DMAs of chunk c + 1 are outstanding
     if (c + 1 < DQ_NC) {
@@ -727,8 +737,12 @@ HX_DEV void dq_main(const ExpertArgs& a, uint8_t* ring, float* rws, const DqSrc&
     __syncthreads();   // chunk c is in LDS for every wave; stage (c - 1) % NST is free
     if (c + DQ_NST - 1 < DQ_NC) dq_issue<NA>(lds0, (c + DQ_NST - 1) % DQ_NST, src, c + DQ_NST - 1, wave_u);
     const lds_u8* st = (const lds_u8*)ring + (c % DQ_NST) * DQ_STAGE;
-    if (c & 1) dq_compute<1, MT>(st, dl, c >> 2, acc, wave, l16, kq, knib, kmagic, k30);
-    else dq_compute<0, MT>(st, dl, c >> 2, acc, wave, l16, kq, knib, kmagic, k30);
+    dq_compute<decltype(par)::value, MT>(st, dl, c >> 2, acc, wave, l16, kq, knib, kmagic, k30);
+  };
+  static_assert(DQ_NC % 2 == 0, "chunks come in pairs");
+  for (int c = 0; c < DQ_NC; c += 2) {
+    step(c, std::integral_constant<int, 0>{});
+    step(c + 1, std::integral_constant<int, 1>{});
   }
   if (threadIdx.x < PM) rws[threadIdx.x] = rw;
   __syncthreads();   // also: every wave is done with the ring
