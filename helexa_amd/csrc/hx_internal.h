@@ -172,7 +172,11 @@ bool route_mfma_ok(const RouterArgs& a, bool xbf, bool rbf);
 int route_mfma_splits(const RouterArgs& a);
 // also writes the f16 tokens for the MFMA expert kernels when xh is not null,
 // and clears the dispatch histogram and bitmap that launch_route_mfma fills
-hipError_t launch_router_mfma(const RouterArgs& a, uint16_t* xh, hipStream_t s);
+hipError_t launch_router_mfma(const RouterArgs& a, uint16_t* xh, bool xnat, hipStream_t s);
+// the f16 tokens of the prefill MFMA kernels keep K in natural order for Q4_K
+// gate/up weights (their dequantisation pairs adjacent elements) and in the
+// order (0, 2, 1, 3) per group of 4 for the other formats
+inline bool xh_natural(int gate_fmt) { return gate_fmt == HX_Q4_K; }
 void launch_route_mfma(const RouterArgs& a, hipStream_t s);
 hipError_t launch_row_norms(const void* R, int E1, int H, float* out, hipStream_t s);
 

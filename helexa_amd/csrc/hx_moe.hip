@@ -529,7 +529,7 @@ static bool route_mfma(const hx_moe* m, const Plan& p) {
 static int run_router(hx_moe* m, Plan& p, hipStream_t s, uint16_t* xh = nullptr) {
   const bool xbf = m->cfg.act_dtype == HX_BF16, rbf = m->rdt == HX_BF16;
   tm_ext(m, SLOT_ROUTER, s);
-  if (route_mfma(m, p)) HX_HIP(launch_router_mfma(p.ra, xh, s));
+  if (route_mfma(m, p)) HX_HIP(launch_router_mfma(p.ra, xh, xh_natural(p.ea.gate.fmt), s));
   else launch_router(p.ra, xbf, rbf, s);
   tm_ext_done(m, SLOT_ROUTER);
   HX_HIP(hipGetLastError());

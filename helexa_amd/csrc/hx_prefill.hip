@@ -12,7 +12,10 @@
 // 0x6400 pattern (f16 1024 + u, exact) and packed f16 arithmetic. Along K the
 // elements of every group of 4 are stored in the order (0, 2, 1, 3) -- in the
 // activations and in the weights alike, so the dot products are unchanged --
-// which lets two 4-bit / 8-bit codes become an f16 pair in one operation.
+// which lets two 4-bit / 8-bit codes become an f16 pair in one operation;
+// the Q4_K gate/up kernel converts adjacent codes instead (FP8 conversion, see
+// q4k_compute), so with Q4_K gate/up weights the f16 tokens are in natural
+// order (xh_natural).
 //
 // Per K chunk of 128 the workgroup stages both operands in LDS (rows padded by
 // 16 bytes: the 16 lanes of a fragment read hit distinct banks) and issues
@@ -414,24 +417,27 @@ HX_DEV void q4k_compute(const lds_u8* st, f32x4_t (*accg)[Q::FPW_], f32x4_t (*ac
   h2_t a[NB][4], nb[NB][4];
 #pragma unroll
   for (int f = 0; f < NB; f++) q4k_scales<PAR>(hdr[f], kbyte, kmagic, a[f], nb[f]);
-  // low nibbles under the pattern 0x6400 (1024 + u), high nibbles masked in
-  // place under 0x5400 (64.0, mantissa step 1/16 there: 64 + u), both exact;
-  // no shift separates the two nibbles of a byte
-  const h2_t off_lo = h2s(-1024.0f), off_hi = h2s(-64.0f);
-  const uint32_t khi = vconst<0x00F000F0u>(), kmagic_hi = vconst<0x54005400u>();
+  // the four nibbles of a word, one per byte (the high ones shifted down), are
+  // FP8 E4M3 codes 0x0u, whose value is u 2^-9 for every u < 16 (denormal
+  // below 8), so v_cvt_scalef32_pk_f16_fp8 with scale 2^9 gives the codes of
+  // two adjacent bytes as the exact f16 pair (u, u'); then a u + nb with one
+  // rounding, as before. K is in natural order here (the tokens are stored so).
 #pragma unroll
   for (int s = 0; s < 4; s++) {
     const int g = s >> 1, hi = s & 1;
-    const uint32_t km = hi ? khi : knib, kg = hi ? kmagic_hi : kmagic;
-    const h2_t off = hi ? off_hi : off_lo;
     f16x8_t bf[NB];
 #pragma unroll
     for (int f = 0; f < NB; f++) {
       const uint32_t w0 = qs[f][g].x, w1 = qs[f][g].y;
-      bf[f] = __builtin_bit_cast(f16x8_t, make_uint4(fma_pair(and_or(w0, km, kg), a[f][s], nb[f][s], off),
-                                                     fma_pair(and_or(w0 >> 8, km, kg), a[f][s], nb[f][s], off),
-                                                     fma_pair(and_or(w1, km, kg), a[f][s], nb[f][s], off),
-                                                     fma_pair(and_or(w1 >> 8, km, kg), a[f][s], nb[f][s], off)));
+      const uint32_t n0 = (hi ? w0 >> 4 : w0) & 0x0F0F0F0Fu, n1 = (hi ? w1 >> 4 : w1) & 0x0F0F0F0Fu;
+      const h2_t u0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(n0, 512.0f, false);
+      const h2_t u1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(n0, 512.0f, true);
+      const h2_t u2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(n1, 512.0f, false);
+      const h2_t u3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(n1, 512.0f, true);
+      bf[f] = __builtin_bit_cast(f16x8_t, make_uint4(u32(__builtin_elementwise_fma(u0, a[f][s], nb[f][s])),
+                                                     u32(__builtin_elementwise_fma(u1, a[f][s], nb[f][s])),
+                                                     u32(__builtin_elementwise_fma(u2, a[f][s], nb[f][s])),
+                                                     u32(__builtin_elementwise_fma(u3, a[f][s], nb[f][s]))));
     }
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
@@ -947,7 +953,7 @@ __global__ __launch_bounds__(256) void k_down_mfma(ExpertArgs a) {
 
 // ---------------------------------------------------------------- tokens -> f16
 // bf16 [T][H] -> f16 [T][H] in the swizzled element order; one thread per 8
-__global__ __launch_bounds__(256) void k_x_to_f16(const uint16_t* x, int64_t n8, uint16_t* xh) {
+__global__ __launch_bounds__(256) void k_x_to_f16(const uint16_t* x, int64_t n8, uint16_t* xh, int nat) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= n8) return;
   const uint4 v = ((const uint4*)x)[i];
@@ -958,11 +964,15 @@ __global__ __launch_bounds__(256) void k_x_to_f16(const uint16_t* x, int64_t n8,
     const h2_t p = {(_Float16)__uint_as_float(w[j] << 16), (_Float16)__uint_as_float(w[j] & 0xffff0000u)};
     h[j] = u32(p);
   }
-  uint4 o;   // (e0,e1)(e2,e3) -> (e0,e2)(e1,e3)
-  o.x = __builtin_amdgcn_perm(h[1], h[0], 0x05040100u);
-  o.y = __builtin_amdgcn_perm(h[1], h[0], 0x07060302u);
-  o.z = __builtin_amdgcn_perm(h[3], h[2], 0x05040100u);
-  o.w = __builtin_amdgcn_perm(h[3], h[2], 0x07060302u);
+  uint4 o;   // natural, or (e0,e1)(e2,e3) -> (e0,e2)(e1,e3)
+  if (nat) {
+    o = make_uint4(h[0], h[1], h[2], h[3]);
+  } else {
+    o.x = __builtin_amdgcn_perm(h[1], h[0], 0x05040100u);
+    o.y = __builtin_amdgcn_perm(h[1], h[0], 0x07060302u);
+    o.z = __builtin_amdgcn_perm(h[3], h[2], 0x05040100u);
+    o.w = __builtin_amdgcn_perm(h[3], h[2], 0x07060302u);
+  }
   ((uint4*)xh)[i] = o;
 }
 
@@ -974,7 +984,8 @@ bool prefill_mfma_ok(const ExpertArgs& a) {
 
 hipError_t launch_x_to_f16(const ExpertArgs& a, hipStream_t s) {
   const int64_t n8 = (int64_t)a.T * a.H / 8;
-  hx_launch(k_x_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, (const uint16_t*)a.x, n8, a.xh);
+  hx_launch(k_x_to_f16, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, (const uint16_t*)a.x, n8, a.xh,
+            xh_natural(a.gate.fmt) ? 1 : 0);
   return hipGetLastError();
 }
 

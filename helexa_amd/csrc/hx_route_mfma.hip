@@ -77,8 +77,9 @@ constexpr int RM_AHEAD = 2;
 // Two jobs ride along (each a null pointer when not wanted): the workgroups
 // write the f16 copy of the tokens the MFMA expert kernels read, K step s by
 // the workgroup of expert block s % (expert blocks)
-// (xh: each group of 8 elements converted exactly and stored in the swizzled
-// order (e0,e2)(e1,e3)(e4,e6)(e5,e7) at its own place), and the dispatch
+// (xh: each group of 8 elements converted exactly and stored at its own place,
+// in natural order when xnat is set, else in the swizzled order
+// (e0,e2)(e1,e3)(e4,e6)(e5,e7)), and the dispatch
 // histogram and token bitmap the routing kernel fills are cleared (ndmap ints).
 //
 // Split K: grid z = s < S takes K steps s NST .. s NST + NST - 1 (NST steps of
@@ -91,7 +92,7 @@ constexpr int RM_AHEAD = 2;
 template <int NST>
 __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict__ x, const uint16_t* __restrict__ R,
                                                      int T, int H, int E, int E1, float* __restrict__ m,
-                                                     float* __restrict__ mp, uint16_t* __restrict__ xh,
+                                                     float* __restrict__ mp, uint16_t* __restrict__ xh, int xnat,
                                                      int32_t* __restrict__ dmap, int ndmap) {
   static_assert(NST % 2 == 0, "K steps come in pairs");
   __shared__ __attribute__((aligned(16))) uint8_t lds[2][2][64 * 128];   // [buffer][A / B][row * 128 + slot * 16]
@@ -151,10 +152,14 @@ __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict_
             h[j2] = (uint32_t)__builtin_bit_cast(uint16_t, lo16) | ((uint32_t)__builtin_bit_cast(uint16_t, hi16) << 16);
           }
           u32x4_t o;
-          o[0] = __builtin_amdgcn_perm(h[1], h[0], 0x05040100u);
-          o[1] = __builtin_amdgcn_perm(h[1], h[0], 0x07060302u);
-          o[2] = __builtin_amdgcn_perm(h[3], h[2], 0x05040100u);
-          o[3] = __builtin_amdgcn_perm(h[3], h[2], 0x07060302u);
+          if (xnat) {
+            o[0] = h[0]; o[1] = h[1]; o[2] = h[2]; o[3] = h[3];
+          } else {
+            o[0] = __builtin_amdgcn_perm(h[1], h[0], 0x05040100u);
+            o[1] = __builtin_amdgcn_perm(h[1], h[0], 0x07060302u);
+            o[2] = __builtin_amdgcn_perm(h[3], h[2], 0x05040100u);
+            o[3] = __builtin_amdgcn_perm(h[3], h[2], 0x07060302u);
+          }
           *(u32x4_t*)(xh + ((int64_t)tb * 64 + r) * H + 64 * (ks0 + step) + 8 * sl) = o;
         }
       }
@@ -544,7 +549,7 @@ int route_mfma_splits(const RouterArgs& a) {
   return nst % S == 0 && nst >= 4 * S && fit ? S : 1;
 }
 
-hipError_t launch_router_mfma(const RouterArgs& a, uint16_t* xh, hipStream_t s) {
+hipError_t launch_router_mfma(const RouterArgs& a, uint16_t* xh, bool xnat, hipStream_t s) {
   int32_t* dmap = a.d.hist;
   const int ndmap = dmap ? (dispatch_chunks(a.T) + dispatch_words(a.T)) * a.E : 0;
   const int S = route_mfma_splits(a), nsw = a.H / 64 / S;
@@ -553,7 +558,7 @@ hipError_t launch_router_mfma(const RouterArgs& a, uint16_t* xh, hipStream_t s) 
 #define RM(N)                                                                                                    \
   case N:                                                                                                        \
     hx_launch(k_router_mfma<N>, grid, dim3(256), 0, s, (const uint16_t*)a.x, (const uint16_t*)a.R, a.T, a.H, a.E, \
-              a.E1, a.logits, a.mplanes, xh, dmap, ndmap);                                                       \
+              a.E1, a.logits, a.mplanes, xh, xnat ? 1 : 0, dmap, ndmap);                                         \
     break;
   switch (nsw) {   // steps per workgroup: every size route_mfma_ok admits, split or not
     RM(2) RM(4) RM(6) RM(8) RM(12) RM(16) RM(24) RM(32) RM(48) RM(64)
