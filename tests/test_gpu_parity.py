@@ -309,6 +309,26 @@ def test_forward_c2_decode_q8_0(c2, T):
     assert rel_err(got, ref) <= TOL_BF16
 
 
+@pytest.mark.parametrize("H,I,gfmt,dfmt", [(256, 96, "Q4_K", "Q8_0"), (512, 96, "Q4_K", "Q8_0"),
+                                          (288, 256, "Q8_0", "Q6_K")])
+def test_blocked_layouts_partial_row_groups(H, I, gfmt, dfmt):
+    """Q4_K and Q6_K matrices are stored in row groups of the largest power of
+    two up to 64 / 128 that divides the row count: gate/up with 96 rows and
+    down with 288 rows use 32-row groups (every prefill MFMA shape uses full
+    64 / 128-row groups); decode (the fast one-token kernels at H = 512) and
+    the generic prefill read them through the same address functions"""
+    hx, synth = _hx()
+    cfg = hx.TextConfig(hidden_size=H, num_experts=16, num_experts_per_tok=4, moe_intermediate_size=I,
+                        shared_expert_intermediate_size=I, norm_topk_prob=True)
+    g, d = getattr(hx, gfmt), getattr(hx, dfmt)
+    fmt = dict(router=hx.BF16, gate=g, up=g, down=d, sgate=g, sup=g, sdown=d, seg=hx.BF16)
+    c = Case(cfg, fmt, 57, O.BF16)
+    for T in (1, 4, 40):
+        x = c.x(T, seed=T)
+        got = c.block.forward(x).float().cpu().numpy()
+        assert rel_err(got, c.oracle.forward(x_np(x))) <= TOL_BF16, (H, I, gfmt, dfmt, T)
+
+
 @pytest.mark.parametrize("pattern", [[0] * 8, [0, 0, 0, 0, 0, 1, 1, 2], [0, 1, 0, 1, 0, 1, 0, 1]])
 def test_forward_c2_decode_repeated_tokens(c2, pattern):
     """tokens that share experts: slots of several rows, which for T = 8 and
