@@ -380,8 +380,14 @@ HX_DEV void q4k_scales(const uint4& hdr, uint32_t kbyte, uint32_t kmagic, h2_t* 
   }
   const h2_t dm = h2(hdr.x), off = h2s(-1024.0f);
   const h2_t d2 = __builtin_shufflevector(dm, dm, 0, 0), nm2 = -__builtin_shufflevector(dm, dm, 1, 1);
-  const h2_t s02 = (h2(and_or(scb, kbyte, kmagic)) + off) * d2, s13 = (h2(and_or(scb >> 8, kbyte, kmagic)) + off) * d2;
-  const h2_t m02 = (h2(and_or(mb, kbyte, kmagic)) + off) * nm2, m13 = (h2(and_or(mb >> 8, kbyte, kmagic)) + off) * nm2;
+  // (1024 + v) d + (-1024 d) = v d exactly inside the fused multiply-add
+  // (-1024 d is exact: a power-of-two scale), so one rounding of v d, as from
+  // subtracting the magic first and multiplying
+  const h2_t cd = d2 * off, cm = nm2 * off;
+  const h2_t s02 = __builtin_elementwise_fma(h2(and_or(scb, kbyte, kmagic)), d2, cd);
+  const h2_t s13 = __builtin_elementwise_fma(h2(and_or(scb >> 8, kbyte, kmagic)), d2, cd);
+  const h2_t m02 = __builtin_elementwise_fma(h2(and_or(mb, kbyte, kmagic)), nm2, cm);
+  const h2_t m13 = __builtin_elementwise_fma(h2(and_or(mb >> 8, kbyte, kmagic)), nm2, cm);
   a[0] = __builtin_shufflevector(s02, s02, 0, 0);
   a[1] = __builtin_shufflevector(s13, s13, 0, 0);
   a[2] = __builtin_shufflevector(s02, s02, 1, 1);
