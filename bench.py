@@ -30,8 +30,9 @@ Method
     tokens: C2 per layer here; C3, the 512-token chunk and C5 full forwards in
     their lines, C4 B = 1 (one layer x 48) in the C3 line.
   * `prefill` (secondary): C3, 2048 tokens of the same layer in Q4_K_M (gate/up
-    Q4_K, down Q6_K), tokens/s with its MFMA and HBM fractions (`us`: 20
-    back-to-back forwards timed by HIP events on the stream; `wall_us`: the
+    Q4_K, down Q6_K), tokens/s with its MFMA and HBM fractions (`us`: 100
+    back-to-back forwards after 20 warm-up ones, timed by HIP events on the
+    stream; `wall_us`: the
     host clock around the same forwards, synchronised on both sides), and a roofline
     object for the gate/up MFMA kernel (event-timed; traced average, HBM traffic
     and MFMA counters from profiles/). `prefill_512`: the same at the
@@ -295,7 +296,7 @@ def prefill_work(cfg, fmts, T, U):
     return total_flops, total_bytes, flops, kbytes
 
 
-def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=20, bias=None, pmc_file=None, mfma_file=None,
+def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=100, bias=None, pmc_file=None, mfma_file=None,
                 trace_file=None, cpu_runs=0, c4_layer=False):
     """One prefill line: `reps` back-to-back forwards timed by HIP events on the
     stream (GPU time per forward, `us`) and by the host clock around them with a
@@ -317,7 +318,10 @@ def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=20, bias=None, pmc_
     r = blk.route(x, router_bias=bias)
     U = int(torch.unique(r["topk_idx"]).numel())
     counts = torch.diff(r["offsets"]).cpu()
-    for _ in range(2):
+    # warm-up long enough (about 8 ms of forwards) to pass the card's clock
+    # transient after idle: forwards 5-15 of a chain started from idle run up to
+    # 12 % slower than the steady state that later forwards settle to
+    for _ in range(20):
         blk.forward(x, router_bias=bias, workspace=ws, out=y)
     torch.cuda.synchronize()
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
@@ -385,7 +389,7 @@ def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=20, bias=None, pmc_
     return out
 
 
-def bench_prefill(T=2048, reps=20, cpu_runs=0):
+def bench_prefill(T=2048, reps=100, cpu_runs=0):
     """C3 (T = 2048) and the production chunk (T = 512): Q4_K_M prefill, seeded
     near-uniform routing"""
     from helexa_amd import synth
@@ -471,7 +475,7 @@ def b_rms(x, w, eps=1e-6):
     return y.to(x.dtype)
 
 
-def bench_c5(T=4096, target_share=0.40, reps=20, cpu_runs=0):
+def bench_c5(T=4096, target_share=0.40, reps=100, cpu_runs=0):
     """C5: 4096-token prefill of the Q4_K_M layer with a seeded Zipf(1.1) router
     bias (router_bias[e] = alpha ln p_{pi(e)}), alpha calibrated on this layer so
     the top 8 experts take about 40% of the assignments."""
