@@ -539,14 +539,29 @@ bool route_mfma_ok(const RouterArgs& a, bool xbf, bool rbf) {
          a.E >= 1 && a.E <= 1024 && a.k >= 1 && a.k <= 64 && a.k <= a.E;
 }
 
-// K splits of the MFMA router (logit planes): HX_RM_SPLITS when the K steps
-// of 64 divide into that many runs of at least 4 and planes 1.. fit in front of
-// the shared expert's rows of the weighted-rows buffer (row F of bf16 rows of
-// H: 2 k H bytes per token), else 1
+// K splits of the MFMA router (logit planes): the fewest of 1, 2, 4 ..
+// HX_RM_SPLITS that gives at least 512 workgroups (two per CU), among the
+// splits whose K steps of 64 divide into that many runs of at least 4 and
+// whose planes 1.. fit in front of the shared expert's rows of the
+// weighted-rows buffer (row F of bf16 rows of H: 2 k H bytes per token).
+// Measured on MI355X (E = 512, H = 2048): 512 tokens take 4 planes (256
+// workgroups; 2 planes were 3.6 us slower), 2048 tokens 2 (router + routing
+// 32.1 -> 30.6 us against 4), 4096 tokens 1 (56.4 -> 51.0 us); more
+// planes add plane traffic to both kernels, fewer leave CUs idle.
 int route_mfma_splits(const RouterArgs& a) {
-  const int nst = a.H / 64, S = HX_RM_SPLITS;
-  const bool fit = a.mplanes && (int64_t)4 * (S - 1) * a.E1 <= (int64_t)2 * a.k * a.H;
-  return nst % S == 0 && nst >= 4 * S && fit ? S : 1;
+  const int nst = a.H / 64;
+  const int64_t nwg1 = (int64_t)((a.E + 63) / 64) * (((a.T + 63) / 64 + 7) / 8 * 8);
+  auto ok = [&](int S) {
+    return S == 1 || (nst % S == 0 && nst >= 4 * S && a.mplanes &&
+                      (int64_t)4 * (S - 1) * a.E1 <= (int64_t)2 * a.k * a.H);
+  };
+  int best = 1;
+  for (int S = 1; S <= HX_RM_SPLITS; S *= 2) {
+    if (!ok(S)) break;
+    best = S;
+    if (nwg1 * S >= 512) break;
+  }
+  return best;
 }
 
 hipError_t launch_router_mfma(const RouterArgs& a, uint16_t* xh, bool xnat, hipStream_t s) {
