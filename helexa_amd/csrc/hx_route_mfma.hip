@@ -56,9 +56,11 @@ typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 // K chunks (of 32) per pair of K steps: H is a multiple of 32 RM_GROUP
 constexpr int RM_GROUP = 4;
 // K steps of 64 whose loads are in flight (a ring of RM_AHEAD + 1 register
-// buffers of 16 VGPRs). Measured on MI355X at 2048 tokens: 8 steps 19.0 us,
-// 6 18.8, 4 16.7, 3 16.2, 2 16.1 -- the registers buy more resident waves
-// than the deeper look-ahead saves.
+// buffers of 16 VGPRs). Measured on MI355X at 2048 tokens over 4 logit
+// planes: 8 steps 19.0 us, 6 18.8, 4 16.7, 3 16.2, 2 16.1 -- the registers buy
+// more resident waves than the deeper look-ahead saves; with 2 planes at 2048
+// tokens and 1 at 4096 (16 and 32 steps per workgroup) 3 and 4 steps ahead
+// measured the same as 2.
 constexpr int RM_AHEAD = 2;
 
 // Grid (E / 64 expert blocks, token blocks of 64 rounded up to 8); workgroup =
