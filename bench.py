@@ -553,8 +553,8 @@ def main():
     ap.add_argument("--no-c5", action="store_true", help="skip the skewed 4096-token prefill line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(expert-parallel sharding is described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU path (expert parallelism would "
+              "give each GPU a contiguous range of the experts; not built). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
     import torch
     if not torch.cuda.is_available():
