@@ -40,7 +40,8 @@ Method
   * `c5_skew` (secondary): C5, 4096 tokens with a Zipf(1.1) router bias
     calibrated so the top 8 experts take ~40% of the assignments.
   * `c4_stack` (secondary): C4, the 48-layer Q4_K_M stack with RMSNorm and
-    residual (attention skipped), decode at B = 1, 4, 8, per token.
+    residual (attention skipped), decode at B = 1, 4, 8, per token (one HIP
+    graph of the 48 layers per B, 50 replays after 10 warm-up ones).
 
     python bench.py [--steps K] [--warmup W] [--layers L] [--no-cpu] [--no-prefill] [--no-c4] [--no-c5]
 """
@@ -402,7 +403,7 @@ def bench_prefill(T=2048, reps=100, cpu_runs=0):
                        cpu_runs=cpu_runs, c4_layer=cpu_runs > 0 and T == 2048)
 
 
-def bench_c4(n_layers=48, batches=(1, 4, 8), reps=20):
+def bench_c4(n_layers=48, batches=(1, 4, 8), reps=50):
     """C4: 48-layer stack of the 80B-A3B MoE block in Q4_K_M with residual adds and
     attention skipped: per layer x <- x + moe(rmsnorm(x)) (decoder.rs:129-132), the
     RMSNorm weight stored as 1.0 with the reference's (1 + w) scaling
@@ -447,7 +448,9 @@ def bench_c4(n_layers=48, batches=(1, 4, 8), reps=20):
         g.replay()
         torch.cuda.synchronize()
         graph_ok = bool(torch.equal(xg, eager))
-        for _ in range(3):
+        # ten replays (10-40 ms) past the clock transient of the first few
+        # milliseconds after idle, as for the prefill lines
+        for _ in range(10):
             g.replay()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
