@@ -269,9 +269,21 @@ def cpu_baseline_c2(cfg, host0, x0, runs=50):
 
 # the routed gate/up launch is the dominant prefill kernel; the shared expert's
 # GEMMs are separate launches (template argument 2) on the handle's side stream
-PREFILL_KERNELS = {"gate_up": "k_gate_up_q4k<1, 4, 1>", "down": "k_down_q6k<1>", "router": "k_router_mfma",
-                   "route_tokens": "k_route_mfma", "shared_gate_up": "k_gate_up_q4k<1, 4, 2>",
-                   "shared_down": "k_down_q6k<2>"}
+# prefill forwards of more tokens than this run the shared expert's GEMMs on the
+# library's side stream (tile selection 1: routed, 2: shared); smaller ones fold
+# the shared tiles into the routed launches (tile selection 0), as
+# HX_SIDE_STREAM_T in helexa_amd/csrc/hx_internal.h
+SIDE_STREAM_T = 2048
+
+
+def prefill_kernels(T):
+    """kernel names of a prefill forward of T tokens, per timing slot"""
+    ts = "1" if T > SIDE_STREAM_T else "0"
+    k = {"gate_up": f"k_gate_up_q4k<1, 4, {ts}>", "down": f"k_down_q6k<{ts}>", "router": "k_router_mfma",
+         "route_tokens": "k_route_mfma"}
+    if T > SIDE_STREAM_T:
+        k.update({"shared_gate_up": "k_gate_up_q4k<1, 4, 2>", "shared_down": "k_down_q6k<2>"})
+    return k
 
 
 def prefill_work(cfg, fmts, T, U):
@@ -279,7 +291,8 @@ def prefill_work(cfg, fmts, T, U):
     kernel (each needed weight byte once; tokens in/out once; a kernel's own
     inputs and outputs: f16 tokens, f16 SwiGLU rows h, weighted bf16 rows):
     gate_up / down are the routed experts' launches, shared_* the shared
-    expert's."""
+    expert's (on the side stream above SIDE_STREAM_T tokens; below, the shared
+    tiles run in the gate_up / down launches and are counted there)."""
     H, I, Is, E, k = cfg.hidden_size, cfg.moe_intermediate_size, cfg.shared_expert_intermediate_size, \
         cfg.num_experts, cfg.num_experts_per_tok
     F = T * k
@@ -292,6 +305,10 @@ def prefill_work(cfg, fmts, T, U):
     kbytes = {"gate_up": gu_w + T * H * 2 + F * I * 2, "down": dn_w + F * I * 2 + F * H * 2,
               "shared_gate_up": sgu_w + T * H * 2 + T * Is * 2, "shared_down": sdn_w + T * Is * 2 + T * H * 2,
               "router": E * H * 2 + T * H * 2 + T * H * 2}
+    if T <= SIDE_STREAM_T:
+        for kk in ("gate_up", "down"):
+            flops[kk] += flops.pop("shared_" + kk)
+            kbytes[kk] += kbytes.pop("shared_" + kk)
     total_flops = 2 * T * k * 3 * H * I + 2 * T * 3 * H * Is + 2 * T * H * E
     total_bytes = gu_w + sgu_w + dn_w + sdn_w + (E + 1) * H * 2 + 2 * T * H * 2
     return total_flops, total_bytes, flops, kbytes
@@ -345,20 +362,22 @@ def prefill_run(cfg, fmts, w_seed, x_seed, T, workload, reps=100, bias=None, pmc
     total_flops, total_bytes, kflops, kbytes = prefill_work(cfg, fmts, T, U)
     d_us = kern.get("gate_up", float("nan"))
     tfs = kflops["gate_up"] / (d_us * 1e-6) / 1e12
-    roof = {"bound": "mfma", "kernel": "routed gate_up (" + PREFILL_KERNELS["gate_up"] + ")", "achieved": round(tfs, 1),
+    kn = prefill_kernels(T)
+    what = "routed gate_up" if T > SIDE_STREAM_T else "gate_up, routed and shared tiles"
+    roof = {"bound": "mfma", "kernel": f"{what} ({kn['gate_up']})", "achieved": round(tfs, 1),
             "peak": MFMA_BF16_PEAK_TFS, "unit": "TFLOP/s", "frac": round(tfs / MFMA_BF16_PEAK_TFS, 4),
             "algorithmic_flops_per_launch": kflops["gate_up"], "algorithmic_bytes_per_launch": kbytes["gate_up"],
             "avg_launch_us": round(d_us, 2),
             "hbm_frac": round(kbytes["gate_up"] / (d_us * 1e-6) / (HBM_PEAK_GBS * 1e9), 4)}
     if pmc_file:
-        tr = read_pmc(os.path.join(ROOT, "profiles", pmc_file), PREFILL_KERNELS["gate_up"])
+        tr = read_pmc(os.path.join(ROOT, "profiles", pmc_file), kn["gate_up"])
         roof["traffic"] = int(tr) if tr else None
         roof["traffic_source"] = f"profiles/{pmc_file} (FETCH_SIZE + WRITE_SIZE, copy-calibrated)" if tr else None
     if trace_file:
-        roof["trace_avg_us"] = read_stats_avg(os.path.join(ROOT, "profiles", trace_file), PREFILL_KERNELS["gate_up"])
+        roof["trace_avg_us"] = read_stats_avg(os.path.join(ROOT, "profiles", trace_file), kn["gate_up"])
         roof["trace_source"] = f"profiles/{trace_file}"
     if mfma_file:
-        mf = read_mfma(os.path.join(ROOT, "profiles", mfma_file), PREFILL_KERNELS["gate_up"])
+        mf = read_mfma(os.path.join(ROOT, "profiles", mfma_file), kn["gate_up"])
         if mf:
             roof["mfma_counters"] = mf
             roof["mfma_source"] = f"profiles/{mfma_file}"

@@ -156,6 +156,13 @@ struct ExpertArgs {
 #define HX_TILES_ROUTED 1
 #define HX_TILES_SHARED 2
 
+// prefill forwards of more tokens than this run the shared expert's GEMMs on
+// the handle's side stream; smaller ones fold its tiles into the routed
+// launches on the caller's stream. Measured on MI355X (A3B, Q4_K_M), one
+// stream against the side stream, paired forwards: 512 tokens -5 to -9 us,
+// 1024 -7.0, 1536 -4.2, 2048 -0.5, skewed 4096 -1.2, uniform 3072 +6.2 us.
+#define HX_SIDE_STREAM_T 2048
+
 // rows of h one decode down workgroup takes (4 waves x 6 rows each)
 constexpr int HX_XCV_WORDS = 20;
 constexpr int HX_DOWN_ROWS = 24;

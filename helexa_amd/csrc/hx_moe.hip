@@ -631,13 +631,17 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
   } else {
     const bool mfma = prefill_mfma_ok(p.ea);
     // MFMA path: one kernel per slot, each timed by its own dispatch. With a
-    // shared expert, its gate/up and down need only the f16 tokens: after the
-    // router kernel (which keeps every CU busy) they run on the side stream,
-    // next to the per-token routing and the dispatch (small kernels that leave
-    // most CUs idle), their down rows unweighted (the combine applies the
-    // sigmoid gate the routing computes); the routed GEMMs follow the dispatch
-    // on the caller's stream and the combine waits for both.
-    const bool split = mfma && m->cfg.shared_expert_intermediate_size > 0;
+    // shared expert and more than HX_SIDE_STREAM_T tokens, its gate/up and
+    // down need only the f16 tokens: after the router kernel (which keeps
+    // every CU busy) they run on the side stream, next to the per-token
+    // routing and the dispatch (small kernels that leave most CUs idle), their
+    // down rows unweighted (the combine applies the sigmoid gate the routing
+    // computes); the routed GEMMs follow the dispatch on the caller's stream
+    // and the combine waits for both. Up to HX_SIDE_STREAM_T tokens the shared
+    // tiles ride in the routed launches instead (the dispatch lists them after
+    // the routed tiles, weighted by the sigmoid gate in the down epilogue):
+    // there the fork and join cost more than the overlap gains.
+    const bool split = mfma && m->cfg.shared_expert_intermediate_size > 0 && T > HX_SIDE_STREAM_T;
     // the MFMA router writes the f16 tokens itself
     const bool xh_in_router = mfma && route_mfma(m, p);
     if (mfma && !xh_in_router) {

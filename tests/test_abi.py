@@ -68,27 +68,33 @@ def test_committed_profile_summaries_parse():
     algorithmic = 11 * 2 * 1114112 + 2 * 2048
     assert abs(traffic / algorithmic - 1.0) < 0.05
     assert 1.0 < avg_us < 100.0
-    assert read_stats_avg(os.path.join(ROOT, "profiles", "c3_prefill_kernels.txt"), "k_gate_up_q4k<1, 4, 1>") is not None
-    assert read_pmc(os.path.join(ROOT, "profiles", "c3_prefill_pmc.txt"), "k_gate_up_q4k<1, 4, 1>") is not None
-    assert read_pmc(os.path.join(ROOT, "profiles", "c5_prefill_pmc.txt"), "k_gate_up_q4k<1, 4, 1>") is not None
+    import bench
+    c3, c5 = bench.prefill_kernels(2048)["gate_up"], bench.prefill_kernels(4096)["gate_up"]
+    assert read_stats_avg(os.path.join(ROOT, "profiles", "c3_prefill_kernels.txt"), c3) is not None
+    assert read_pmc(os.path.join(ROOT, "profiles", "c3_prefill_pmc.txt"), c3) is not None
+    assert read_pmc(os.path.join(ROOT, "profiles", "c5_prefill_pmc.txt"), c5) is not None
 
 
 def test_timed_window_average_and_mfma_summaries():
     """the decode summary carries the average over the dispatches bench.py times
     (queued behind a sleep kernel), which differs from the all-dispatch one; the
     prefill MFMA summaries give f16 MFMA flops no smaller than the algorithmic
-    flops of the routed gate/up launch (2 F 2 H I at C3, F = 10 T) and of the
-    shared expert's (2 T 2 H I)"""
+    flops of the gate/up launch (at C3 the routed and the shared expert's tiles
+    in one launch, 2 (F + T) 2 H I with F = 10 T; at C5 the routed ones, the
+    shared expert's in a launch of its own on the side stream)"""
     from helexa_amd.profsum import read_mfma, read_stats_avg
     path = os.path.join(ROOT, "profiles", "c2_decode_kernels.txt")
     timed = read_stats_avg(path, "k_gate_up_dec", timed=True)
     every = read_stats_avg(path, "k_gate_up_dec", timed=False)
     assert timed is not None and every is not None and timed != every
-    T, H, I = 2048, 2048, 512
-    for name in ("c3_prefill_mfma.txt", "c5_prefill_mfma.txt"):
-        mf = read_mfma(os.path.join(ROOT, "profiles", name), "k_gate_up_q4k<1, 4, 1>")
+    import bench
+    from helexa_amd import synth
+    for name, T in (("c3_prefill_mfma.txt", 2048), ("c5_prefill_mfma.txt", 4096)):
+        kn = bench.prefill_kernels(T)
+        _, _, flops, _ = bench.prefill_work(synth.A3B, synth.FMT_Q4_K_M, T, synth.A3B.num_experts)
+        mf = read_mfma(os.path.join(ROOT, "profiles", name), kn["gate_up"])
         assert mf is not None and 0.0 < mf["mfma_util_pct"] < 100.0
-        if name.startswith("c3"):
-            assert 0.999 <= mf["mfma_flops_f16"] / (2 * 10 * T * 2 * H * I) < 1.5   # 5 digits in the file
-            ms = read_mfma(os.path.join(ROOT, "profiles", name), "k_gate_up_q4k<1, 4, 2>")
-            assert 0.999 <= ms["mfma_flops_f16"] / (2 * T * 2 * H * I) < 1.5
+        assert 0.999 <= mf["mfma_flops_f16"] / flops["gate_up"] < 1.5   # 5 digits in the file
+        if "shared_gate_up" in kn:
+            ms = read_mfma(os.path.join(ROOT, "profiles", name), kn["shared_gate_up"])
+            assert 0.999 <= ms["mfma_flops_f16"] / flops["shared_gate_up"] < 1.5
