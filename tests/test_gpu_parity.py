@@ -512,6 +512,17 @@ def test_forward_q8_0_prefill_sampled_tokens(c2):
     assert rel_err(y[sample], c2.oracle.forward(x_np(x)[sample])) <= TOL_BF16
 
 
+@pytest.mark.parametrize("T", [2048, 2049])
+def test_forward_prefill_stream_threshold(c2, T):
+    """Up to 2048 tokens the shared expert's tiles run inside the routed
+    launches on one stream; from 2049 its GEMMs run on the side stream, here
+    with a last shared tile of one row."""
+    x = c2.x(T, seed=21)
+    y = c2.block.forward(x).float().cpu().numpy()
+    sample = np.array([0, 777, 2047, T - 1])
+    assert rel_err(y[sample], c2.oracle.forward(x_np(x)[sample])) <= TOL_BF16
+
+
 def test_forward_skewed_routing_prefill(c2):
     """Zipf router bias: a few experts take most rows, so their segments span
     several 64-row M tiles (the skewed-prefill shape)."""
