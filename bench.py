@@ -11,8 +11,11 @@ Method
     the ~37 MB a step touches is never still resident in the 256 MB Infinity
     Cache when that layer comes round again.
   * The steps are captured into one HIP graph (the library launches three
-    kernels per decode step on the capturing stream) and the graph is replayed;
-    the timed region is bracketed by torch.cuda.synchronize() on both sides.
+    kernels per decode step on the capturing stream) and the graph is replayed:
+    warm-up replays (at least --warmup steps and at least 20 ms of replays, past
+    the card's clock transient), then HIP events on the replay stream around
+    exactly K steps queued right behind them (`value`); `wall_us` is the host
+    clock around the same K steps with torch.cuda.synchronize() on both sides.
   * Kernel durations for the roofline come from HIP events the library has
     recorded by each kernel's own dispatch (hx_moe_timing_*, hipExtLaunchKernel)
     on the stream it launches on, over 4 x 256 steps launched eagerly behind a
@@ -60,6 +63,7 @@ HBM_PEAK_GBS = 8000.0           # MI355X HBM3E
 MFMA_BF16_PEAK_TFS = 2516.6     # dense bf16: 256 CU x 4096 flop/clk x 2.4 GHz
 METRIC = "MoE-layer decode µs + % HBM peak; prefill tok/s + % MFMA peak (Q4_K_M)"
 KERNEL_NAMES = {"router": "k_router_dec", "gate_up": "k_gate_up_dec", "down": "k_down_dec"}
+WARM_MS = 20.0                  # least warm-up of the decode headline, in ms of graph replays
 
 
 def log(*a):
@@ -157,16 +161,38 @@ def bench_decode(args):
     steps = max(1, args.steps)
     G = max(d for d in range(1, min(256, steps) + 1) if steps % d == 0)
     g = capture(blocks, xs, ys, wss, G)
-    for _ in range(max(1, -(-args.warmup // G))):
-        g.replay()
-    torch.cuda.synchronize()
     reps = steps // G
+    # one replay (host clock) sizes the warm-up: at least --warmup steps and at
+    # least WARM_MS of replays, which carries the card past its clock
+    # transient (a chain started from idle runs slower for its first few ms)
+    g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    g.replay()
+    torch.cuda.synchronize()
+    replay_ms = (time.perf_counter() - t0) * 1e3
+    warm_reps = max(-(-args.warmup // G), int(WARM_MS / max(replay_ms, 1e-3)) + 1)
+    # timed region: the warm-up replays, then a start event, the K steps and a
+    # stop event, all queued on the replay stream without a synchronisation in
+    # between, so the K steps run back to back behind the warm-up at the clock
+    # it settled at; the events time exactly those K steps on the GPU
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    for _ in range(warm_reps):
+        g.replay()
+    ev0.record()
+    for _ in range(reps):
+        g.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    us_per_layer = ev0.elapsed_time(ev1) * 1e3 / steps
+    # the host clock around the same K steps, synchronised on both sides (adds
+    # the host's launch of the first replay)
     t0 = time.perf_counter()
     for _ in range(reps):
         g.replay()
     torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    us_per_layer = dt / steps * 1e6
+    wall_us = (time.perf_counter() - t0) / steps * 1e6
 
     # the graph's last write of ys[(G - 1) % 64] came from layer (G - 1) % L on
     # xs[(G - 1) % 64]: it must equal an eager forward bit for bit
@@ -205,7 +231,12 @@ def bench_decode(args):
 
     out = {
         "metric": METRIC, "value": round(us_per_layer, 3), "unit": "us/layer (C2 decode)",
-        "n_gpus": 1, "steps": steps, "warmup": args.warmup, "ms_per_step": round(us_per_layer / 1e3, 6),
+        "n_gpus": 1, "steps": steps, "warmup": warm_reps * G, "ms_per_step": round(us_per_layer / 1e3, 6),
+        "wall_us": round(wall_us, 3),
+        "timing": f"HIP events on the replay stream around exactly {steps} steps ({reps} replay(s) of a "
+                  f"{G}-step graph), queued directly behind {warm_reps * G} warm-up steps (at least --warmup "
+                  f"{args.warmup} and at least {WARM_MS:g} ms of replays); wall_us: host clock around the same "
+                  f"steps, synchronised on both sides",
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
         "dtype_note": "expert products f16 x f16 (Q8_0 codes exact in f16, bf16 tokens converted) with f32 "
                       "accumulation; router bf16 x bf16 f32 fmaf",

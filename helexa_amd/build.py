@@ -22,7 +22,8 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libhxmoe.so")
-SOURCES = ["hx_route.hip", "hx_route_mfma.hip", "hx_experts.hip", "hx_decode.hip", "hx_prefill.hip", "hx_weights.hip", "hx_moe.hip"]
+SOURCES = ["hx_route.hip", "hx_route_mfma.hip", "hx_experts.hip", "hx_decode.hip", "hx_prefill.hip", "hx_actq.hip",
+           "hx_weights.hip", "hx_moe.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 CFLAGS = [

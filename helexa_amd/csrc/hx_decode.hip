@@ -2,17 +2,25 @@
 //
 // Reference: Qwen3_5MLP::forward (crates/neuron/src/harness/arch/qwen3_5/mlp.rs:54-60)
 // inside the scatter loop of Module::forward (moe.rs:177-195) and
-// MaybeQuantLinear's GGUF GEMV arm (crates/neuron/src/harness/tp/tp_linear.rs:120-137).
+// MaybeQuantLinear's GGUF GEMV arm (crates/neuron/src/harness/tp/tp_linear.rs:120-137):
+// every expert call of a decode step has m = T <= 8 <= 64 rows, so the
+// reference quantises each activation row to the weight type's vec_dot type
+// (Q8_0 or Q8_K, hx_quant.h) and sums integer products of codes per block.
 //
-// Arithmetic: each quantised weight is turned into the f16 value 1024 + u, where
-// u is its unsigned code (Q8_0: q + 128; Q4_K: the nibble; Q6_K: the 6-bit
-// code), by writing u under the f16 pattern 0x6400 -- exact, one v_perm or
-// v_and_or per two weights. Activations are bf16, which converts to f16
-// exactly in f16's normal range, and the pair products go through
-// v_dot2_f32_f16 into f32. The offset is removed with the per-run activation
-// sums: sum((1024 + u) x) - (1024 + bias) sum(x) = sum((u - bias) x).
-// The SwiGLU activations between the two passes are stored as f16.
+// Arithmetic: the activation codes (integers in [-128, 127]) come as f16 pairs
+// in chunk records (hx_quant.h): the tokens' records are written by the router
+// kernel, those of the SwiGLU rows h (stored as f32) by the down kernel itself
+// (one token) or by k_hrec. Each quantised weight is turned into the f16 value
+// 1024 + u, where u is its unsigned code (Q8_0: q + 128; Q4_K: the nibble;
+// Q6_K: the 6-bit code), by writing u under the f16 pattern 0x6400 -- exact,
+// one v_perm or v_and_or per two weights -- and v_dot2_f32_f16 forms the pair
+// products into f32. All of these are integers below 2^24, so the sums are
+// exact: sum((1024 + u) q) - (1024 + bias) sum(q) = sum((u - bias) q), the
+// integer block dot product of the reference. Per chunk the float steps
+// follow: Q8_0 (d_w isum) d_x; Q4_K (d_w d_x) S - (dmin_w d_x) M with S the
+// scaled sums and M the mins times the code sums; Q6_K (d_w d_x) S.
 #include "hx_internal.h"
+#include "hx_quant.h"
 #include "hx_route_small.h"
 #include "hx_router_dev.h"
 
@@ -23,89 +31,35 @@ typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 HX_DEV half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
 HX_DEV float dot2(uint32_t w, uint32_t x, float acc) { return __builtin_amdgcn_fdot2(as_h2(w), as_h2(x), acc, false); }
 
-// two bf16 (packed) -> two f16 (packed)
-HX_DEV uint32_t bf16x2_to_f16x2(uint32_t v) {
-  float lo = __uint_as_float(v << 16), hi = __uint_as_float(v & 0xffff0000u);
-  half2_t h = {(_Float16)lo, (_Float16)hi};
-  return __builtin_bit_cast(uint32_t, h);
-}
-
-HX_DEV float f16x2_sum(uint32_t v) {
-  half2_t h = as_h2(v);
-  return (float)h.x + (float)h.y;
-}
-
-// 16 bytes of f16 (8 values) at p -> 4 packed pairs ordered (e0,e2) (e1,e3) (e4,e6) (e5,e7)
-// to match the weight pairing below (bytes i, i+2 of each dword)
-HX_DEV void pairs_from_f16x8(uint4 v, uint32_t* out) {
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};  // (e0,e1) (e2,e3) (e4,e5) (e6,e7)
-#pragma unroll
-  for (int j = 0; j < 2; j++) {
-    const uint32_t a = w[2 * j], b = w[2 * j + 1];
-    out[2 * j] = __builtin_amdgcn_perm(b, a, 0x05040100u);      // (lo a, lo b) = (e0, e2)
-    out[2 * j + 1] = __builtin_amdgcn_perm(b, a, 0x07060302u);  // (hi a, hi b) = (e1, e3)
-  }
-}
-
-// x: 8 bf16 (loaded) -> 4 f16 pairs in weight-pair order
-HX_DEV void x_pairs_bf16v(uint4 v, uint32_t* out) {
-  uint4 h;
-  h.x = bf16x2_to_f16x2(v.x);
-  h.y = bf16x2_to_f16x2(v.y);
-  h.z = bf16x2_to_f16x2(v.z);
-  h.w = bf16x2_to_f16x2(v.w);
-  pairs_from_f16x8(h, out);
-}
-// x: 8 bf16 at p -> 4 f16 pairs in weight-pair order
-HX_DEV void x_pairs_bf16(const uint16_t* p, uint32_t* out) { x_pairs_bf16v(*(const uint4*)p, out); }
-
-typedef const __attribute__((address_space(3))) uint16_t* lds_cu16;
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-HX_DEV uint4 ld16(const uint16_t* p) { return *(const uint4*)p; }
-HX_DEV uint4 ld16(lds_cu16 p) {
-  const u32x4v v = *(const __attribute__((address_space(3))) u32x4v*)p;
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-// 8 f16 at p (global or LDS) -> 4 pairs in weight-pair order
-template <class P>
-HX_DEV void x_pairs_f16(P p, uint32_t* out) { pairs_from_f16x8(ld16(p), out); }
+typedef __attribute__((address_space(3))) u32x4v lds_v4;
 
 // 4 bytes b0..b3 (already offset to unsigned) -> f16 pairs (1024+b0, 1024+b2), (1024+b1, 1024+b3)
 HX_DEV uint32_t bytes02(uint32_t q) { return __builtin_amdgcn_perm(q, 0x64646464u, 0x00060004u); }
 HX_DEV uint32_t bytes13(uint32_t q) { return __builtin_amdgcn_perm(q, 0x64646464u, 0x00070005u); }
-// nibble pairs (low nibbles of bytes 0,2) etc, as 1024 + nibble
-HX_DEV uint32_t nib02(uint32_t q) { return (q & 0x000F000Fu) | 0x64006400u; }
 
+// DChunk<FMT>: one lane's chunk of 32 weights of a row and its dot product
+// with the chunk's activation codes. xp: the record's 16 f16 code pairs; xs:
+// the code sums the format's offset correction needs (rec_sums); dx: the
+// activation block's d. Slot g of a chunk (xp[4g .. 4g + 3]) holds elements
+// x_group_off(c, g) .. + 7 of the row.
 template <int FMT>
 struct DChunk;
 
 // Q8_0 planar: chunk = one 32-weight block: 32 int8 + f16 scale
 template <>
 struct DChunk<HX_Q8_0> {
-  static constexpr int NX = 16;  // f16 pairs of activations per chunk
-  static constexpr int NS = 1;   // activation sums per chunk
+  static constexpr int NX = 16;  // f16 pairs of activation codes per chunk
+  static constexpr int NS = 1;   // code sums per chunk
   using Raw = Chunk<HX_Q8_0>::Raw;
   HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
     Chunk<HX_Q8_0>::load(mat, R, K, row, c, r);
   }
-  // activation positions: elements 32c .. 32c+31; group g of 8 -> pairs xp[4g ..]
+  // activation positions: elements 32c .. 32c+31; slot g of 8 -> pairs xp[4g ..]
   HX_DEV static int x_group_off(int c, int g) { return 32 * c + 8 * g; }
-  HX_DEV static void x_sums(const uint32_t* xp, float* xs) {
-    float s = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; i++) s += f16x2_sum(xp[i]);
-    xs[0] = s;
-  }
-  template <bool XF16, class P = const uint16_t*>
-  HX_DEV static void load_x(P xrow, int c, uint32_t* xp, float* xs) {
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-      if constexpr (XF16) x_pairs_f16(xrow + x_group_off(c, v), xp + 4 * v);
-      else x_pairs_bf16(xrow + x_group_off(c, v), xp + 4 * v);
-    }
-    x_sums(xp, xs);
-  }
-  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs) {
+  HX_DEV static void rec_sums(const float (&s)[4], float* xs) { xs[0] = (s[0] + s[1]) + (s[2] + s[3]); }
+  // isum = sum((q + 128 + 1024) x) - 1152 sum(x), exact; then (d_w isum) d_x
+  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs, float dx) {
     const uint32_t q[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
     float acc = 0.f;
 #pragma unroll
@@ -114,7 +68,7 @@ struct DChunk<HX_Q8_0> {
       acc = dot2(bytes02(u), xp[2 * j], acc);
       acc = dot2(bytes13(u), xp[2 * j + 1], acc);
     }
-    return f16_to_f32((uint16_t)r.d) * (acc - 1152.0f * xs[0]);
+    return (f16_to_f32((uint16_t)r.d) * (acc - 1152.0f * xs[0])) * dx;
   }
 };
 
@@ -126,35 +80,23 @@ struct DChunk<HX_Q4_K> {
   HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
     Chunk<HX_Q4_K>::load(mat, R, K, row, c, r);
   }
-  // activation positions: the low run (groups 0, 1) and the high run (2, 3)
+  // activation positions: the low run (slots 0, 1) and the high run (2, 3)
   HX_DEV static int x_group_off(int c, int g) {
     const int sb = c >> 3, cc = c & 7, p = cc >> 1, h = cc & 1;
     return sb * 256 + 64 * p + 16 * h + 8 * (g & 1) + 32 * (g >> 1);
   }
-  HX_DEV static void x_sums(const uint32_t* xp, float* xs) {
-    float a = 0.f, b = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      a += f16x2_sum(xp[i]);
-      b += f16x2_sum(xp[8 + i]);
-    }
-    xs[0] = a;
-    xs[1] = b;
-  }
-  template <bool XF16, class P = const uint16_t*>
-  HX_DEV static void load_x(P xrow, int c, uint32_t* xp, float* xs) {
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-      if constexpr (XF16) x_pairs_f16(xrow + x_group_off(c, g), xp + 4 * g);
-      else x_pairs_bf16(xrow + x_group_off(c, g), xp + 4 * g);
-    }
-    x_sums(xp, xs);
+  HX_DEV static void rec_sums(const float (&s)[4], float* xs) {
+    xs[0] = s[0] + s[1];
+    xs[1] = s[2] + s[3];
   }
   // low nibbles (the low run) as 1024 + u, high nibbles masked in place as
   // 1024 + 16 u (exact in f16: < 2048), so no shift separates them; the 1/16
-  // goes into the high run's scale. Scales and mins of the two runs without
-  // branches (the lanes of a wave hold different sub-blocks).
-  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs) {
+  // goes into the high run's scale (exact). Scales and mins of the two runs
+  // without branches (the lanes of a wave hold different sub-blocks).
+  // S = sc0 D0 + sc1 D1 and M = m0 X0 + m1 X1 are exact integers (D the code
+  // dot products, X the code sums of the two runs); the reference's
+  // superblock step is (d d_x) sum S - (dmin d_x) sum M.
+  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs, float dx) {
     const uint32_t kmagic = vconst<0x64006400u>(), klo = vconst<0x000F000Fu>(), khi = vconst<0x00F000F0u>();
     const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
     float lo = 0.f, hi = 0.f;
@@ -176,8 +118,9 @@ struct DChunk<HX_Q4_K> {
     const uint32_t mp = p < 2 ? a1 & 0x3F3Fu : ((a2 >> 4) & 0x0F0Fu) | ((a1 >> 2) & 0x3030u);
     const float sc0 = (float)(scp & 0xffu), sc1 = (float)((scp >> 8) & 0xffu);
     const float m0 = (float)(mp & 0xffu), m1 = (float)((mp >> 8) & 0xffu);
-    return d * (sc0 * (lo - 1024.0f * xs[0]) + (sc1 * 0.0625f) * (hi - 1024.0f * xs[1])) -
-           dmin * (m0 * xs[0] + m1 * xs[1]);
+    const float S = sc0 * (lo - 1024.0f * xs[0]) + (sc1 * 0.0625f) * (hi - 1024.0f * xs[1]);
+    const float M = m0 * xs[0] + m1 * xs[1];
+    return (d * dx) * S - (dmin * dx) * M;
   }
 };
 
@@ -194,29 +137,16 @@ struct DChunk<HX_Q6_K> {
     const int sb = c >> 3, cc = c & 7, n = cc >> 2, a = cc & 3;
     return sb * 256 + 128 * n + 8 * a + 32 * g;
   }
-  HX_DEV static void x_sums(const uint32_t* xp, float* xs) {
+  HX_DEV static void rec_sums(const float (&s)[4], float* xs) {
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-      float t = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; i++) t += f16x2_sum(xp[4 * s + i]);
-      xs[s] = t;
-    }
-  }
-  template <bool XF16, class P = const uint16_t*>
-  HX_DEV static void load_x(P xrow, int c, uint32_t* xp, float* xs) {
-#pragma unroll
-    for (int g = 0; g < 4; g++) {
-      if constexpr (XF16) x_pairs_f16(xrow + x_group_off(c, g), xp + 4 * g);
-      else x_pairs_bf16(xrow + x_group_off(c, g), xp + 4 * g);
-    }
-    x_sums(xp, xs);
+    for (int q = 0; q < 4; q++) xs[q] = s[q];
   }
   // quarters 0, 1: code = low nibble | qh bits << 4 as 1024 + code; quarters
   // 2, 3: high nibble masked in place, qh bits placed above it, as
   // 1024 + 16 code (exact in f16: < 2048), the 1/16 going into the scale.
-  // One v_and_or_b32 per merge.
-  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs) {
+  // One v_and_or_b32 per merge. S = sum of sc (code - 32) . x over the four
+  // quarters, an exact integer; the reference's step is (d d_x) S.
+  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs, float dx) {
     const uint32_t kmagic = vconst<0x64006400u>(), klo = vconst<0x000F000Fu>(), khi = vconst<0x00F000F0u>();
     const uint32_t k30 = vconst<0x00300030u>(), k300 = vconst<0x03000300u>();
     const uint32_t l0[2] = {r.l0.x, r.l0.y}, l1[2] = {r.l1.x, r.l1.y}, hh[2] = {r.h.x, r.h.y};
@@ -246,9 +176,27 @@ struct DChunk<HX_Q6_K> {
       const float sc = (float)(int8_t)((r.sc >> (8 * q)) & 0xffu);
       s = q < 2 ? __builtin_fmaf(sc, acc[q] - 1056.0f * xs[q], s) : __builtin_fmaf(sc * 0.0625f, acc[q] - 1536.0f * xs[q], s);
     }
-    return f16_to_f32((uint16_t)r.d) * s;
+    return (f16_to_f32((uint16_t)r.d) * dx) * s;
   }
 };
+
+// one chunk record (5 x 16 bytes, hx_quant.h) -> the dot's code pairs, sums and d
+template <class D>
+HX_DEV void unpack_record(const u32x4v (&v)[5], uint32_t* xp, float* xs, float& dx) {
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    xp[4 * g] = v[g][0]; xp[4 * g + 1] = v[g][1]; xp[4 * g + 2] = v[g][2]; xp[4 * g + 3] = v[g][3];
+  }
+  const uint32_t t[4] = {v[4][0], v[4][1], v[4][2], v[4][3]};
+  float s[4];
+  record_tail(t, s, dx);
+  D::rec_sums(s, xs);
+}
+template <class P>
+HX_DEV void load_record(P src, u32x4v (&v)[5]) {
+#pragma unroll
+  for (int g = 0; g < 5; g++) v[g] = src[g];
+}
 
 // the decode plan, pulled into LDS by the whole workgroup in one pass
 HX_DEV void load_plan(const ExpertArgs& a, int32_t* splan) {
@@ -257,32 +205,12 @@ HX_DEV void load_plan(const ExpertArgs& a, int32_t* splan) {
   __syncthreads();
 }
 
-// Touch one dword in each of (at most) two 128-byte lines per thread of
-// [base, base + nbytes) (<= 64 KiB per workgroup) so those lines come from HBM
-// into the caches -- the memory-side Infinity Cache keeps them for the next
-// kernel. The values are consumed only at the end of the kernel (touch_sink),
-// so the loads are in flight during the workgroup's own work.
-struct Touch {
-  uint32_t a, b;
-};
-HX_DEV Touch touch_lines(const uint8_t* base, int64_t nbytes) {
-  Touch t{0u, 0u};
-  const int64_t o0 = (int64_t)threadIdx.x * 128, o1 = o0 + 256 * 128;
-  if (o0 < nbytes) t.a = *(const uint32_t*)(base + o0);
-  if (o1 < nbytes) t.b = *(const uint32_t*)(base + o1);
-  return t;
-}
-// the condition is never true for a decode call (y is set); it keeps the loads live
-HX_DEV void touch_sink(const ExpertArgs& a, Touch t) {
-  if ((t.a ^ t.b) == 0x9e3779b9u && a.y == nullptr) ((uint32_t*)a.hbf)[0] = t.a;
-}
-
-// NR (gate, up) row pairs of one expert for a list of tokens; h stored as f16
-// BATCH: tokens may come several at a time (the single-token kernel leaves the
-// batched path out, which keeps its register count and occupancy)
-template <int FMT, int LPR, int NR, bool BATCH = true>
+// NR (gate, up) row pairs of one expert for a list of tokens: the tokens'
+// chunk records come from a.xcv (written by the router kernel); h = silu(g) u
+// is stored as f32 for the down kernels' quantisation
+template <int FMT, int LPR, int NR>
 HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U, int rows, int row0, int count,
-                         const int* tok, const int* hrow, const uint32_t* xcv = nullptr) {
+                         const int* tok, const int* hrow) {
   using D = DChunk<FMT>;
   constexpr int RG = 64 / LPR;
   const int c = lane_id() % LPR, K = a.H;
@@ -293,139 +221,76 @@ HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U
     D::load(G, rows, K, row, c, rgt[g]);
     D::load(U, rows, K, row, c, rup[g]);
   }
-  if constexpr (BATCH && LPR == 64) {
-    if (count > 1) {
-      // tokens four at a time: every activation load of the batch first, then
-      // the 4 NR (gate, up) pairs of dot products, summed by one reduce-scatter
-      constexpr int TB = 4, M = TB * NR;
-      const int lane = lane_id();
-      for (int j0 = 0; j0 < count; j0 += TB) {
-        uint32_t xp[TB][D::NX];
-        float xs[TB][D::NS];
-#pragma unroll
-        for (int jj = 0; jj < TB; jj++) {
-          const int j = min(j0 + jj, count - 1);
-          D::template load_x<false>((const uint16_t*)a.x + (int64_t)tok[j] * K, c, xp[jj], xs[jj]);
-        }
-        float pg[M], pu[M];
-#pragma unroll
-        for (int jj = 0; jj < TB; jj++)
-#pragma unroll
-          for (int g = 0; g < NR; g++) {
-            const bool ok = row0 + g * RG < rows;
-            pg[jj * NR + g] = ok ? D::dot(rgt[g], xp[jj], xs[jj]) : 0.f;
-            pu[jj * NR + g] = ok ? D::dot(rup[g], xp[jj], xs[jj]) : 0.f;
-          }
-        rs_pairs64<M>(pg, pu);
-        constexpr int SH = M == 8 ? 3 : (M == 4 ? 4 : 5);
-        const int m = lane >> SH, jj = m / NR, g = m % NR, j = j0 + jj, row = row0 + g * RG;
-        if ((lane & ((1 << SH) - 1)) == 0 && j < count && row < rows)
-          ((_Float16*)a.hbf)[(int64_t)hrow[j] * a.hstride + row] = (_Float16)(siluf_(pg[0]) * pu[0]);
-      }
-      return;
-    }
-  }
-  // token j's activations are loaded before token j - 1's dot products
-  // (token 0's together with the weights), so each load overlaps work: already
-  // converted (pairs + sums, written by the router kernel) when a.xcv is set,
-  // else raw bf16
-  const bool cv = xcv != nullptr;
+  // token j's record is loaded before token j - 1's dot products (token 0's
+  // together with the weights), so each load overlaps work
   u32x4v xr[5];
   auto xload = [&](int t) __attribute__((always_inline)) {
-    if (cv) {
-      const u32x4v* q = (const u32x4v*)(xcv + ((int64_t)t * (K / 32) + c) * HX_XCV_WORDS);
-#pragma unroll
-      for (int g = 0; g < 5; g++) xr[g] = q[g];
-    } else {
-#pragma unroll
-      for (int g = 0; g < 4; g++) xr[g] = *(const u32x4v*)((const uint16_t*)a.x + (int64_t)t * K + D::x_group_off(c, g));
-    }
+    load_record((const u32x4v*)(a.xcv + ((int64_t)t * (K / 32) + c) * HX_XCV_WORDS), xr);
   };
   xload(tok[0]);
   __builtin_amdgcn_sched_barrier(0);   // no weight arithmetic above these loads
   for (int j = 0; j < count; j++) {
     uint32_t xp[D::NX];
-    float xs[D::NS];
-    if (cv) {
-#pragma unroll
-      for (int g = 0; g < 4; g++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) xp[4 * g + i] = xr[g][i];
-#pragma unroll
-      for (int i = 0; i < D::NS; i++) xs[i] = __uint_as_float(xr[4][i]);
-    } else {
-#pragma unroll
-      for (int g = 0; g < 4; g++) x_pairs_bf16v(make_uint4(xr[g][0], xr[g][1], xr[g][2], xr[g][3]), xp + 4 * g);
-      D::x_sums(xp, xs);
-    }
+    float xs[D::NS], dx;
+    unpack_record<D>(xr, xp, xs, dx);
     if (j + 1 < count) xload(tok[j + 1]);
 #pragma unroll
     for (int g = 0; g < NR; g++) {
       const int row = row0 + g * RG;
-      float pg = row < rows ? D::dot(rgt[g], xp, xs) : 0.f;
-      float pu = row < rows ? D::dot(rup[g], xp, xs) : 0.f;
+      float pg = row < rows ? D::dot(rgt[g], xp, xs, dx) : 0.f;
+      float pu = row < rows ? D::dot(rup[g], xp, xs, dx) : 0.f;
       pg = wave_sum<LPR>(pg);
       pu = wave_sum<LPR>(pu);
-      if (c == 0 && row < rows) {
-        const float h = siluf_(pg) * pu;
-        ((_Float16*)a.hbf)[(int64_t)hrow[j] * a.hstride + row] = (_Float16)h;
-      }
+      if (c == 0 && row < rows) a.hbuf[(int64_t)hrow[j] * a.hstride + row] = siluf_(pg) * pu;
     }
   }
 }
 
 // ----------------------------------------------------------------------------
-// K1: router logits (blocks [0, nrb)) and, for T > 1, the shared expert's
-// gate/up + SwiGLU (blocks [nrb, ...)), which needs only the tokens; those
-// blocks also pull the shared down projection into the caches for K3. For
-// T == 1 the shared expert is computed inside K2 while it routes.
+// K1: router logits (blocks [0, nrb)) and the tokens' chunk records (blocks
+// nrb.., one wave per token): the token row in the router's canonical layout
+// -- with the decoder RMSNorm applied by the same code as in the router waves
+// when it is fused (one token), so the normalised row is the same bits --
+// quantised to the vec_dot type of the expert weights (hx_quant.h).
 // ----------------------------------------------------------------------------
-template <int FMT, int LPR, int NR, bool RBF, int TT>
-__global__ __launch_bounds__(256) void k_router_dec(RouterArgs r, ExpertArgs a, int nrb, int nsb) {
+template <int FMT, int NG>
+HX_DEV void x_records(const RouterArgs& r, const ExpertArgs& a, int t) {
+  const int lane = lane_id(), H = r.H;
+  uint32_t xr[1][NG][4];
+#pragma unroll
+  for (int i = 0; i < NG; i++) {
+    const uint4 v = *(const uint4*)((const uint16_t*)r.x + (int64_t)t * H + 8 * (lane + 64 * i));
+    xr[0][i][0] = v.x; xr[0][i][1] = v.y; xr[0][i][2] = v.z; xr[0][i][3] = v.w;
+  }
+  if (r.norm_w) rmsnorm_regs<1, NG>(r, xr, t);
+  uint32_t* rec = a.xcv + (int64_t)t * (H / 32) * HX_XCV_WORDS;
+#pragma unroll
+  for (int i = 0; i < NG; i++) {
+    float x[8];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      x[2 * q] = __uint_as_float(xr[0][i][q] << 16);
+      x[2 * q + 1] = __uint_as_float(xr[0][i][q] & 0xffff0000u);
+    }
+    group_to_record<FMT>(x, lane + 64 * i, rec);
+  }
+}
+
+template <int FMT, bool RBF, int TT>
+__global__ __launch_bounds__(256) void k_router_dec(RouterArgs r, ExpertArgs a, int nrb) {
   const int wave = threadIdx.x >> 6;
   if ((int)blockIdx.x < nrb) {
     constexpr int RTE = TT > 4 ? 2 : 1;   // router rows per wave
     router_rows<true, RBF, TT, RTE>(r, (blockIdx.x * 4 + wave) * RTE, 0);
     return;
   }
-  if ((int)blockIdx.x >= nrb + nsb) {
-    // token t = 4 (block - nrb - nsb) + wave: each 32-wide chunk converted once
-    // to the expert dot's f16 pairs and activation sums, for k_gate_up_plan
-    using D = DChunk<FMT>;
-    const int t = 4 * ((int)blockIdx.x - nrb - nsb) + wave, nc = a.H / 32;
-    if (t >= a.T) return;
-    for (int c = lane_id(); c < nc; c += 64) {
-      uint32_t xp[D::NX];
-      float xs[D::NS];
-      D::template load_x<false>((const uint16_t*)a.x + (int64_t)t * a.H, c, xp, xs);
-      u32x4v* q = (u32x4v*)(a.xcv + ((int64_t)t * nc + c) * HX_XCV_WORDS);
-#pragma unroll
-      for (int g = 0; g < 4; g++) q[g] = u32x4v{xp[4 * g], xp[4 * g + 1], xp[4 * g + 2], xp[4 * g + 3]};
-      u32x4v sv = {0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int i = 0; i < D::NS; i++) sv[i] = __float_as_uint(xs[i]);
-      q[4] = sv;
-    }
-    return;
+  const int t = 4 * ((int)blockIdx.x - nrb) + wave;
+  if (t >= a.T) return;
+  switch (a.H >> 9) {   // groups of 8 per lane: H / 512 (H = 512, 1024, 2048)
+    case 1: x_records<FMT, 1>(r, a, t); break;
+    case 2: x_records<FMT, 2>(r, a, t); break;
+    default: x_records<FMT, 4>(r, a, t); break;
   }
-  // shared-expert block b: rows of group b / TS for the tokens of part b % TS
-  // (above 4 tokens the tokens are split in two, so each wave's serial token
-  // loop is half as long)
-  constexpr int RG = 64 / LPR, TS = TT > 4 ? 2 : 1;
-  const int b = blockIdx.x - nrb, sb = b / TS, ts = b % TS;
-  const int64_t per = (a.sdown.mat_bytes + nsb - 1) / nsb;
-  const int64_t lo = (int64_t)b * per, n = lo + per < a.sdown.mat_bytes ? per : a.sdown.mat_bytes - lo;
-  const Touch pf = n > 0 ? touch_lines(a.sdown.base + lo, n) : Touch{0u, 0u};
-  const int tpp = (a.T + TS - 1) / TS, t0 = ts * tpp, t1 = min(a.T, t0 + tpp);
-  int tok[HX_DECODE_MAX_T], hrow[HX_DECODE_MAX_T];
-  for (int j = 0; j < t1 - t0; j++) {
-    tok[j] = t0 + j;
-    hrow[j] = a.F + t0 + j;
-  }
-  const int row0 = (sb * 4 + wave) * (RG * NR) + lane_id() / LPR;
-  if (row0 - lane_id() / LPR < a.Is && t1 > t0)
-    gate_up_rows<FMT, LPR, NR>(a, a.sgate.base, a.sup.base, a.Is, row0, t1 - t0, tok, hrow);
-  touch_sink(a, pf);
 }
 
 // ----------------------------------------------------------------------------
@@ -454,7 +319,7 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
         tok[j] = j;
         hrow[j] = a.F + j;
       }
-      gate_up_rows<FMT, LPR, NR, false>(a, a.sgate.base, a.sup.base, a.Is, r0 + lane_id() / LPR, a.T, tok, hrow);
+      gate_up_rows<FMT, LPR, NR>(a, a.sgate.base, a.sup.base, a.Is, r0 + lane_id() / LPR, a.T, tok, hrow);
     }
   }
   if (publisher && blockIdx.x > 0) return;
@@ -473,7 +338,7 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
   }
   const int row0 = (blockIdx.x * 4 + wave) * (RG * NR) + lane_id() / LPR;
   if (row0 - lane_id() / LPR < a.I)
-    gate_up_rows<FMT, LPR, NR, false>(a, a.gate.mat(e), a.up.mat(e), a.I, row0, count, tok, hrow);
+    gate_up_rows<FMT, LPR, NR>(a, a.gate.mat(e), a.up.mat(e), a.I, row0, count, tok, hrow);
 }
 
 // ----------------------------------------------------------------------------
@@ -483,11 +348,12 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
 // routes the token itself (same arithmetic as route_token_core, so all waves
 // agree; no barrier) and issues the loads of its row of the rank-r expert right
 // after round r, so the weight stream overlaps the rest of the selection; the
-// shared expert's row is loaded before routing starts. The KR + 1 dot products
-// of a wave are summed by one reduce-scatter, and wave 2i combines them with
-// wave 2i + 1's into h = silu(gate) * up, stored at the row of h of the
-// expert's dispatch position. Workgroup 0 also publishes the plan (and, unless
-// the forward asks for the plan only, the routing).
+// shared expert's row and the token's chunk record are loaded before routing
+// starts. The KR + 1 dot products of a wave are summed by one reduce-scatter,
+// and wave 2i combines them with wave 2i + 1's into h = silu(gate) * up,
+// stored (f32) at the row of h of the expert's dispatch position. Workgroup 0
+// also publishes the plan (and, unless the forward asks for the plan only,
+// the routing).
 // ----------------------------------------------------------------------------
 template <int FMT, int EPL, int KR>
 __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a) {
@@ -503,9 +369,8 @@ __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a
   float lv[EPL];
   route_logits_load<EPL>(r.logits, r.E, lv);
   const float sg = r.has_shared ? r.logits[r.E] : 0.f;
-  uint32_t xp[D::NX];
-  float xs[D::NS];
-  D::template load_x<false>((const uint16_t*)a.x, lane, xp, xs);
+  u32x4v xr[5];
+  load_record((const u32x4v*)(a.xcv + (int64_t)lane * HX_XCV_WORDS), xr);
   const bool shrow = a.Is > 0 && row < a.Is, rrow = row < a.I;
   // loads are unconditional (out-of-range rows read row 0 and are dropped at
   // the end), and a scheduling barrier after each round's loads keeps the
@@ -540,10 +405,13 @@ __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a
   int pos = 0;
 #pragma unroll
   for (int j = 0; j < KR; j++) pos += __builtin_amdgcn_readlane(my_e, j) < my_e;
+  uint32_t xp[D::NX];
+  float xs[D::NS], dx;
+  unpack_record<D>(xr, xp, xs, dx);
   float v[16];
 #pragma unroll
-  for (int j = 0; j < KR; j++) v[j] = D::dot(raw[j], xp, xs);
-  const float vs = D::dot(rsh, xp, xs);
+  for (int j = 0; j < KR; j++) v[j] = D::dot(raw[j], xp, xs, dx);
+  const float vs = D::dot(rsh, xp, xs, dx);
   v[KR] = hs ? vs : 0.f;
 #pragma unroll
   for (int j = KR + 1; j < 16; j++) v[j] = 0.f;
@@ -569,26 +437,34 @@ __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a
   __syncthreads();
   if (mat == 0 && lane <= KR) {
     const float g = sums[wave][lane], u = sums[wave + 1][lane];
-    const _Float16 h = (_Float16)(siluf_(g) * u);
-    if (lane < KR && rrow) ((_Float16*)a.hbf)[(int64_t)pos * a.hstride + row] = h;
-    if (lane == KR && shrow) ((_Float16*)a.hbf)[(int64_t)a.F * a.hstride + row] = h;
+    const float h = siluf_(g) * u;
+    if (lane < KR && rrow) a.hbuf[(int64_t)pos * a.hstride + row] = h;
+    if (lane == KR && shrow) a.hbuf[(int64_t)a.F * a.hstride + row] = h;
   }
   if (publisher) publish_route(r.d, r.topk_w, r.sgw, sm);
 }
 
 // ----------------------------------------------------------------------------
 // K2 for T > 1: the routing and plan were published by one workgroup
-// (k_route_small); grid row u computes rows of slot u's expert from the plan.
-// The shared expert's slot (the last) was computed by the router kernel.
+// (k_route_small); grid row y computes rows of one slot's expert from the
+// plan: row 0 the shared expert's slot (the plan's last; its T tokens make
+// its workgroups the longest, so they are dispatched first), rows 1.. the
+// routed slots.
 // ----------------------------------------------------------------------------
 template <int FMT, int LPR, int NR>
 __global__ __launch_bounds__(256) void k_gate_up_plan(ExpertArgs a) {
   constexpr int RG = 64 / LPR;
-  const int u = blockIdx.y;
   const int nslots = a.plan[0];
+  int u = blockIdx.y;
+  if (a.Is > 0) {
+    u = blockIdx.y == 0 ? nslots - 1 : (int)blockIdx.y - 1;
+    if (blockIdx.y > 0 && u >= nslots - 1) return;
+  } else if (u >= nslots) {
+    return;
+  }
   const int4 sr = *(const int4*)(a.plan + 4 + 4 * u);   // expert, first row, rows, first row's token
   const int e = sr.x, start = sr.y, count = sr.z;
-  if (u >= nslots || e >= a.E) return;
+  const bool sh = e == a.E;
   const int tok0 = 4 + 4 * a.max_slots;
   int tok[HX_DECODE_MAX_T], hrow[HX_DECODE_MAX_T];
   tok[0] = sr.w;
@@ -597,70 +473,65 @@ __global__ __launch_bounds__(256) void k_gate_up_plan(ExpertArgs a) {
     hrow[j] = start + j;
     tok[j] = a.plan[tok0 + start + j];
   }
+  const int rows = sh ? a.Is : a.I;
   const int wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * 4 + wave) * (RG * NR) + lane_id() / LPR;
-  if (row0 - lane_id() / LPR < a.I)
-    gate_up_rows<FMT, LPR, NR, false>(a, a.gate.mat(e), a.up.mat(e), a.I, row0, count, tok, hrow, a.xcv);
+  if (row0 - lane_id() / LPR < rows)
+    gate_up_rows<FMT, LPR, NR>(a, sh ? a.sgate.base : a.gate.mat(e), sh ? a.sup.base : a.up.mat(e), rows, row0, count,
+                               tok, hrow);
 }
 
 // ----------------------------------------------------------------------------
-// down + combine: block = RG output rows; the 4 waves split the slots; per-slot
-// contributions w * (row . h) go to LDS and are summed in slot order (experts
-// ascending, then the shared expert).
+// Rows of h (f32) -> chunk records for the down projection: one wave per row,
+// the row in the canonical layout (group g of 8 in lane g % 64, register
+// g / 64), quantised to the vec_dot type of the down weights.
 // ----------------------------------------------------------------------------
-// The expert dot's form of one 32-wide chunk of activations: its f16 pairs
-// (16 words) and activation sums (up to 4 floats), HX_XCV_WORDS words in all.
-typedef __attribute__((address_space(3))) u32x4v lds_v4;
-template <class D>
-HX_DEV void chunk_record(const u32x4v (&g4)[4], lds_v4* dst) {
-  uint32_t xp[D::NX];
-  float xs[D::NS];
+template <int FMT, int NG>
+HX_DEV void h_row_records(const float* hrow, uint32_t* rec) {
+  const int lane = lane_id();
+  float x[NG][8];
 #pragma unroll
-  for (int g = 0; g < 4; g++) pairs_from_f16x8(make_uint4(g4[g][0], g4[g][1], g4[g][2], g4[g][3]), xp + 4 * g);
-  D::x_sums(xp, xs);
-#pragma unroll
-  for (int g = 0; g < 4; g++) dst[g] = u32x4v{xp[4 * g], xp[4 * g + 1], xp[4 * g + 2], xp[4 * g + 3]};
-  u32x4v sv = {0u, 0u, 0u, 0u};
-#pragma unroll
-  for (int i = 0; i < D::NS; i++) sv[i] = __float_as_uint(xs[i]);
-  dst[4] = sv;
-}
-template <class D>
-HX_DEV void chunk_from_record(const lds_v4* src, uint32_t* xp, float* xs) {
-#pragma unroll
-  for (int g = 0; g < 4; g++) {
-    const u32x4v v = src[g];
-    xp[4 * g] = v[0]; xp[4 * g + 1] = v[1]; xp[4 * g + 2] = v[2]; xp[4 * g + 3] = v[3];
+  for (int i = 0; i < NG; i++) {
+    const float4 p = *(const float4*)(hrow + 8 * (lane + 64 * i)), q = *(const float4*)(hrow + 8 * (lane + 64 * i) + 4);
+    x[i][0] = p.x; x[i][1] = p.y; x[i][2] = p.z; x[i][3] = p.w;
+    x[i][4] = q.x; x[i][5] = q.y; x[i][6] = q.z; x[i][7] = q.w;
   }
-  const u32x4v v = src[4];
 #pragma unroll
-  for (int i = 0; i < D::NS; i++) xs[i] = __uint_as_float(v[i]);
+  for (int i = 0; i < NG; i++) group_to_record<FMT>(x[i], lane + 64 * i, rec);
 }
 
-// XLDS: the group's rows of h are staged in LDS first (many rows: each row of
-// h is read by every output-row block, and the activations then stay out of
-// the registers while the weight loads are in flight). Otherwise (one token)
-// each wave loads its activations from global memory together with its
-// weights, every load unconditional (rows past the group's end, and chunks past
-// a shorter shared expert's K, read valid data whose result is dropped) and
-// all of them issued before any is used, so the kernel makes one memory round
-// trip after the plan.
-template <int FMT, int LPR, int SPW, int NW, bool XLDS>
+// the rows of h of a forward (routed, then the shared expert's) into a.hrec
+template <int FMT, int NG>
+__global__ __launch_bounds__(256) void k_hrec(ExpertArgs a, int nrows) {
+  const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+  if (row >= nrows) return;
+  h_row_records<FMT, NG>(a.hbuf + (int64_t)row * a.hstride, a.hrec + (int64_t)row * (16 * NG) * HX_XCV_WORDS);
+}
+
+// ----------------------------------------------------------------------------
+// down + combine: block = RG output rows; the NW waves take the group's rows
+// of h SPW at a time (groups of ROWS = NW SPW rows, grid.y of them); each row's
+// contribution w * (row . h) goes to LDS, and each token's output is the sum
+// of its rows in row order (slots by ascending expert, then the shared
+// expert), as the reference's combine order; with several groups, the group's
+// partial sum, which k_down_reduce adds up in group order.
+// QH (one token, every row of h in one group): the workgroup quantises the
+// rows of h into chunk records in LDS itself -- after issuing its weight
+// loads, so the quantisation runs while the weights stream in; wave w takes
+// rows w, w + NW, ... Otherwise the records come from k_hrec and each wave
+// loads those of a row from memory right before its dot product.
+// ----------------------------------------------------------------------------
+template <int FMT, int LPR, int SPW, int NW, bool QH>
 __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
   using D = DChunk<FMT>;
-  constexpr int RG = 64 / LPR;
+  constexpr int RG = 64 / LPR, NG = LPR / 16;   // K = 32 LPR: groups of 8 per lane of a row
   constexpr int ROWS = NW * SPW;   // rows of h per group (one pass per wave)
   static_assert(ROWS <= HX_DOWN_ROWS, "groups of at most HX_DOWN_ROWS rows of h");
-  // CV (K = 512): the staged rows are converted once per workgroup, in place,
-  // into one chunk record per (row, chunk) (the RG lanes of a wave that share
-  // a chunk would otherwise each convert it)
-  constexpr bool CV = XLDS && LPR == 16;
-  // LDS: the group's rows of h (f16, Kmax each; XLDS only; with CV the larger
-  // chunk records), then per row its token, weight and expert, then the
-  // contributions [ROWS][RG]
+  // LDS: (QH) the group's chunk records [ROWS][LPR]; then per row its token,
+  // weight and expert; then the contributions [ROWS][RG]
   extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
-  const int Kmax = XLDS ? (a.I > a.Is ? a.I : a.Is) : 0;
-  int* stok = (int*)((uint8_t*)xl + (CV ? ROWS * LPR * HX_XCV_WORDS * 4 : ROWS * Kmax * 2));
+  uint32_t* srec = (uint32_t*)xl;
+  int* stok = (int*)(srec + (QH ? ROWS * LPR * HX_XCV_WORDS : 0));
   float* swt = (float*)(stok + ROWS);
   int* sexp = (int*)(swt + ROWS);
   float* contrib = (float*)(sexp + ROWS);
@@ -685,11 +556,10 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
   __syncthreads();
   const int lane = lane_id(), wave = threadIdx.x >> 6, rg = lane / LPR, c = lane % LPR;
   const int n0 = blockIdx.x * RG, row = n0 + rg;
-  // every weight (and, for one token, activation) load of the wave first,
-  // then the dot products; all unconditional (rows past the group's end, and
-  // chunks past a shorter shared expert's K, read valid data that is dropped)
+  // every weight load of the wave first, all unconditional (rows past the
+  // group's end, and chunks past a shorter shared expert's K, read valid data
+  // that is dropped)
   typename D::Raw raw[SPW];
-  uint4 xr[XLDS ? 1 : SPW][4];
 #pragma unroll
   for (int s = 0; s < SPW; s++) {
     const int hr = wave + NW * s;
@@ -699,48 +569,13 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
     const int K = sh ? a.Is : a.I;
     const int cc = c < K / 32 ? c : 0;
     D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row < a.H ? row : 0, cc, raw[s]);
-    if constexpr (!XLDS) {
-      const uint16_t* xrow = (const uint16_t*)a.hbf + (int64_t)(h0 + hq) * a.hstride;
-#pragma unroll
-      for (int g = 0; g < 4; g++) xr[s][g] = *(const uint4*)(xrow + D::x_group_off(cc, g));
-    }
   }
-  if constexpr (XLDS) {
-    // the group's rows of h into LDS by DMA, issued after the weight loads so
-    // that both arrive in one round trip. The rows are contiguous in memory
-    // (pitch hstride == Kmax) and in LDS (pitch Kmax): 16-byte piece q goes
-    // to LDS byte 16 q. A wave moves 64 pieces per instruction; ROWS Kmax / 8
-    // is a multiple of 64 (Kmax = 512, 1024, 2048), so the pieces past the
-    // group's rows land inside the staging area; their sources are clamped to
-    // the last piece.
-    const int n16 = nh * (Kmax / 8);
-    const uint16_t* src = a.hbf + (int64_t)h0 * a.hstride;
-    const uint32_t xbase = (uint32_t)(uintptr_t)(lds_u8*)xl;
-    for (int q0 = 64 * __builtin_amdgcn_readfirstlane(wave); q0 < n16; q0 += 64 * NW)
-      dma16(src + 8 * min(q0 + lane, n16 - 1), xbase + 16u * (uint32_t)q0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if constexpr (QH) {
+    __builtin_amdgcn_sched_barrier(0);   // the weight loads go out first
+    for (int hr = wave; hr < nh; hr += NW)
+      h_row_records<FMT, NG>(a.hbuf + (int64_t)(h0 + hr) * a.hstride, srec + hr * LPR * HX_XCV_WORDS);
     __syncthreads();
-    if constexpr (CV) {
-      // item q = (row q / 16, chunk q % 16): every thread reads its items' raw
-      // groups, then (after the barrier) writes their records over the rows
-      constexpr int IPT = (ROWS * LPR + 64 * NW - 1) / (64 * NW);
-      u32x4v g4[IPT][4];
-#pragma unroll
-      for (int it = 0; it < IPT; it++) {
-        const int q = min(it * 64 * NW + (int)threadIdx.x, nh * LPR - 1), hr = q / LPR, cc = q % LPR;
-#pragma unroll
-        for (int g = 0; g < 4; g++) g4[it][g] = *(const lds_v4*)(xl + hr * Kmax + D::x_group_off(cc, g));
-      }
-      __syncthreads();
-#pragma unroll
-      for (int it = 0; it < IPT; it++) {
-        const int q = it * 64 * NW + (int)threadIdx.x;
-        if (q < nh * LPR) chunk_record<D>(g4[it], (lds_v4*)xl + q * (HX_XCV_WORDS / 4));
-      }
-      __syncthreads();
-    }
   }
-  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int s = 0; s < SPW; s++) {
     const int hr = wave + NW * s;
@@ -751,26 +586,18 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
     const int K = sexp[hr] == a.E ? a.Is : a.I;
     float p = 0.f;
     if (c < K / 32) {
+      u32x4v v[5];
+      if constexpr (QH) load_record((const lds_v4*)(srec + (hr * LPR + c) * HX_XCV_WORDS), v);
+      else load_record((const u32x4v*)(a.hrec + ((int64_t)(h0 + hr) * LPR + c) * HX_XCV_WORDS), v);
       uint32_t xp[D::NX];
-      float xs[D::NS];
-      if constexpr (CV) {
-        chunk_from_record<D>((const lds_v4*)xl + (hr * LPR + c) * (HX_XCV_WORDS / 4), xp, xs);
-      } else if constexpr (XLDS) {
-        D::template load_x<true>((lds_cu16)(xl + hr * Kmax), c, xp, xs);
-      } else {
-#pragma unroll
-        for (int g = 0; g < 4; g++) pairs_from_f16x8(xr[s][g], xp + 4 * g);
-        D::x_sums(xp, xs);
-      }
-      p = D::dot(raw[s], xp, xs);
+      float xs[D::NS], dx;
+      unpack_record<D>(v, xp, xs, dx);
+      p = D::dot(raw[s], xp, xs, dx);
     }
     p = wave_sum<LPR>(p);
     if (c == 0 && row < a.H) contrib[hr * RG + rg] = swt[hr] * p;
   }
   __syncthreads();
-  // token t's output: its rows of h in order (slots by ascending expert, then
-  // the shared expert), as the reference's combine order; with several groups,
-  // the group's partial sum, which k_down_reduce adds up in group order
   for (int i = threadIdx.x; i < T * RG; i += 64 * NW) {
     const int t = i / RG, r = i % RG;
     if (n0 + r >= a.H) continue;
@@ -794,24 +621,23 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
 // down + combine for T > 1 and K = 512, pipelined: workgroup = RG output rows
 // over every row of h, taken in groups of 24 (24 / NW per wave; NW = 8 keeps
 // the registers under 128, so 4 waves share each SIMD). The weights of
-// group g + 1 (registers, two buffers) and its rows of h (registers, then LDS,
-// two buffers) are loaded while group g's dot products run, so memory and
-// arithmetic overlap; the contributions of all rows stay in LDS and each
+// group g + 1 (registers, two buffers) and its chunk records (registers, then
+// LDS, two buffers) are loaded while group g's dot products run, so memory
+// and arithmetic overlap; the contributions of all rows stay in LDS and each
 // token's output is their sum in row order (slots by ascending expert, then
 // the shared expert), written directly, with no partial sums to reduce.
 // ----------------------------------------------------------------------------
 constexpr int DP_K = 512;
 template <int FMT, int LPR, int NW>
-__global__ __launch_bounds__(64 * NW) void k_down_pipe(ExpertArgs a) {
+__global__ __launch_bounds__(64 * NW, 4) void k_down_pipe(ExpertArgs a) {
   using D = DChunk<FMT>;
   using Raw = typename D::Raw;
   constexpr int ROWS = 24, SPW = ROWS / NW, RG = 64 / LPR, NC = DP_K / 32;
   static_assert(SPW * NW == ROWS, "the waves split a group's rows of h evenly");
   static_assert(ROWS * NC <= 64 * NW, "one chunk of a group's rows of h per thread");
   constexpr int REC = HX_XCV_WORDS / 4;   // 16-byte words per chunk record
-  // LDS: chunk records of the rows of h [2][ROWS][NC] (pairs + sums, converted
-  // once per workgroup), then per row of h its token, weight and expert, then
-  // the contributions [rows of h][RG]
+  // LDS: chunk records of the rows of h [2][ROWS][NC], then per row of h its
+  // token, weight and expert, then the contributions [rows of h][RG]
   extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
   const int T = a.T, NH = a.F + T;
   const int nh_all = a.F + (a.Is > 0 ? T : 0);
@@ -842,9 +668,9 @@ __global__ __launch_bounds__(64 * NW) void k_down_pipe(ExpertArgs a) {
   const int lane = lane_id(), wave = threadIdx.x >> 6, rg = lane / LPR, c = lane % LPR;
   const int n0 = blockIdx.x * RG, row = n0 + rg;
   Raw ra[SPW], rb[SPW];
-  u32x4v xv[4];   // a native vector type, so the array stays in registers across the loop
+  u32x4v xv[REC];   // a native vector type, so the array stays in registers across the loop
   // loads of group g: the wave's SPW weight rows (rows past the end read
-  // row 0 of the group, dropped later) and this thread's chunk of h (item
+  // row 0 of the group, dropped later) and this thread's chunk record (item
   // q = thread: row q / NC, chunk q % NC; past the end, the group's last row)
   auto issue = [&](int g, Raw(&raw)[SPW]) __attribute__((always_inline)) {
     const int h0 = g * ROWS, nh = min(nh_all - h0, ROWS);
@@ -857,13 +683,15 @@ __global__ __launch_bounds__(64 * NW) void k_down_pipe(ExpertArgs a) {
       D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row < a.H ? row : 0, c < K / 32 ? c : 0, raw[s]);
     }
     const int q = min((int)threadIdx.x, nh * NC - 1), hr = q / NC, cc = q % NC;
-    const uint16_t* src = a.hbf + (int64_t)(h0 + hr) * a.hstride;
-#pragma unroll
-    for (int g = 0; g < 4; g++) xv[g] = *(const u32x4v*)(src + D::x_group_off(cc, g));
+    load_record((const u32x4v*)(a.hrec + ((int64_t)(h0 + hr) * NC + cc) * HX_XCV_WORDS), xv);
   };
   // records past the group's rows land in slots that are not read
   auto stage = [&](int g) __attribute__((always_inline)) {
-    if ((int)threadIdx.x < ROWS * NC) chunk_record<D>(xv, rec + ((g & 1) * ROWS * NC + (int)threadIdx.x) * REC);
+    if ((int)threadIdx.x < ROWS * NC) {
+      lds_v4* dst = rec + ((g & 1) * ROWS * NC + (int)threadIdx.x) * REC;
+#pragma unroll
+      for (int w = 0; w < REC; w++) dst[w] = xv[w];
+    }
   };
   auto compute = [&](int g, const Raw(&raw)[SPW]) __attribute__((always_inline)) {
     const int h0 = g * ROWS, nh = min(nh_all - h0, ROWS);
@@ -875,18 +703,20 @@ __global__ __launch_bounds__(64 * NW) void k_down_pipe(ExpertArgs a) {
       const int K = sexp[h0 + hr] == a.E ? a.Is : a.I;
       float p = 0.f;
       if (c < K / 32) {
+        u32x4v v[REC];
+        load_record(xb + (hr * NC + c) * REC, v);
         uint32_t xp[D::NX];
-        float xs[D::NS];
-        chunk_from_record<D>(xb + (hr * NC + c) * REC, xp, xs);
-        p = D::dot(raw[s], xp, xs);
+        float xs[D::NS], dx;
+        unpack_record<D>(v, xp, xs, dx);
+        p = D::dot(raw[s], xp, xs, dx);
       }
       p = wave_sum<LPR>(p);
       if (c == 0 && row < a.H) contrib[(h0 + hr) * RG + rg] = swt[h0 + hr] * p;
     }
   };
-  // group g's h goes to LDS buffer g & 1 once it has arrived; every wave has
-  // finished group g - 1 (the other user of that buffer) before any passes
-  // the barrier that precedes group g's dot products
+  // group g's records go to LDS buffer g & 1 once they have arrived; every
+  // wave has finished group g - 1 (the other user of that buffer) before any
+  // passes the barrier that precedes group g's dot products
   issue(0, ra);
   for (int g = 0; g < ng; g += 2) {
     stage(g);
@@ -935,32 +765,25 @@ bool decode_fast_ok(const ExpertArgs& a) {
     return (fmt == HX_Q8_0 || fmt == HX_Q4_K || fmt == HX_Q6_K) && (K == 512 || K == 1024 || K == 2048);
   };
   const int Kd = a.I > a.Is ? a.I : a.Is;
-  return a.xbf && ok(a.gate.fmt, a.H) && ok(a.down.fmt, Kd) && (a.Is == 0 || a.Is == a.I);
+  // one vec_dot type for the tokens (gate and up) and one for h (down)
+  const bool same = a.up.fmt == a.gate.fmt &&
+                    (a.Is == 0 || (a.sgate.fmt == a.gate.fmt && a.sup.fmt == a.gate.fmt && a.sdown.fmt == a.down.fmt));
+  return a.xbf && same && ok(a.gate.fmt, a.H) && ok(a.down.fmt, Kd) && (a.Is == 0 || a.Is == a.I);
 }
 
 template <int FMT>
 static hipError_t router_dec_fmt(const RouterArgs& r, const ExpertArgs& a, bool rbf, hipStream_t s) {
-  const int nch = a.H / 32;
-  // NR: shared-expert rows per wave (T > 1): one for up to 4 tokens, two for
-  // more (measured on MI355X: more workgroups win while the tokens are few).
-  // Above 4 tokens (about 300 registers: one workgroup per CU) each wave takes
-  // two router rows and the shared-expert tokens are split over two
-  // workgroups, so the grid (65 + 128 + xcv blocks) fits the 256 CUs at once
-  // and the shared part, which ends the kernel, is half as long per wave
-  // (measured on MI355X at T = 8: 10.1 -> 8.4 us; at T = 4 two rows per wave
-  // were slower)
-#define RD(LPR, RB, TT)                                                                     \
+  // Above 4 tokens (about 300 registers: one workgroup per CU) each wave
+  // takes two router rows, so the grid fits the 256 CUs at once. The blocks
+  // after the router's quantise the tokens (one wave each).
+#define RD(RB, TT)                                                                          \
   {                                                                                         \
-    constexpr int RG = 64 / LPR, NR = TT <= 4 ? 1 : 2, RTE = TT > 4 ? 2 : 1, TS = TT > 4 ? 2 : 1; \
-    const int nrb = (r.E1 + 4 * RTE - 1) / (4 * RTE);                                        \
-    const int nsb = a.Is > 0 && a.T > 1 ? TS * ((a.Is + 4 * RG * NR - 1) / (4 * RG * NR)) : 0; \
-    const int ncb = a.xcv && a.T > 1 ? (a.T + 3) / 4 : 0;                                   \
-    hx_launch(k_router_dec<FMT, LPR, NR, RB, TT>, dim3(nrb + nsb + ncb), dim3(256), 0, s, r, a, nrb, nsb); \
+    constexpr int RTE = TT > 4 ? 2 : 1;                                                     \
+    const int nrb = (r.E1 + 4 * RTE - 1) / (4 * RTE), ncb = (a.T + 3) / 4;                  \
+    hx_launch(k_router_dec<FMT, RB, TT>, dim3(nrb + ncb), dim3(256), 0, s, r, a, nrb);      \
   }
-#define RD_T(LPR, RB) { if (r.T <= 1) RD(LPR, RB, 1) else if (r.T <= 2) RD(LPR, RB, 2) else if (r.T <= 4) RD(LPR, RB, 4) else RD(LPR, RB, 8) }
-#define RD_R(LPR) { if (rbf) RD_T(LPR, true) else RD_T(LPR, false) }
-  if (nch == 64) RD_R(64) else if (nch == 32) RD_R(32) else RD_R(16)
-#undef RD_R
+#define RD_T(RB) { if (r.T <= 1) RD(RB, 1) else if (r.T <= 2) RD(RB, 2) else if (r.T <= 4) RD(RB, 4) else RD(RB, 8) }
+  if (rbf) RD_T(true) else RD_T(false)
 #undef RD_T
 #undef RD
   return hipGetLastError();
@@ -985,11 +808,14 @@ static hipError_t gate_up_dec_fmt(const RouterArgs& r, const ExpertArgs& a, hipS
 template <int FMT>
 static hipError_t gate_up_plan_fmt(const ExpertArgs& a, hipStream_t s) {
   const int nch = a.H / 32;
+  const int rows = a.I > a.Is ? a.I : a.Is;
   constexpr int NR = 2;
+  // grid rows: the shared expert's slot, then one per routed slot
+  // (max_slots = min(F, E) + 1 covers both)
 #define GUP(LPR)                                                                          \
   {                                                                                       \
     constexpr int RG = 64 / LPR;                                                          \
-    dim3 grid((a.I + 4 * RG * NR - 1) / (4 * RG * NR), a.max_slots);                      \
+    dim3 grid((rows + 4 * RG * NR - 1) / (4 * RG * NR), a.max_slots);                     \
     hipLaunchKernelGGL((k_gate_up_plan<FMT, LPR, NR>), grid, dim3(256), 0, s, a);         \
   }
   if (nch == 64) GUP(64) else if (nch == 32) GUP(32) else GUP(16)
@@ -999,36 +825,42 @@ static hipError_t gate_up_plan_fmt(const ExpertArgs& a, hipStream_t s) {
 
 template <int FMT>
 static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
-  const int nch = (a.I > a.Is ? a.I : a.Is) / 32;
+  const int K = a.I > a.Is ? a.I : a.Is, nch = K / 32;
+  const int nh_all = a.F + (a.Is > 0 ? a.T : 0);
   const int groups = down_groups(a.F, a.Is > 0 ? a.T : 0);
-  const bool xlds = a.T > 1;   // one token: activations straight from global memory
-  if (xlds && a.hstride != (a.I > a.Is ? a.I : a.Is)) return hipErrorInvalidValue;   // rows of h contiguous
+  if (a.hstride != K) return hipErrorInvalidValue;   // rows of h contiguous
+  // one token with at most 12 rows of h (k <= 11): the workgroup quantises the
+  // rows of h itself; otherwise k_hrec writes their records first
+  const bool qh = a.T == 1 && nh_all <= 12;
+  if (!qh) {
+    const dim3 g((unsigned)((nh_all + 3) / 4));
+    if (nch == 64) hipLaunchKernelGGL((k_hrec<FMT, 4>), g, dim3(256), 0, s, a, nh_all);
+    else if (nch == 32) hipLaunchKernelGGL((k_hrec<FMT, 2>), g, dim3(256), 0, s, a, nh_all);
+    else hipLaunchKernelGGL((k_hrec<FMT, 1>), g, dim3(256), 0, s, a, nh_all);
+  }
   // every row of h in one workgroup per RG output rows, pipelined over groups
   // (measured on MI355X at T = 4 and 8: faster than the grouped kernel + the
   // partial-sum pass); the plan of all rows is read in one pass (3 rows <= 512)
-  if (xlds && nch == DP_K / 32 && 3 * (a.F + (a.Is > 0 ? a.T : 0)) <= 512) {
+  if (a.T > 1 && nch == DP_K / 32 && 3 * nh_all <= 512) {
     constexpr int LPR = DP_K / 32, RG = 64 / LPR;
-    const int nh_all = a.F + (a.Is > 0 ? a.T : 0);
     const size_t lds = (size_t)2 * 24 * (DP_K / 32) * HX_XCV_WORDS * 4 + (size_t)nh_all * (3 + RG) * 4;
     hipLaunchKernelGGL((k_down_pipe<FMT, LPR, 8>), dim3((a.H + RG - 1) / RG), dim3(512), lds, s, a);
     return hipGetLastError();
   }
-  // one token with at most 12 rows of h (k <= 11): 3 rows per wave
-  const bool small = !xlds && a.F + (a.Is > 0 ? 1 : 0) <= 12;
-#define DD(LPR)                                                                                   \
-  {                                                                                               \
-    constexpr int RG = 64 / LPR;                                                                  \
-    const int Kmax = xlds ? (a.I > a.Is ? a.I : a.Is) : 0;                                        \
-    size_t lds = (size_t)HX_DOWN_ROWS * (Kmax == 512 ? 16 * HX_XCV_WORDS * 4 : Kmax * 2) +         \
-                 (size_t)HX_DOWN_ROWS * (3 + RG) * 4;                                              \
-    const dim3 grid((a.H + RG - 1) / RG, groups);                                                   \
-    if (xlds) hipLaunchKernelGGL((k_down_dec<FMT, LPR, 6, 4, true>), grid, dim3(256), lds, s, a);   \
-    else if (small) hx_launch(k_down_dec<FMT, LPR, 3, 4, false>, grid, dim3(256), (uint32_t)lds, s, a); \
-    else hipLaunchKernelGGL((k_down_dec<FMT, LPR, 6, 4, false>), grid, dim3(256), lds, s, a);       \
+#define DD(LPR)                                                                                       \
+  {                                                                                                   \
+    constexpr int RG = 64 / LPR;                                                                      \
+    if (qh) {                                                                                         \
+      const size_t lds = (size_t)12 * LPR * HX_XCV_WORDS * 4 + (size_t)12 * (3 + RG) * 4;             \
+      hx_launch(k_down_dec<FMT, LPR, 3, 4, true>, dim3((a.H + RG - 1) / RG, 1), dim3(256), (uint32_t)lds, s, a); \
+    } else {                                                                                          \
+      const size_t lds = (size_t)HX_DOWN_ROWS * (3 + RG) * 4;                                         \
+      hipLaunchKernelGGL((k_down_dec<FMT, LPR, 6, 4, false>), dim3((a.H + RG - 1) / RG, groups), dim3(256), lds, s, a); \
+    }                                                                                                 \
   }
   if (nch == 64) DD(64) else if (nch == 32) DD(32) else DD(16)
 #undef DD
-  if (groups > 1)
+  if (!qh && groups > 1)
     hipLaunchKernelGGL(k_down_reduce, dim3((unsigned)(((int64_t)a.T * a.H + 255) / 256)), dim3(256), 0, s, a, groups);
   return hipGetLastError();
 }

@@ -1,4 +1,9 @@
-// Expert kernels: SwiGLU gate/up GEMV, down GEMV with the weighted combine.
+// Expert kernels: SwiGLU gate/up GEMV, down GEMV with the weighted combine
+// (every shape outside the fast decode and prefill MFMA kernels). For GGUF
+// weights the expert calls of m <= 64 rows read the f32 d q of the Q8 codes
+// of their tokens (k_xq_f32) and of their rows of h (k_hq_f32, in place),
+// the reference's quantised arm up to f32 rounding; larger calls compute
+// exactly in f32 (the reference's f16 arm within f16 operand rounding).
 //
 // Reference: Qwen3_5MLP::forward (crates/neuron/src/harness/arch/qwen3_5/mlp.rs:54-60),
 // the scatter loop of Module::forward (moe.rs:177-195: experts ascending,
@@ -62,6 +67,10 @@ __global__ __launch_bounds__(256) void k_gate_up(ExpertArgs a) {
   const int lane = lane_id(), wave = threadIdx.x >> 6, rg = lane / LPR, ll = lane % LPR;
   const int row_base = (blockIdx.x * 4 + wave) * (RG * NRG);
   if (row_base >= rows) return;
+  // GGUF weights, a call of m <= HX_QUANT_M rows: the reference quantises the
+  // tokens to the vec_dot type (MaybeQuantLinear, tp_linear.rs:120-137); they
+  // come as the f32 d q of their codes (k_xq_f32)
+  const bool qa = a.xq32 && count <= HX_QUANT_M;
 
   // weights first: every load of the wave is in flight before any math
   typename CK::Raw rgt[NRG][CPL], rup[NRG][CPL];
@@ -85,13 +94,15 @@ __global__ __launch_bounds__(256) void k_gate_up(ExpertArgs a) {
       const int j = tg + tok < count ? tg + tok : count - 1;
       const int t = sh ? j : a.perm[start + j] / a.k;
       hrow[tok] = sh ? a.F + j : start + j;
-      const void* xr = a.xbf ? (const void*)((const uint16_t*)a.x + (int64_t)t * K)
-                             : (const void*)((const float*)a.x + (int64_t)t * K);
+      const bool xb = a.xbf && !qa;
+      const void* xr = qa ? (const void*)(a.xq32 + (int64_t)t * K)
+                          : xb ? (const void*)((const uint16_t*)a.x + (int64_t)t * K)
+                               : (const void*)((const float*)a.x + (int64_t)t * K);
 #pragma unroll
       for (int ci = 0; ci < CPL; ci++) {
         const int c = ll + LPR * ci;
         if (c < nch) {
-          load_chunk_x<FMT>(xr, a.xbf, c, xv[tok][ci]);
+          load_chunk_x<FMT>(xr, xb, c, xv[tok][ci]);
           CK::sums(xv[tok][ci], xs[tok][ci]);
         }
       }

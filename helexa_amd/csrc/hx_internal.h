@@ -19,6 +19,11 @@
 #define HX_DECODE_MAX_T 8
 // Rows of a grouped-GEMM M tile.
 #define HX_TILE_M 64
+// Largest row count of an expert call that takes the reference's quantised
+// arm (activations quantised to the vec_dot type, integer block products):
+// QUANT_PREFILL_M_THRESHOLD (crates/neuron/src/harness/tp/tp_linear.rs:96);
+// larger calls take its f16 arm (forward_via_f16, tp_linear.rs:111-118).
+#define HX_QUANT_M 64
 
 namespace hx {
 
@@ -31,7 +36,8 @@ struct DispatchArgs {
   int32_t* inv;        // [F] or null
   int32_t* offsets;    // [E+1]
   int32_t* slots;      // [(min(F,E)+1) * 3]: expert, start position, count
-  int32_t* tiles;      // [max_tiles * 4]: slot, expert, start position, rows
+  int32_t* tiles;      // [max_tiles * 4]: rows of the expert's call (its count; T for the
+                       // shared expert), expert, start position, rows of the tile
   int32_t* counts;     // [2]: number of slots, number of tiles
   int32_t* plan;       // decode plan (written by the decode routing tail), see plan_ints()
   int max_slots;
@@ -126,8 +132,13 @@ struct ExpertArgs {
   int hstride;
   uint16_t* hbf;       // [(F+T), hstride] f16 copy (prefill: elements swizzled in groups of 4)
   uint16_t* xh;        // [T, H] f16 tokens in the swizzled order (prefill)
-  uint32_t* xcv;       // [T][H / 32][HX_XCV_WORDS] decode, T > 1: each 32-wide chunk of a token as
-                       // the expert dot's f16 pairs (16 words) + its activation sums (4 floats)
+  uint16_t* xq;        // [T, H] prefill: f16 d q of the tokens' Q8 codes (the operand of the
+                       // m <= 64 expert calls), in the order of xh
+  float* xq32;         // [T, H] generic paths: f32 d q of the tokens' Q8 codes
+  uint32_t* xcv;       // [T][H / 32][HX_XCV_WORDS] decode: each 32-wide chunk of a token quantised
+                       // to the gate/up weights' vec_dot type, as a chunk record (hx_quant.h)
+  uint32_t* hrec;      // [(F+T)][I / 32][HX_XCV_WORDS] decode: the rows of h as chunk records
+                       // (the down weights' vec_dot type)
   void* obuf;          // [(F+T), H] weighted expert outputs (prefill): bf16 for bf16
                        // activations, f32 for f32 ones
   const int32_t* inv;
@@ -163,7 +174,8 @@ struct ExpertArgs {
 // 1024 -7.0, 1536 -4.2, 2048 -0.5, skewed 4096 -1.2, uniform 3072 +6.2 us.
 #define HX_SIDE_STREAM_T 2048
 
-// rows of h one decode down workgroup takes (4 waves x 6 rows each)
+// words of a chunk record (hx_quant.h); rows of h one decode down workgroup
+// takes (4 waves x 6 rows each)
 constexpr int HX_XCV_WORDS = 20;
 constexpr int HX_DOWN_ROWS = 24;
 __host__ __device__ inline int down_groups(int F, int T) { return (F + T + HX_DOWN_ROWS - 1) / HX_DOWN_ROWS; }
@@ -203,6 +215,16 @@ hipError_t launch_down_mfma(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_gate_up_prefill(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_down_prefill(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_combine(const ExpertArgs& a, hipStream_t s);
+
+// activation quantisation (hx_actq.hip): the reference's Q8 codes of the rows
+// of the m <= 64 expert calls
+bool gguf_fmt(int fmt);
+hipError_t launch_xq_fq(const ExpertArgs& a, hipStream_t s);               // tokens -> xq (prefill)
+hipError_t launch_hq_fq(const ExpertArgs& a, int ntiles, hipStream_t s);   // h rows of m <= 64 tiles -> hbf
+hipError_t launch_xq_f32(const ExpertArgs& a, hipStream_t s);              // tokens -> xq32 (generic)
+hipError_t launch_hq_f32(const ExpertArgs& a, hipStream_t s);              // h rows of m <= 64 slots, in place
+hipError_t launch_actq_codes(int wfmt, const void* x, bool xbf, int64_t rows, int cols, int8_t* codes, float* d,
+                             hipStream_t s);
 
 // weights
 hipError_t launch_quantize(int fmt, const float* src, int64_t rows, int64_t cols, void* dst, hipStream_t s);

@@ -122,10 +122,26 @@ static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 #define HX_MAX_TOKENS ((int64_t)1 << 24)
 
 struct WsLayout {
-  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, dmap, hbuf, hbf, xh, xcv, obuf, xn, ym, dpart,
-      wpos, total;
+  size_t logits, topk_idx, topk_w, sgw, perm, inv, offsets, slots, tiles, counts, plan, dmap, hbuf, hbf, xh, xq, xq32, xcv,
+      hrec, obuf, xn, ym, dpart, wpos, total;
   int hstride, max_slots, max_tiles;
 };
+
+// which expert kernels a forward of T tokens takes: the fast decode GEMVs,
+// the prefill MFMA GEMMs, or the generic GEMVs (everything else)
+static ExpertArgs shape_args(const hx_moe* m) {
+  ExpertArgs a{};
+  a.gate = m->gate; a.up = m->up; a.down = m->down;
+  a.sgate = m->sgate; a.sup = m->sup; a.sdown = m->sdown;
+  a.E = m->cfg.num_experts; a.k = m->cfg.num_experts_per_tok; a.H = m->cfg.hidden_size;
+  a.I = m->cfg.moe_intermediate_size; a.Is = m->cfg.shared_expert_intermediate_size;
+  a.xbf = m->cfg.act_dtype == HX_BF16;
+  return a;
+}
+static bool generic_path(const hx_moe* m, int64_t T) {
+  const ExpertArgs a = shape_args(m);
+  return T <= HX_DECODE_MAX_T ? !decode_fast_ok(a) : !prefill_mfma_ok(a);
+}
 
 static WsLayout ws_layout(const hx_moe* m, int64_t T) {
   WsLayout L{};
@@ -159,7 +175,18 @@ static WsLayout ws_layout(const hx_moe* m, int64_t T) {
   const size_t act = m->cfg.act_dtype == HX_BF16 ? 2 : 4;
   L.obuf = decode ? 0 : take(act * (F + T) * H);
   L.xh = decode ? 0 : take(sizeof(uint16_t) * T * H);
-  L.xcv = decode && T > 1 ? take(sizeof(uint32_t) * (size_t)T * (H / 32) * HX_XCV_WORDS) : 0;
+  const bool generic = generic_path(m, T);
+  // the MFMA path's xq lives in the routed rows of the weighted-rows buffer,
+  // behind the router's logit planes: it is read by the gate/up kernels only,
+  // before the down kernels write those rows (the shared expert's rows, which
+  // the side stream may write meanwhile, start at row F)
+  if (!decode && !generic) {
+    const size_t at = align256(sizeof(float) * (HX_RM_SPLITS - 1) * T * m->E1), need = sizeof(uint16_t) * T * H;
+    L.xq = at + need <= act * F * H ? L.obuf + at : take(need);
+  }
+  L.xq32 = generic && gguf_fmt(m->gate.fmt) ? take(sizeof(float) * T * H) : 0;
+  L.xcv = decode ? take(sizeof(uint32_t) * (size_t)T * (H / 32) * HX_XCV_WORDS) : 0;
+  L.hrec = decode ? take(sizeof(uint32_t) * (size_t)(F + T) * ((I > Is ? I : Is) / 32) * HX_XCV_WORDS) : 0;
   L.xn = take(act * T * H);
   L.ym = take(act * T * H);
   L.dpart = decode ? take(sizeof(float) * (size_t)down_groups((int)F, (int)T) * T * H) : 0;
@@ -464,7 +491,10 @@ static void make_plan(hx_moe* m, const void* x, int64_t T, void* y, uint8_t* ws,
   a.hbf = L.hbf ? (uint16_t*)(ws + L.hbf) : nullptr;
   a.obuf = L.obuf ? (void*)(ws + L.obuf) : nullptr;
   a.xh = L.xh ? (uint16_t*)(ws + L.xh) : nullptr;
+  a.xq = L.xq ? (uint16_t*)(ws + L.xq) : nullptr;
+  a.xq32 = L.xq32 ? (float*)(ws + L.xq32) : nullptr;
   a.xcv = L.xcv ? (uint32_t*)(ws + L.xcv) : nullptr;
+  a.hrec = L.hrec ? (uint32_t*)(ws + L.hrec) : nullptr;
   a.inv = d.inv;
   a.topk_idx = d.topk_idx;
   a.y = y;
@@ -561,6 +591,21 @@ static int run_routing(hx_moe* m, Plan& p, hipStream_t s) {
   return rc ? rc : run_route_dispatch(m, p, s);
 }
 
+// the join of the side stream on every way out of a forward that forked it:
+// the join event recorded on the side stream (if the forward had not got to
+// it) and waited on by the caller's stream
+struct SideJoin {
+  hipStream_t s, side;
+  hipEvent_t ev;
+  bool armed = false, recorded = false;
+  SideJoin(hipStream_t s_, hipStream_t side_, hipEvent_t ev_) : s(s_), side(side_), ev(ev_) {}
+  ~SideJoin() {
+    if (!armed) return;
+    if (!recorded) (void)hipEventRecord(ev, side);
+    (void)hipStreamWaitEvent(s, ev, 0);
+  }
+};
+
 // the decoder's RMSNorm and residual around the block (hx_moe_decoder_mlp)
 struct DecoderFuse {
   const float* norm_w;
@@ -621,11 +666,16 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
     if (T == 1) tm_ext_done(m, SLOT_DOWN);
     else tm_mark(m, SLOT_DOWN, 1, s);
   } else if (decode) {
+    // generic GEMVs; for GGUF weights every expert call (m = T <= 8) takes the
+    // quantised arm: the tokens and then the rows of h as f32 d q of their Q8
+    // codes
     if ((rc = run_routing(m, p, s))) return rc;
     tm_mark(m, SLOT_GATE_UP, 0, s);
+    if (p.ea.xq32) HX_HIP(launch_xq_f32(p.ea, s));
     HX_HIP(launch_gate_up_gemv(p.ea, s));
     tm_mark(m, SLOT_GATE_UP, 1, s);
     tm_mark(m, SLOT_DOWN, 0, s);
+    if (gguf_fmt(p.ea.down.fmt)) HX_HIP(launch_hq_f32(p.ea, s));
     HX_HIP(launch_down_gemv_combine(p.ea, s));
     tm_mark(m, SLOT_DOWN, 1, s);
   } else {
@@ -650,36 +700,54 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
       tm_ext_done(m, SLOT_X_F16);
     }
     if ((rc = run_router(m, p, s, xh_in_router ? p.ea.xh : nullptr))) return rc;
+    // the m > 64 calls (the shared expert above 64 tokens, hot experts) read
+    // xh; the m <= 64 ones the f16 d q of the tokens' Q8 codes
+    const bool hq_shared = T <= HX_QUANT_M;   // the shared expert's call takes the quantised arm
+    // once the side stream has forked, every return joins it back (so that a
+    // failure under stream capture leaves no stream in capture state)
+    SideJoin join(s, m->side, m->ev_join);
     if (split) {
       ExpertArgs sa = p.ea;
       sa.tsel = HX_TILES_SHARED;
       sa.shared_raw = true;
       HX_HIP(hipEventRecord(m->ev_fork, s));
       HX_HIP(hipStreamWaitEvent(m->side, m->ev_fork, 0));
+      join.armed = true;
       tm_ext(m, SLOT_SH_GATE_UP, m->side);
       HX_HIP(launch_gate_up_mfma(sa, m->side));
       tm_ext_done(m, SLOT_SH_GATE_UP);
+      if (hq_shared) HX_HIP(launch_hq_fq(sa, (int)((T + HX_TILE_M - 1) / HX_TILE_M), m->side));
       tm_ext(m, SLOT_SH_DOWN, m->side);
       HX_HIP(launch_down_mfma(sa, m->side));
       tm_ext_done(m, SLOT_SH_DOWN);
       HX_HIP(hipEventRecord(m->ev_join, m->side));
+      join.recorded = true;
       p.ea.tsel = HX_TILES_ROUTED;
       p.ea.shared_raw = true;
     }
+    if (mfma) HX_HIP(launch_xq_fq(p.ea, s));
     if ((rc = run_route_dispatch(m, p, s))) return rc;
     if (mfma) {
       tm_ext(m, SLOT_GATE_UP, s);
       HX_HIP(launch_gate_up_mfma(p.ea, s));
       tm_ext_done(m, SLOT_GATE_UP);
+      HX_HIP(launch_hq_fq(p.ea, p.ea.max_tiles, s));
       tm_ext(m, SLOT_DOWN, s);
       HX_HIP(launch_down_mfma(p.ea, s));
       tm_ext_done(m, SLOT_DOWN);
-      if (split) HX_HIP(hipStreamWaitEvent(s, m->ev_join, 0));
+      if (split) {
+        join.armed = false;
+        HX_HIP(hipStreamWaitEvent(s, m->ev_join, 0));
+      }
     } else {
+      // generic GEMVs: the m <= 64 slots read the f32 d q of the tokens' and
+      // then of their rows of h's Q8 codes (GGUF weights)
       tm_mark(m, SLOT_GATE_UP, 0, s);
+      if (p.ea.xq32) HX_HIP(launch_xq_f32(p.ea, s));
       HX_HIP(launch_gate_up_prefill(p.ea, s));
       tm_mark(m, SLOT_GATE_UP, 1, s);
       tm_mark(m, SLOT_DOWN, 0, s);
+      if (gguf_fmt(p.ea.down.fmt)) HX_HIP(launch_hq_f32(p.ea, s));
       HX_HIP(launch_down_prefill(p.ea, s));
       tm_mark(m, SLOT_DOWN, 1, s);
     }
@@ -822,6 +890,20 @@ extern "C" int hx_dequantize(int dtype, const void* src, int64_t rows, int64_t c
     return fail(HX_ERR_INVALID_ARGUMENT, "hx_dequantize: %lld columns do not tile into dtype %d blocks", (long long)cols, dtype);
   if (rows == 0) return HX_OK;
   HX_HIP(launch_dequantize(dtype, src, rows, cols, dst, (hipStream_t)stream));
+  return HX_OK;
+}
+
+extern "C" int hx_quantize_activations(int weight_dtype, const void* x, int x_dtype, int64_t rows, int64_t cols,
+                                       int8_t* codes, float* d, void* stream) {
+  if (!x || !codes || !d || rows < 0 || cols <= 0 || cols > (1 << 20)) return fail(HX_ERR_INVALID_ARGUMENT, "bad argument");
+  if (!gguf_fmt(weight_dtype)) return fail(HX_ERR_UNSUPPORTED, "hx_quantize_activations: weight dtype %d has no vec_dot type", weight_dtype);
+  if (x_dtype != HX_F32 && x_dtype != HX_BF16) return fail(HX_ERR_UNSUPPORTED, "hx_quantize_activations: x dtype %d", x_dtype);
+  const int64_t blk = weight_dtype == HX_Q8_0 ? 32 : 256;
+  if (cols % blk)
+    return fail(HX_ERR_INVALID_ARGUMENT, "hx_quantize_activations: %lld columns are not whole blocks of %lld",
+                (long long)cols, (long long)blk);
+  if (rows == 0) return HX_OK;
+  HX_HIP(launch_actq_codes(weight_dtype, x, x_dtype == HX_BF16, rows, (int)cols, codes, d, (hipStream_t)stream));
   return HX_OK;
 }
 

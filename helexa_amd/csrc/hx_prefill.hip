@@ -6,9 +6,21 @@
 // the down GEMM, then the sum over k; crates/neuron/src/harness/tp/tp_qwen3_5.rs:1192-1225).
 //
 // Work unit: one M tile of the dispatch tile list (<= 64 permuted rows of one
-// expert, or of the shared expert) x one N tile. Operands are f16: the tokens
-// are converted once (bf16 -> f16 is exact in f16's normal range), the SwiGLU
-// activations are stored as f16, and weights are dequantised to f16 with the
+// expert, or of the shared expert) x one N tile. The reference computes an
+// expert call of m rows in one of two arms (tp_linear.rs:107-137), and so does
+// each tile, by its expert's m (the tile record's first word):
+//   * m <= HX_QUANT_M (= 64): the rows quantised to the weights' vec_dot type
+//     (Q8_0 / Q8_K codes, exactly the reference's, hx_quant.h) and integer
+//     block products. Here the operand is the f16 value d q of each code
+//     (one rounding of the dequantised code; the weights are f16 as well), so
+//     the products equal the reference's to f16 operand rounding. Tokens come
+//     from xq (k_xq_fq); h leaves the gate/up epilogue in f32 and k_hq_fq
+//     quantises it into hbf before the down GEMM.
+//   * m > 64 (forward_via_f16): f16 weights and activations, f32 sums, and the
+//     products rounded to f16 in the epilogues, as the reference's f16 output.
+// Operands are f16: the tokens are converted once (bf16 -> f16 is exact in
+// f16's normal range), the SwiGLU activations are stored as f16, and weights
+// are dequantised to f16 with the
 // 0x6400 pattern (f16 1024 + u, exact) and packed f16 arithmetic. Along K the
 // elements of every group of 4 are stored in the order (0, 2, 1, 3) -- in the
 // activations and in the weights alike, so the dot products are unchanged --
@@ -222,17 +234,21 @@ HX_DEV f16x8_t frag(const uint16_t* base) { return __builtin_bit_cast(f16x8_t, *
 // the workgroup has no tile (past the end, or a tile the launch skips). TS is
 // the launch's tile selection (HX_TILES_*), a template parameter so that each
 // selection is a kernel of its own name in traces and counter runs.
+// m: the rows of the expert's call (the reference's arm: m <= HX_QUANT_M
+// quantised activations, else f16)
 template <int TS>
-HX_DEV bool get_tile(const ExpertArgs& a, int tile, int& e, int& p0, int& rows) {
+HX_DEV bool get_tile(const ExpertArgs& a, int tile, int& e, int& p0, int& rows, int& m) {
   if (TS == HX_TILES_SHARED) {
     const int m0 = tile * PM;
     if (m0 >= a.T) return false;
     e = a.E;
     p0 = a.F + m0;
     rows = min(PM, a.T - m0);
+    m = a.T;
     return true;
   }
   if (tile >= a.counts[1]) return false;
+  m = a.tiles[4 * tile + 0];
   e = a.tiles[4 * tile + 1];
   p0 = a.tiles[4 * tile + 2];
   rows = a.tiles[4 * tile + 3];
@@ -479,9 +495,13 @@ HX_DEV void q4k_wait(int ahead, int wave_u) {
 
 // the K loop and epilogue of k_gate_up_q4k for tiles of at most 16 MT rows:
 // DMAs, activation-fragment reads and MFMAs only for the sub-tiles in use
+// qa: the tile's expert call takes the quantised arm (m <= HX_QUANT_M): its
+// tokens are the f16 d q operands and h goes out in f32 for quantisation;
+// otherwise the f16 arm: gate and up rounded to f16 (the reference's
+// forward_via_f16 output), h = silu(g) u rounded to f16 as the down input
 template <class Q, int MT>
 HX_DEV void q4k_main(const ExpertArgs& a, uint8_t* ring, const Q4kSrc<Q>& src, int nk, int rows, int p0, int n0,
-                     int wave, int wave_u, int l16, int kq, uint32_t knib, uint32_t kbyte, uint32_t kmagic) {
+                     int wave, int wave_u, int l16, int kq, uint32_t knib, uint32_t kbyte, uint32_t kmagic, bool qa) {
   constexpr int FPW = Q::FPW_;
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)ring;
   f32x4_t accg[MT][FPW], accu[MT][FPW];
@@ -512,9 +532,32 @@ HX_DEV void q4k_main(const ExpertArgs& a, uint8_t* ring, const Q4kSrc<Q>& src, i
     step(kc, std::integral_constant<int, 0>{});
     step(kc + 1, std::integral_constant<int, 1>{});
   }
+  __syncthreads();   // every wave is done with the ring
+  if (qa) {
+    // the 16 MT x COLS f32 rows of h (natural column order, row pitch
+    // COLS + 4) through LDS, out as 16-byte pieces into hbuf
+    constexpr int OP = Q::COLS + 4;
+    float* ot = (float*)ring;
+#pragma unroll
+    for (int j = 0; j < FPW; j++) {
+      const int col = 16 * (FPW * wave + j) + l16;
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) ot[(16 * mt + 4 * kq + i) * OP + col] = siluf_(accg[mt][j][i]) * accu[mt][j][i];
+    }
+    __syncthreads();
+    constexpr int PER_ROW = Q::COLS / 4;
+    constexpr int RSTEP = Q::NT / PER_ROW;
+    const int m0 = threadIdx.x / PER_ROW, c4 = (threadIdx.x % PER_ROW) * 4;
+    float* hrow = a.hbuf + (int64_t)(p0 + m0) * a.hstride + n0 + c4;
+#pragma unroll
+    for (int m = m0; m < 16 * MT; m += RSTEP, hrow += (int64_t)RSTEP * a.hstride)
+      if (m < rows) *(float4*)hrow = *(const float4*)(ot + m * OP + c4);
+    return;
+  }
   // the 16 MT x COLS f16 rows of h go through LDS (columns in the swizzled
   // order, row pitch COLS + 8) and out as 16-byte pieces
-  __syncthreads();   // every wave is done with the ring
   constexpr int OP = Q::COLS + 8;
   _Float16* ot = (_Float16*)ring;
 #pragma unroll
@@ -525,7 +568,8 @@ HX_DEV void q4k_main(const ExpertArgs& a, uint8_t* ring, const Q4kSrc<Q>& src, i
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int m = 16 * mt + 4 * kq + i;
-        ot[m * OP + col] = (_Float16)(silu_rcp(accg[mt][j][i]) * accu[mt][j][i]);
+        const float g = (float)(_Float16)accg[mt][j][i], u = (float)(_Float16)accu[mt][j][i];
+        ot[m * OP + col] = (_Float16)(silu_rcp(g) * u);
       }
   }
   __syncthreads();
@@ -548,9 +592,9 @@ __global__ __launch_bounds__(64 * NW, 3) void k_gate_up_q4k(ExpertArgs a) {
   __shared__ int rowsrc[PM];
   int nt, tile;
   xcd_tile(nt, tile);
-  int e, p0, rows;
-  if (!get_tile<TS>(a, tile, e, p0, rows)) return;
-  const bool sh = e == a.E;
+  int e, p0, rows, mc;
+  if (!get_tile<TS>(a, tile, e, p0, rows, mc)) return;
+  const bool sh = e == a.E, qa = mc <= HX_QUANT_M;
   const int n0 = nt * Q::COLS;
   const uint8_t* G = sh ? a.sgate.base : a.gate.mat(e);
   const uint8_t* U = sh ? a.sup.base : a.up.mat(e);
@@ -562,16 +606,16 @@ __global__ __launch_bounds__(64 * NW, 3) void k_gate_up_q4k(ExpertArgs a) {
   __syncthreads();
   const int lane = lane_id(), wave = threadIdx.x >> 6, l16 = lane & 15, kq = lane >> 4;
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  const Q4kSrc<Q> src = q4k_sources<Q>(a.xh, a.H, rowsrc, G, U, n0, sh ? a.Is : a.I, K);
+  const Q4kSrc<Q> src = q4k_sources<Q>(qa ? a.xq : a.xh, a.H, rowsrc, G, U, n0, sh ? a.Is : a.I, K);
   // dequantisation constants, kept in registers for v_and_or_b32
   const uint32_t knib = __builtin_amdgcn_readfirstlane(0x000F000Fu), kbyte = __builtin_amdgcn_readfirstlane(0x00FF00FFu);
   uint32_t kmagic;
   asm("v_mov_b32 %0, 0x64006400" : "=v"(kmagic));
   switch ((rows + 15) >> 4) {   // uniform over the workgroup
-    case 1: q4k_main<Q, 1>(a, ring, src, nk, rows, p0, n0, wave, wave_u, l16, kq, knib, kbyte, kmagic); break;
-    case 2: q4k_main<Q, 2>(a, ring, src, nk, rows, p0, n0, wave, wave_u, l16, kq, knib, kbyte, kmagic); break;
-    case 3: q4k_main<Q, 3>(a, ring, src, nk, rows, p0, n0, wave, wave_u, l16, kq, knib, kbyte, kmagic); break;
-    default: q4k_main<Q, 4>(a, ring, src, nk, rows, p0, n0, wave, wave_u, l16, kq, knib, kbyte, kmagic); break;
+    case 1: q4k_main<Q, 1>(a, ring, src, nk, rows, p0, n0, wave, wave_u, l16, kq, knib, kbyte, kmagic, qa); break;
+    case 2: q4k_main<Q, 2>(a, ring, src, nk, rows, p0, n0, wave, wave_u, l16, kq, knib, kbyte, kmagic, qa); break;
+    case 3: q4k_main<Q, 3>(a, ring, src, nk, rows, p0, n0, wave, wave_u, l16, kq, knib, kbyte, kmagic, qa); break;
+    default: q4k_main<Q, 4>(a, ring, src, nk, rows, p0, n0, wave, wave_u, l16, kq, knib, kbyte, kmagic, qa); break;
   }
 }
 
@@ -719,9 +763,11 @@ HX_DEV void dq_compute(const lds_u8* st, const uint16_t* dl, int sb, f32x4_t (*a
 // grid (H / 128, tiles rounded up to 8), mapped by xcd_tile
 // the K loop and epilogue of k_down_q6k for tiles of at most 16 MT rows (MFMAs,
 // activation-fragment reads and A DMA rounds for the sub-tiles in use)
+// fa: the f16 arm (m > HX_QUANT_M): the products rounded to f16 (the
+// reference's forward_via_f16 output) before the routing weight
 template <int MT>
 HX_DEV void dq_main(const ExpertArgs& a, uint8_t* ring, float* rws, const DqSrc& src, float rw, int rows, int p0,
-                    int n0, int wave, int wave_u, int l16, int kq) {
+                    int n0, int wave, int wave_u, int l16, int kq, bool fa) {
   const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_u8*)ring;
   const uint16_t* dl = (const uint16_t*)(ring + DQ_NST * DQ_STAGE);
   constexpr int NA = MT <= 2 ? 1 : 2;   // A rounds (32 rows each) the tile needs
@@ -771,7 +817,10 @@ HX_DEV void dq_main(const ExpertArgs& a, uint8_t* ring, float* rws, const DqSrc&
     for (int j = 0; j < 2; j++) {
       const int col = 32 * wave + 16 * j + l16;
 #pragma unroll
-      for (int i = 0; i < 4; i++) ot[(16 * mt + 4 * kq + i) * OP + col] = f32_to_bf16(wv[i] * acc[j][mt][i]);
+      for (int i = 0; i < 4; i++) {
+        const float v = fa ? (float)(_Float16)acc[j][mt][i] : acc[j][mt][i];
+        ot[(16 * mt + 4 * kq + i) * OP + col] = f32_to_bf16(wv[i] * v);
+      }
     }
   }
   __syncthreads();
@@ -790,8 +839,9 @@ __global__ __launch_bounds__(256, 3) void k_down_q6k(ExpertArgs a) {
   __shared__ __attribute__((aligned(16))) float rws[PM];
   int nt, tile;
   xcd_tile(nt, tile);
-  int e, p0, rows;
-  if (!get_tile<TS>(a, tile, e, p0, rows)) return;
+  int e, p0, rows, mc;
+  if (!get_tile<TS>(a, tile, e, p0, rows, mc)) return;
+  const bool fa = mc > HX_QUANT_M;
   const bool sh = e == a.E;
   const int n0 = nt * 128;
   const uint8_t* W = sh ? a.sdown.base : a.down.mat(e);
@@ -806,18 +856,20 @@ __global__ __launch_bounds__(256, 3) void k_down_q6k(ExpertArgs a) {
          lds0 + (uint32_t)(DQ_NST * DQ_STAGE + wave_u * 256));
   const DqSrc src = dq_sources(a.hbf, a.hstride, p0, rows, W, a.H, n0);
   switch ((rows + 15) >> 4) {   // uniform over the workgroup
-    case 1: dq_main<1>(a, ring, rws, src, rw, rows, p0, n0, wave, wave_u, l16, kq); break;
-    case 2: dq_main<2>(a, ring, rws, src, rw, rows, p0, n0, wave, wave_u, l16, kq); break;
-    case 3: dq_main<3>(a, ring, rws, src, rw, rows, p0, n0, wave, wave_u, l16, kq); break;
-    default: dq_main<4>(a, ring, rws, src, rw, rows, p0, n0, wave, wave_u, l16, kq); break;
+    case 1: dq_main<1>(a, ring, rws, src, rw, rows, p0, n0, wave, wave_u, l16, kq, fa); break;
+    case 2: dq_main<2>(a, ring, rws, src, rw, rows, p0, n0, wave, wave_u, l16, kq, fa); break;
+    case 3: dq_main<3>(a, ring, rws, src, rw, rows, p0, n0, wave, wave_u, l16, kq, fa); break;
+    default: dq_main<4>(a, ring, rws, src, rw, rows, p0, n0, wave, wave_u, l16, kq, fa); break;
   }
 }
 
 // ---------------------------------------------------------------- gate/up
 // grid (I / 64, tiles rounded up to 8), mapped by xcd_tile: 64 rows x 64
 // intermediate columns; wave w owns columns
-// 16w .. 16w+15 of gate and of up for all 64 rows. h = silu(gate) * up is
-// written as f16 in the swizzled order.
+// 16w .. 16w+15 of gate and of up for all 64 rows. Quantised arm (m <=
+// HX_QUANT_M): the tokens are the f16 d q operands and h = silu(gate) * up goes
+// to hbuf in f32; f16 arm: gate and up rounded to f16, h written as f16 in the
+// swizzled order.
 template <int FMT, int TS>
 __global__ __launch_bounds__(256) void k_gate_up_mfma(ExpertArgs a) {
   __shared__ uint16_t As[PM * PLD];
@@ -825,9 +877,10 @@ __global__ __launch_bounds__(256) void k_gate_up_mfma(ExpertArgs a) {
   __shared__ int rowsrc[PM];
   int nt, tile;
   xcd_tile(nt, tile);
-  int e, p0, rows;
-  if (!get_tile<TS>(a, tile, e, p0, rows)) return;
-  const bool sh = e == a.E;
+  int e, p0, rows, mc;
+  if (!get_tile<TS>(a, tile, e, p0, rows, mc)) return;
+  const bool sh = e == a.E, qa = mc <= HX_QUANT_M;
+  const uint16_t* X = qa ? a.xq : a.xh;
   const int I = sh ? a.Is : a.I, n0 = nt * 64;
   if (n0 >= I) return;
   const uint8_t* G = sh ? a.sgate.base : a.gate.mat(e);
@@ -852,13 +905,13 @@ __global__ __launch_bounds__(256) void k_gate_up_mfma(ExpertArgs a) {
   }
   ARaw ar;
   PRaw<FMT> br;
-  ar.load(a.xh, K, rowsrc, rows, 0);
+  ar.load(X, K, rowsrc, rows, 0);
   br.load(Wm, I, K, wrow, 0, bpt);
   for (int kc = 0; kc < nk; kc++) {
     ar.to_lds(As);
     br.to_lds(Bs + brow * PLD + 64 * bpt);
     if (kc + 1 < nk) {
-      ar.load(a.xh, K, rowsrc, rows, kc + 1);
+      ar.load(X, K, rowsrc, rows, kc + 1);
       br.load(Wm, I, K, wrow, kc + 1, bpt);
     }
     __syncthreads();
@@ -876,13 +929,19 @@ __global__ __launch_bounds__(256) void k_gate_up_mfma(ExpertArgs a) {
     }
     __syncthreads();
   }
-  const int col = swz(n0 + 16 * wave + l16);
+  const int coln = n0 + 16 * wave + l16, col = swz(coln);
 #pragma unroll
   for (int mt = 0; mt < 4; mt++)
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int m = 16 * mt + 4 * kq + i;
-      if (m < rows) ((_Float16*)a.hbf)[(int64_t)(p0 + m) * a.hstride + col] = (_Float16)(siluf_(accg[mt][i]) * accu[mt][i]);
+      if (m >= rows) continue;
+      if (qa) {
+        a.hbuf[(int64_t)(p0 + m) * a.hstride + coln] = siluf_(accg[mt][i]) * accu[mt][i];
+      } else {
+        const float g = (float)(_Float16)accg[mt][i], u = (float)(_Float16)accu[mt][i];
+        ((_Float16*)a.hbf)[(int64_t)(p0 + m) * a.hstride + col] = (_Float16)(siluf_(g) * u);
+      }
     }
 }
 
@@ -890,7 +949,8 @@ __global__ __launch_bounds__(256) void k_gate_up_mfma(ExpertArgs a) {
 // grid (H / 128, tiles rounded up to 8), mapped by xcd_tile: 64 rows x 128
 // output columns; wave w owns columns
 // 32w .. 32w+31. Rows are scaled by their routing weight (shared expert: the
-// sigmoid gate) and written to the per-assignment output rows.
+// sigmoid gate) and written to the per-assignment output rows; in the f16 arm
+// (m > HX_QUANT_M) the products are rounded to f16 first.
 template <int FMT, int TS>
 __global__ __launch_bounds__(256) void k_down_mfma(ExpertArgs a) {
   __shared__ uint16_t As[PM * PLD];
@@ -899,8 +959,9 @@ __global__ __launch_bounds__(256) void k_down_mfma(ExpertArgs a) {
   __shared__ float rw[PM];
   int nt, tile;
   xcd_tile(nt, tile);
-  int e, p0, rows;
-  if (!get_tile<TS>(a, tile, e, p0, rows)) return;
+  int e, p0, rows, mc;
+  if (!get_tile<TS>(a, tile, e, p0, rows, mc)) return;
+  const bool fa = mc > HX_QUANT_M;
   const bool sh = e == a.E;
   const int K = sh ? a.Is : a.I, n0 = nt * 128, nk = K / PKC;
   const uint8_t* W = sh ? a.sdown.base : a.down.mat(e);
@@ -952,7 +1013,9 @@ __global__ __launch_bounds__(256) void k_down_mfma(ExpertArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int m = 16 * mt + 4 * kq + i;
-        if (m < rows) ((uint16_t*)a.obuf)[(int64_t)(p0 + m) * a.H + col] = f32_to_bf16(rw[m] * acc[j][mt][i]);
+        if (m < rows)
+          ((uint16_t*)a.obuf)[(int64_t)(p0 + m) * a.H + col] =
+              f32_to_bf16(rw[m] * (fa ? (float)(_Float16)acc[j][mt][i] : acc[j][mt][i]));
       }
   }
 }

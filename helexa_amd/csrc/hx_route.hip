@@ -102,7 +102,7 @@ constexpr int DISP_MAXC = DISP_EPB / HX_DISPATCH_TOK + 2;
 __global__ __launch_bounds__(1024) void k_disp_fused(DispatchArgs a) {
   constexpr int WPC = HX_DISPATCH_TOK / 32, PB = 16;
   __shared__ int sh[3][17];
-  __shared__ int s_first[HX_MAX_EXPERTS], s_slot[HX_MAX_EXPERTS], s_off[HX_MAX_EXPERTS], s_cnt[HX_MAX_EXPERTS];
+  __shared__ int s_first[HX_MAX_EXPERTS], s_off[HX_MAX_EXPERTS], s_cnt[HX_MAX_EXPERTS];
   __shared__ int s_base[DISP_MAXC][HX_MAX_EXPERTS];
   const int e = threadIdx.x, E = a.E, nb = dispatch_chunks(a.T), k = a.k;
   const int f0 = blockIdx.x * DISP_EPB, f1 = min(a.F, f0 + DISP_EPB);
@@ -146,7 +146,6 @@ __global__ __launch_bounds__(1024) void k_disp_fused(DispatchArgs a) {
     if (blockIdx.x == 0) {
       a.offsets[e] = off;
       s_first[e] = ex[2];
-      s_slot[e] = ex[1];
       s_off[e] = off;
       s_cnt[e] = count;
       if (count > 0) {
@@ -166,7 +165,7 @@ __global__ __launch_bounds__(1024) void k_disp_fused(DispatchArgs a) {
         else hi = mid - 1;
       }
       const int m0 = (i - s_first[lo]) * a.tile_m, c = s_cnt[lo];
-      a.tiles[4 * i + 0] = s_slot[lo];
+      a.tiles[4 * i + 0] = c;   // the rows of the expert's call: its arithmetic arm
       a.tiles[4 * i + 1] = lo;
       a.tiles[4 * i + 2] = s_off[lo] + m0;
       a.tiles[4 * i + 3] = c - m0 < a.tile_m ? c - m0 : a.tile_m;
@@ -177,7 +176,7 @@ __global__ __launch_bounds__(1024) void k_disp_fused(DispatchArgs a) {
       const int nst = (a.T + a.tile_m - 1) / a.tile_m;
       for (int i = threadIdx.x; i < nst; i += 1024) {
         const int m0 = i * a.tile_m;
-        a.tiles[4 * (ntile + i) + 0] = nslot;
+        a.tiles[4 * (ntile + i) + 0] = a.T;
         a.tiles[4 * (ntile + i) + 1] = E;
         a.tiles[4 * (ntile + i) + 2] = a.F + m0;
         a.tiles[4 * (ntile + i) + 3] = a.T - m0 < a.tile_m ? a.T - m0 : a.tile_m;

@@ -36,7 +36,8 @@ STATUS = {0: "HX_OK", 1: "HX_ERR_INVALID_ARGUMENT", 2: "HX_ERR_UNSUPPORTED", 3: 
 EXPORTS = ("hx_moe_create", "hx_moe_destroy", "hx_moe_workspace_size", "hx_moe_forward", "hx_moe_forward_noalloc",
            "hx_moe_forward_host",
            "hx_moe_route", "hx_moe_router_logits", "hx_moe_decoder_mlp", "hx_quantize", "hx_dequantize",
-           "hx_row_bytes", "hx_moe_timing_begin", "hx_moe_timing_read", "hx_moe_timing_end", "hx_moe_timing_name", "hx_last_error")
+           "hx_row_bytes", "hx_quantize_activations", "hx_moe_timing_begin", "hx_moe_timing_read", "hx_moe_timing_end",
+           "hx_moe_timing_name", "hx_last_error")
 
 
 class HxError(RuntimeError):
@@ -87,6 +88,7 @@ def lib() -> C.CDLL:
             "hx_quantize": (i32, [i32, vp, i64, i64, vp, vp]),
             "hx_dequantize": (i32, [i32, vp, i64, i64, vp, vp]),
             "hx_row_bytes": (i64, [i32, i64]),
+            "hx_quantize_activations": (i32, [i32, vp, i32, i64, i64, vp, vp, vp]),
             "hx_moe_timing_begin": (i32, [vp, i32]),
             "hx_moe_timing_read": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.POINTER(C.c_int)]),
             "hx_moe_timing_end": (i32, [vp, C.POINTER(C.c_double), C.POINTER(C.c_int64), C.POINTER(C.c_int)]),
@@ -372,3 +374,23 @@ def dequantize(dtype: int, q, cols: int, stream=None):
     out = torch.empty(q.shape[:-1] + (cols,), dtype=torch.float32, device=q.device)
     check(lib().hx_dequantize(dtype, _ptr(q), rows, cols, _ptr(out), _stream(stream)), "hx_dequantize")
     return out
+
+
+def quantize_activations(weight_dtype: int, x, stream=None):
+    """The activation quantisation of the reference's quantised arm (the rows of
+    an expert call of at most 64 rows, quantised to the weight type's vec_dot
+    type: Q8_0 blocks for Q8_0 weights, Q8_K for Q4_K / Q6_K) on the device:
+    float32 or bfloat16 cuda tensor [rows, cols] -> (int8 codes [rows, cols],
+    float32 d [rows, cols / block])."""
+    import torch
+    x = x.contiguous()
+    if not x.is_cuda or x.dim() != 2:
+        raise TypeError("quantize_activations needs a 2-d cuda tensor")
+    act = _act_dtype(x.dtype)
+    rows, cols = x.shape
+    blk = 32 if weight_dtype == Q8_0 else 256
+    codes = torch.empty((rows, cols), dtype=torch.int8, device=x.device)
+    d = torch.empty((rows, max(cols // blk, 1)), dtype=torch.float32, device=x.device)
+    check(lib().hx_quantize_activations(weight_dtype, _ptr(x), act, rows, cols, _ptr(codes), _ptr(d), _stream(stream)),
+          "hx_quantize_activations")
+    return codes, d

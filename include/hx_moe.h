@@ -163,6 +163,19 @@ int hx_dequantize(int dtype, const void* src, int64_t rows, int64_t cols, float*
 /* Bytes of one GGUF row of n elements, or -1 if n does not tile into blocks. */
 int64_t hx_row_bytes(int dtype, int64_t n);
 
+/* The activation quantisation of MaybeQuantLinear's quantised arm
+ * (crates/neuron/src/harness/tp/tp_linear.rs:120-137: an expert call of at
+ * most 64 rows quantises each activation row to the weight type's vec_dot
+ * type before candle's integer vec_dot), as the forward kernels compute it,
+ * on the device: x [rows, cols] (x_dtype HX_F32 or HX_BF16) -> codes int8
+ * [rows, cols] and d f32 [rows, cols / block]. weight_dtype HX_Q8_0 gives Q8_0
+ * blocks of 32 (d = amax / 127, rounded to f16; codes round(x / d) half away
+ * from zero); HX_Q4_K or HX_Q6_K gives Q8_K blocks of 256 (iscale = -128 /
+ * the first largest-magnitude value, codes min(round(iscale x), 127),
+ * d = 1 / iscale). cols must be a multiple of the block. */
+int hx_quantize_activations(int weight_dtype, const void* x, int x_dtype, int64_t rows, int64_t cols, int8_t* codes,
+                            float* d, void* stream);
+
 /* Per-kernel timing (a measurement hook with no reference counterpart): HIP
  * events recorded on the forward's stream around each kernel it launches.
  * hx_moe_timing_begin arms it for the next max_calls forwards (forwards under

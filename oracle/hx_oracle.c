@@ -1119,12 +1119,16 @@ static void dot_chain8(const float* xt, const float* w, int64_t K, float* out) {
     memcpy(out, &acc, sizeof acc);
 }
 
-/* MaybeQuantLinear::forward over m rows: out[m][N] = X[m][K] . W[N][K]^T */
-static void qlinear(int dt, const void* W, int64_t N, int64_t K, const float* X, int64_t m, float* out,
+/* MaybeQuantLinear::forward over m rows: out[m][N] = X[m][K] . W[N][K]^T. The
+ * arm follows marm, the rows of the reference's call (tp_linear.rs:107-109;
+ * QUANT_PREFILL_M_THRESHOLD = 64, tp_linear.rs:96): a caller that evaluates
+ * only some rows of a call passes the call's full row count (every arm
+ * computes each row independently). */
+static void qlinear(int dt, const void* W, int64_t N, int64_t K, const float* X, int64_t m, int64_t marm, float* out,
                     int nthreads) {
     const int64_t rb = hxo_row_bytes(dt, K);
     const int quant = dt == HXO_Q8_0 || dt == HXO_Q4_K || dt == HXO_Q6_K;
-    if (!quant || m > 64) {
+    if (!quant || marm > 64) {
         /* plain f32 Linear, or forward_via_f16: f16 weights and x, f16 output */
         const int f16 = quant;
         float* xr = (float*)malloc(sizeof(float) * m * K);
@@ -1215,24 +1219,47 @@ int hxo_qlinear(int dt, const void* W, int64_t N, int64_t K, const float* X, int
 #ifdef _OPENMP
     if (nthreads <= 0) nthreads = omp_get_max_threads();
 #endif
-    qlinear(dt, W, N, K, X, m, out, nthreads);
+    qlinear(dt, W, N, K, X, m, m, out, nthreads);
     return 0;
 }
 
 /* TpExpert::forward_partial at world size 1 over m rows of xf (gathered):
  * out[m][H] = down(silu(gate x) * up x) */
 static void candle_expert(int gdt, const void* g, int udt, const void* u, int ddt, const void* d, int64_t H,
-                          int64_t I, const float* X, int64_t m, float* out, float* gbuf, float* ubuf, int nthreads) {
-    qlinear(gdt, g, I, H, X, m, gbuf, nthreads);
-    qlinear(udt, u, I, H, X, m, ubuf, nthreads);
+                          int64_t I, const float* X, int64_t m, int64_t marm, float* out, float* gbuf, float* ubuf,
+                          int nthreads) {
+    qlinear(gdt, g, I, H, X, m, marm, gbuf, nthreads);
+    qlinear(udt, u, I, H, X, m, marm, ubuf, nthreads);
     for (int64_t i = 0; i < m * I; i++) {
         const float v = gbuf[i];
         gbuf[i] = (v / (1.0f + expf(-v))) * ubuf[i];
     }
-    qlinear(ddt, d, H, I, gbuf, m, out, nthreads);
+    qlinear(ddt, d, H, I, gbuf, m, marm, out, nthreads);
 }
 
+static int forward_candle_impl(const hxo_moe* m, const void* x, int64_t T, const float* bias, const int32_t* sel,
+                               int64_t nsel, float* y, int nthreads);
+
 int hxo_moe_forward_candle(const hxo_moe* m, const void* x, int64_t T, const float* bias, float* y, int nthreads) {
+    return forward_candle_impl(m, x, T, bias, NULL, 0, y, nthreads);
+}
+
+/* the outputs of the distinct tokens sel[0 .. nsel) of a forward of all T tokens, in
+ * candle arithmetic: every expert call takes the arm of its full row count,
+ * and only the selected tokens' rows are computed (y: [nsel][H]) */
+int hxo_moe_forward_candle_sel(const hxo_moe* m, const void* x, int64_t T, const float* bias, const int32_t* sel,
+                               int64_t nsel, float* y, int nthreads) {
+    if (!sel || nsel <= 0) return 1;
+    for (int64_t i = 0; i < nsel; i++) {   /* distinct tokens in [0, T) */
+        if (sel[i] < 0 || sel[i] >= T) return 1;
+        for (int64_t j = 0; j < i; j++)
+            if (sel[j] == sel[i]) return 1;
+    }
+    return forward_candle_impl(m, x, T, bias, sel, nsel, y, nthreads);
+}
+
+static int forward_candle_impl(const hxo_moe* m, const void* x, int64_t T, const float* bias, const int32_t* sel,
+                               int64_t nsel, float* y, int nthreads) {
     int64_t H = m->hidden, E = m->num_experts, I = m->inter, Is = m->shared_inter;
     int k = m->top_k;
     if (hxo_row_bytes(m->gate_dtype, H) < 0 || hxo_row_bytes(m->up_dtype, H) < 0 ||
@@ -1246,37 +1273,44 @@ int hxo_moe_forward_candle(const hxo_moe* m, const void* x, int64_t T, const flo
 #else
     nthreads = 1;
 #endif
-    const int64_t F = T * k, KM = I > Is ? I : Is, R = T > F ? T : F;
+    const int64_t F = T * k, KM = I > Is ? I : Is, R = T > F ? T : F, ny = sel ? nsel : T;
     int32_t* idx = (int32_t*)malloc(sizeof(int32_t) * F);
     float* w = (float*)malloc(sizeof(float) * F);
     int32_t* perm = (int32_t*)malloc(sizeof(int32_t) * F);
     int32_t* offs = (int32_t*)malloc(sizeof(int32_t) * (E + 1));
+    int64_t* yrow = (int64_t*)malloc(sizeof(int64_t) * T);   /* output row of token t, or -1 */
+    int32_t* rows = (int32_t*)malloc(sizeof(int32_t) * R);   /* the computed rows of a call */
     float* xf = (float*)malloc(sizeof(float) * T * H);
     float* xg = (float*)malloc(sizeof(float) * R * H);
     float* og = (float*)malloc(sizeof(float) * R * H);
     float* gbuf = (float*)malloc(sizeof(float) * R * KM);
     float* ubuf = (float*)malloc(sizeof(float) * R * KM);
     int rc = 0;
-    if (!idx || !w || !perm || !offs || !xf || !xg || !og || !gbuf || !ubuf) { rc = 2; goto done; }
+    if (!idx || !w || !perm || !offs || !yrow || !rows || !xf || !xg || !og || !gbuf || !ubuf) { rc = 2; goto done; }
     rc = hxo_route(m, x, T, bias, NULL, NULL, idx, w);
     if (rc) goto done;
     rc = hxo_dispatch(idx, T, k, E, perm, offs, NULL);
     if (rc) goto done;
+    for (int64_t t = 0; t < T; t++) yrow[t] = sel ? -1 : t;
+    if (sel)
+        for (int64_t i = 0; i < nsel; i++) yrow[sel[i]] = i;
     for (int64_t i = 0; i < T * H; i++) xf[i] = ld_act(m->act_dtype, x, i);
-    for (int64_t i = 0; i < T * H; i++) y[i] = 0.0f;
+    for (int64_t i = 0; i < ny * H; i++) y[i] = 0.0f;
     {
         const int64_t gb = hxo_row_bytes(m->gate_dtype, H) * I, ub = hxo_row_bytes(m->up_dtype, H) * I;
         const int64_t db = hxo_row_bytes(m->down_dtype, I) * H;
         for (int64_t e = 0; e < E; e++) {
             const int64_t n = offs[e + 1] - offs[e];
-            if (n == 0) continue;
+            int64_t nc = 0;   /* rows of the call computed here (all, or those of selected tokens) */
             for (int64_t p = 0; p < n; p++)
-                memcpy(xg + p * H, xf + (int64_t)(perm[offs[e] + p] / k) * H, sizeof(float) * H);
+                if (yrow[perm[offs[e] + p] / k] >= 0) rows[nc++] = perm[offs[e] + p];
+            if (nc == 0) continue;
+            for (int64_t p = 0; p < nc; p++) memcpy(xg + p * H, xf + (int64_t)(rows[p] / k) * H, sizeof(float) * H);
             candle_expert(m->gate_dtype, (const uint8_t*)m->gate + e * gb, m->up_dtype, (const uint8_t*)m->up + e * ub,
-                          m->down_dtype, (const uint8_t*)m->down + e * db, H, I, xg, n, og, gbuf, ubuf, nthreads);
-            for (int64_t p = 0; p < n; p++) {
-                const int32_t f = perm[offs[e] + p];
-                float* yt = y + (int64_t)(f / k) * H;
+                          m->down_dtype, (const uint8_t*)m->down + e * db, H, I, xg, nc, n, og, gbuf, ubuf, nthreads);
+            for (int64_t p = 0; p < nc; p++) {
+                const int32_t f = rows[p];
+                float* yt = y + yrow[f / k] * H;
                 for (int64_t h = 0; h < H; h++) yt[h] = yt[h] + og[p * H + h] * w[f];
             }
         }
@@ -1284,15 +1318,20 @@ int hxo_moe_forward_candle(const hxo_moe* m, const void* x, int64_t T, const flo
     if (Is > 0) {
         float* wr = (float*)malloc(sizeof(float) * H);
         hxo_dequant(m->seg_dtype, m->seg, H, wr);
-        candle_expert(m->sgate_dtype, m->sgate, m->sup_dtype, m->sup, m->sdown_dtype, m->sdown, H, Is, xf, T, og,
+        for (int64_t t = 0; t < T; t++)
+            if (yrow[t] >= 0) memcpy(xg + yrow[t] * H, xf + t * H, sizeof(float) * H);
+        candle_expert(m->sgate_dtype, m->sgate, m->sup_dtype, m->sup, m->sdown_dtype, m->sdown, H, Is, xg, ny, T, og,
                       gbuf, ubuf, nthreads);
         for (int64_t t = 0; t < T; t++) {
+            const int64_t r = yrow[t];
+            if (r < 0) continue;
             const float mix = 1.0f / (1.0f + expf(-dot_chain(xf + t * H, wr, H)));
-            for (int64_t h = 0; h < H; h++) y[t * H + h] = y[t * H + h] + og[t * H + h] * mix;
+            for (int64_t h = 0; h < H; h++) y[r * H + h] = y[r * H + h] + og[r * H + h] * mix;
         }
         free(wr);
     }
 done:
-    free(idx); free(w); free(perm); free(offs); free(xf); free(xg); free(og); free(gbuf); free(ubuf);
+    free(idx); free(w); free(perm); free(offs); free(yrow); free(rows); free(xf); free(xg); free(og); free(gbuf);
+    free(ubuf);
     return rc;
 }

@@ -61,6 +61,8 @@ def lib() -> C.CDLL:
         L.hxo_moe_forward.argtypes = [vp, vp, i64, vp, vp, i32]
         L.hxo_moe_forward_candle.restype = i32
         L.hxo_moe_forward_candle.argtypes = [vp, vp, i64, vp, vp, i32]
+        L.hxo_moe_forward_candle_sel.restype = i32
+        L.hxo_moe_forward_candle_sel.argtypes = [vp, vp, i64, vp, vp, i64, vp, i32]
         L.hxo_qlinear.restype = i32
         L.hxo_qlinear.argtypes = [i32, vp, i64, i64, vp, i64, vp, i32]
         L.hxo_quant_q8_k.restype = i32
@@ -258,6 +260,20 @@ class OracleMoe:
         rc = lib().hxo_moe_forward_candle(C.byref(self.s), _p(x), T, _p(b), _p(y), nthreads)
         if rc:
             raise ValueError(f"hxo_moe_forward_candle rc={rc}")
+        return y
+
+    def forward_candle_tokens(self, x, tokens, bias=None, nthreads=0):
+        """candle-arithmetic mode for the tokens `tokens` of a forward of all of x:
+        each expert call takes the arm of its full row count (so a sample of a
+        prefill is computed as in the full forward), only the sampled rows are
+        computed; -> [len(tokens), H]"""
+        x, T = self._x(x)
+        sel = np.ascontiguousarray(tokens, dtype=np.int32)
+        y = np.empty((sel.size, self.cfg[0]), np.float32)
+        b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+        rc = lib().hxo_moe_forward_candle_sel(C.byref(self.s), _p(x), T, _p(b), _p(sel), sel.size, _p(y), nthreads)
+        if rc:
+            raise ValueError(f"hxo_moe_forward_candle_sel rc={rc}")
         return y
 
 

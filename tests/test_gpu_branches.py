@@ -5,7 +5,9 @@ weights under f32 activations, the generic Q6_K prefill down kernel, large
 activations, and the 48-layer C4 stack captured in one HIP graph. Everything
 runs through the C ABI against the CPU oracle (or the reference test's own
 per-token computation); routing bit-exact, outputs within the north-star
-tolerances."""
+tolerances of the reference's arithmetic: the oracle's candle mode for GGUF
+experts (quantised activations for calls of m <= 64 rows, f16 above), its
+exact mode for f32 / bf16 experts."""
 import numpy as np
 import pytest
 
@@ -17,6 +19,12 @@ from tests.common import assert_topk_w, mfma_routing, rel_err, report  # noqa: E
 pytestmark = pytest.mark.gpu
 
 TOL_BF16, TOL_F32 = 1e-2, 1e-4
+# GGUF experts under f32 activations: the tokens' codes are the reference's bit
+# for bit, but the rows of h are quantised from the GPU's own f32 h, whose last
+# bits differ from the reference's (summation order of the block products, the
+# exp of SiLU), so now and then a code of h lands one step away, which moves
+# that output row by up to ~1e-3 of max|y|
+TOL_F32_GGUF = 2e-3
 
 
 def _hx():
@@ -42,6 +50,17 @@ class Blk:
         self.block = hx.Qwen3_5MoeBlock.load(self.cfg, self.w, act_dtype=act)
         self.wnp = synth.to_numpy(self.w)
         self.oracle = O.OracleMoe(H, E, k, I, Is, norm, act, self.wnp)
+        self.quant = any(self.w[n][0] in (hx.Q8_0, hx.Q4_K, hx.Q6_K) for n in ("gate", "up", "down"))
+
+    def ref(self, xin, bias=None):
+        """the reference's output: candle arithmetic for GGUF experts, else exact"""
+        return self.oracle.forward_candle(xin, bias=bias) if self.quant else self.oracle.forward(xin, bias=bias)
+
+    def ref_tokens(self, xin, sel, bias=None):
+        """the reference's output for the tokens sel of a forward of all of x"""
+        if self.quant:
+            return self.oracle.forward_candle_tokens(xin, sel, bias=bias)
+        return self.oracle.forward(xin[sel], bias=bias)
 
     def x(self, T, seed=0, scale=1.0):
         _, synth = _hx()
@@ -51,7 +70,7 @@ class Blk:
 
     def check(self, x, tol, bias=None, tag=""):
         """routing bit-exact (ids and weight bits) and the output within tol of
-        the exact oracle"""
+        the reference's arithmetic (ref)"""
         r = self.block.route(x, router_bias=bias)
         bn = None if bias is None else bias.cpu().numpy()
         _, _, ix, wt = self.oracle.route(x_np(x), bias=bn)
@@ -65,7 +84,7 @@ class Blk:
         assert np.array_equal(r["offsets"].cpu().numpy(), offs)
         got = self.block.forward(x, router_bias=bias).float().cpu().numpy()
         assert np.isfinite(got).all()
-        e = report(tag or f"T={x.shape[0]}", got, self.oracle.forward(x_np(x), bias=bn))
+        e = report(tag or f"T={x.shape[0]}", got, self.ref(x_np(x), bias=bn))
         assert e["normwise"] <= tol
         return got
 
@@ -193,12 +212,13 @@ def test_bf16_weights(T):
 @pytest.mark.parametrize("fmt", ["FMT_Q8_0", "FMT_Q4_K_M"])
 def test_gguf_weights_with_f32_activations(fmt):
     """GGUF experts under f32 activations: decode and prefill take the generic
-    kernels (the fast ones need bf16 tokens); f32 tolerance against the exact
-    oracle, which uses the same dequantised weights"""
+    kernels (the fast ones need bf16 tokens), whose calls of m <= 64 rows read
+    the f32 d q of the tokens' and of h's Q8 codes; against the candle
+    arithmetic within TOL_F32_GGUF"""
     _, synth = _hx()
     b = Blk(512, 16, 4, 512, 512, True, getattr(synth, fmt), O.F32, 309)
     for T in (1, 8, 100):
-        b.check(b.x(T, seed=9), TOL_F32, tag=f"{fmt} f32 acts T={T}")
+        b.check(b.x(T, seed=9), TOL_F32_GGUF, tag=f"{fmt} f32 acts T={T}")
 
 
 def test_prefill_q6_k_down_i1024():
@@ -220,17 +240,22 @@ def test_large_activations(T):
 
 # ------------------------------------------------------------------ C4: 48 layers in one graph
 def test_c4_48_layer_graph_against_oracle():
-    """the C4 stack: 48 Q4_K_M layers of x <- x + moe(rmsnorm(x)) (per-channel
-    RMSNorm weight under the (1 + w) scaling) captured in one HIP graph, with a
-    copy of the residual stream after every layer captured alongside; replayed
-    twice, the result equals the eager stack bit for bit, and every layer's
-    output is checked against the oracle applied to that layer's input as the
-    replay produced it (bf16 RMSNorm, the block, bf16 residual add). Compared
-    end to end instead, 48 layers of bf16 rounding and the occasional flipped
-    near-tie in a later router would dominate the comparison."""
+    """the C4 stack at B = 1, 4 and 8: 48 Q4_K_M layers of x <- x + moe(rmsnorm(x))
+    (per-channel RMSNorm weight under the (1 + w) scaling) captured in one HIP
+    graph per batch size, with a copy of the residual stream after every layer
+    captured alongside; replayed twice, the result equals the eager stack bit
+    for bit. Every layer is then checked on the input the replay gave it: its
+    routing ids equal the oracle's bit for bit, and its output is within the
+    tolerance of the reference's arithmetic (bf16 RMSNorm, the block in candle
+    arithmetic, bf16 residual add). End to end, the oracle's own chain from the
+    same tokens is reported beside the GPU's: the normwise distance of the last
+    layer's outputs and the number of (layer, token) routing decisions in which
+    the two chains' inputs select different experts (a near-tie falling the
+    other way after 48 layers of bf16 rounding)."""
     hx, synth = _hx()
     cfg = synth.A3B
-    H, L, B = cfg.hidden_size, 48, 2
+    H, L = cfg.hidden_size, 48
+    batches = (1, 4, 8)
     norm_w = torch.linspace(-0.5, 0.5, H, device="cuda")
     wn = norm_w.cpu().numpy()
     blocks = []
@@ -239,44 +264,63 @@ def test_c4_48_layer_graph_against_oracle():
         blocks.append(hx.Qwen3_5MoeBlock.load(cfg, w, act_dtype=hx.BF16))
         del w
     print("[c4-graph] 48 layers loaded", flush=True)
-    x0 = synth.make_x(cfg, B, 12)
-    ws = torch.empty(blocks[0].workspace_size(B), dtype=torch.uint8, device="cuda")
-    xe = x0.clone()
-    for b in blocks:
-        b.decoder_mlp_(xe, norm_w, 1e-6, workspace=ws)
-    xg = x0.clone()
-    snaps = torch.empty((L, B, H), dtype=torch.bfloat16, device="cuda")
-    s = torch.cuda.Stream()
-    s.wait_stream(torch.cuda.current_stream())
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(s):
-        with torch.cuda.graph(g, stream=s):
-            for i, b in enumerate(blocks):
-                b.decoder_mlp_(xg, norm_w, 1e-6, workspace=ws, stream=s)
-                snaps[i].copy_(xg)
-    torch.cuda.current_stream().wait_stream(s)
-    for rep in range(2):
-        xg.copy_(x0)
-        snaps.zero_()
-        g.replay()
-        torch.cuda.synchronize()
-        assert torch.equal(xg, xe) and torch.equal(snaps[L - 1], xe), f"replay {rep}"
-    print("[c4-graph] replays equal the eager stack", flush=True)
-    # the oracle on every layer, one layer's weights on the host at a time
-    worst = 0.0
+    ws = torch.empty(blocks[0].workspace_size(max(batches)), dtype=torch.uint8, device="cuda")
+    x0, snaps = {}, {}
+    for B in batches:
+        x0[B] = synth.make_x(cfg, B, 12 + B)
+        xe = x0[B].clone()
+        for b in blocks:
+            b.decoder_mlp_(xe, norm_w, 1e-6, workspace=ws)
+        xg = x0[B].clone()
+        sn = torch.empty((L, B, H), dtype=torch.bfloat16, device="cuda")
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            with torch.cuda.graph(g, stream=s):
+                for i, b in enumerate(blocks):
+                    b.decoder_mlp_(xg, norm_w, 1e-6, workspace=ws, stream=s)
+                    sn[i].copy_(xg)
+        torch.cuda.current_stream().wait_stream(s)
+        for rep in range(2):
+            xg.copy_(x0[B])
+            sn.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(xg, xe) and torch.equal(sn[L - 1], xe), f"B={B} replay {rep}"
+        snaps[B] = sn
+        del g
+        print(f"[c4-graph] B={B}: replays equal the eager stack", flush=True)
+    # every layer against the oracle, one layer's weights on the host at a time;
+    # beside it the oracle's own chain from the same tokens
+    worst = {B: 0.0 for B in batches}
+    chain = {B: x_np(x0[B]) for B in batches}
+    flips = {B: 0 for B in batches}
     for i, b in enumerate(blocks):
         w = synth.make_weights(cfg, synth.FMT_Q4_K_M, 9000 + i)
         orc = O.OracleMoe(H, cfg.num_experts, cfg.num_experts_per_tok, cfg.moe_intermediate_size,
                           cfg.shared_expert_intermediate_size, cfg.norm_topk_prob, O.BF16, synth.to_numpy(w))
         del w
-        xin = x_np(x0 if i == 0 else snaps[i - 1])
-        xn = O.f32_to_bf16_bits(O.rmsnorm(xin, wn, 1e-6, O.BF16))
-        ref = O.bf16_bits_to_f32(xin) + O.bf16_bits_to_f32(O.f32_to_bf16_bits(orc.forward(xn)))
-        e = rel_err(snaps[i].float().cpu().numpy(), ref)
-        worst = max(worst, e)
-        assert e <= TOL_BF16, (i, e)
+        for B in batches:
+            xin = x_np(x0[B] if i == 0 else snaps[B][i - 1])
+            xn = O.f32_to_bf16_bits(O.rmsnorm(xin, wn, 1e-6, O.BF16))
+            _, _, ix, _ = orc.route(xn)
+            got_ix = b.route(torch.from_numpy(xn.view(np.int16)).cuda().view(torch.bfloat16))["topk_idx"]
+            assert np.array_equal(got_ix.cpu().numpy(), ix), (B, i)
+            ref = O.bf16_bits_to_f32(xin) + O.bf16_bits_to_f32(O.f32_to_bf16_bits(orc.forward_candle(xn)))
+            e = rel_err(snaps[B][i].float().cpu().numpy(), ref)
+            worst[B] = max(worst[B], e)
+            assert e <= TOL_BF16, (B, i, e)
+            cn = O.f32_to_bf16_bits(O.rmsnorm(chain[B], wn, 1e-6, O.BF16))
+            _, _, cix, _ = orc.route(cn)
+            flips[B] += int(sum(set(ix[t]) != set(cix[t]) for t in range(B)))
+            chain[B] = O.f32_to_bf16_bits(O.bf16_bits_to_f32(chain[B]) + O.bf16_bits_to_f32(
+                O.f32_to_bf16_bits(orc.forward_candle(cn))))
         b.close()
-    print(f"[c4-graph] 48 layers against the oracle: worst normwise {worst:.3e}", flush=True)
+    for B in batches:
+        e2e = rel_err(snaps[B][L - 1].float().cpu().numpy(), O.bf16_bits_to_f32(chain[B]))
+        print(f"[c4-graph] B={B}: worst layer normwise {worst[B]:.3e}; end to end against the oracle's chain "
+              f"{e2e:.3e}; routing decisions that differ between the chains: {flips[B]} of {L * B}", flush=True)
 
 
 def test_wrapper_rejects_bad_arguments():
@@ -316,19 +360,24 @@ def test_wrapper_rejects_bad_arguments():
     b.check(x, TOL_BF16)
 
 
-def test_prefill_shared_expert_side_stream_in_a_graph():
-    """prefill with a shared expert runs the shared expert's GEMMs on the
-    handle's side stream (forked from and joined back to the caller's stream):
-    captured into a HIP graph on a caller stream and replayed three times with
-    eager forwards between the replays, every replay equals the eager result
-    bit for bit, which is within tolerance of the oracle"""
+@pytest.mark.parametrize("T", [200, 2100])
+def test_prefill_forward_in_a_graph(T):
+    """a prefill forward captured into a HIP graph on a caller stream and
+    replayed three times with eager forwards between the replays: every replay
+    equals the eager result bit for bit, which is within tolerance of the
+    reference's arithmetic on sampled tokens. T = 200: the shared expert's tiles
+    ride in the routed launches (one stream); T = 2100 (above the one-stream
+    threshold of 2048 tokens): its GEMMs run on the handle's side stream,
+    forked from and joined back to the caller's stream inside the graph, with
+    a last shared tile of 52 rows"""
     _, synth = _hx()
     b = Blk(2048, 64, 8, 512, 512, True, synth.FMT_Q4_K_M, O.BF16, 313)
-    x = b.x(200, seed=13)
+    x = b.x(T, seed=13)
     ref = b.block.forward(x)
-    e = report("side-stream prefill T=200", ref.float().cpu().numpy(), b.oracle.forward(x_np(x)))
+    sample = np.linspace(0, T - 1, 8).astype(int)
+    e = report(f"prefill T={T}", ref.float().cpu().numpy()[sample], b.ref_tokens(x_np(x), sample))
     assert e["normwise"] <= TOL_BF16
-    ws = torch.empty(b.block.workspace_size(200), dtype=torch.uint8, device="cuda")
+    ws = torch.empty(b.block.workspace_size(T), dtype=torch.uint8, device="cuda")
     out = torch.zeros_like(x)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())

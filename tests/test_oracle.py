@@ -422,6 +422,32 @@ def test_candle_mode_close_to_exact_mode(fmt):
         assert 0 < rel_err(c, a) <= 3e-2
 
 
+def test_candle_mode_sampled_tokens_equal_the_full_forward():
+    """forward_candle_tokens (what the GPU tests compare sampled prefill tokens
+    with) equals the full candle forward's rows bit for bit: every expert call
+    keeps the arm of its full row count (here some experts get more than 64
+    rows, so both arms occur), and each arm computes rows independently"""
+    H, E, k, I, Is = 256, 8, 2, 256, 256
+    w = make_f32_block(42, H, E, I, Is)
+    fm = {"gate": O.Q4_K, "up": O.Q4_K, "down": O.Q6_K, "router": O.BF16, "seg": O.BF16}
+    fm.update({"sgate": O.Q4_K, "sup": O.Q4_K, "sdown": O.Q6_K})
+    orc = oracle_block((H, E, k, I, Is, True), store(w, fm), O.BF16)
+    T = 400
+    x = bf16_bits(make_x(43, T, H))
+    counts = np.bincount(orc.route(x)[2].ravel(), minlength=E)
+    assert counts.max() > 64
+    full = orc.forward_candle(x)
+    sel = np.array([0, 7, 150, 399, 8])
+    part = orc.forward_candle_tokens(x, sel)
+    assert np.array_equal(part.view(np.uint32), full[sel].view(np.uint32))
+    with pytest.raises(ValueError):
+        orc.forward_candle_tokens(x, np.array([3, 3]))
+    # and the arm really follows the full count: on the sampled tokens alone
+    # every call has m <= 5 and takes the quantised arm, which differs
+    alone = orc.forward_candle(x[sel])
+    assert not np.array_equal(alone, part)
+
+
 # ------------------------------------------------------------------ router
 def tiny(seed=0, H=64, E=8, k=2, I=16, Is=16, norm=True, act=O.F32, fmt=None):
     w = make_f32_block(seed, H, E, I, Is, std=0.5)
