@@ -16,24 +16,27 @@
 
 namespace hx {
 
-// one row of K elements (K % 256 == 0 for Q8_K, % 32 for Q8_0): load(g, x)
+// groups g0 .. g0 + 63 of a row of G groups of 8 (one pass of a wave; G % 4 ==
+// 0, % 32 for Q8_K, so a block lies wholly inside or past the row): load(g, x)
 // fills the 8 values of group g, emit(g, q, d) takes its codes and block d
 template <int FMT, class Load, class Emit>
-HX_DEV void quant_row(int K, Load load, Emit emit) {
-  const int G = K / 8, lane = lane_id();
-  for (int g0 = 0; g0 < G; g0 += 64) {   // wave-uniform: every lane takes part in the block reductions
-    const int g = g0 + lane;
-    float x[8];
-    if (g < G) {
-      load(g, x);
-    } else {
+HX_DEV void quant_pass(int g0, int G, Load load, Emit emit) {
+  const int g = g0 + lane_id();
+  float x[8];
+  if (g < G) {
+    load(g, x);
+  } else {
 #pragma unroll
-      for (int j = 0; j < 8; j++) x[j] = 0.f;   // whole blocks past the end (G % 4 == 0, % 32 for Q8_K)
-    }
-    float q[8], d;
-    quant_group<FMT>(x, q, d);
-    if (g < G) emit(g, q, d);
+    for (int j = 0; j < 8; j++) x[j] = 0.f;
   }
+  float q[8], d;
+  quant_group<FMT>(x, q, d);
+  if (g < G) emit(g, q, d);
+}
+// a row of K elements (K % 256 == 0 for Q8_K, % 32 for Q8_0) in passes
+template <int FMT, class Load, class Emit>
+HX_DEV void quant_row(int K, Load load, Emit emit) {
+  for (int g0 = 0; g0 < K / 8; g0 += 64) quant_pass<FMT>(g0, K / 8, load, emit);   // wave-uniform
 }
 
 HX_DEV void load_bf16x8(const uint16_t* p, float (&x)[8]) {
@@ -61,34 +64,29 @@ HX_DEV void store_fq8(uint16_t* p, const float (&q)[8], float d, bool nat) {
   *(uint4*)p = nat ? make_uint4(pk(0, 1), pk(2, 3), pk(4, 5), pk(6, 7)) : make_uint4(pk(0, 2), pk(1, 3), pk(4, 6), pk(5, 7));
 }
 
-template <int FMT>
-HX_DEV void fq_row_bf16(const uint16_t* src, int K, uint16_t* dst, bool nat) {
-  quant_row<FMT>(K, [&](int g, float (&x)[8]) { load_bf16x8(src + 8 * g, x); },
-                 [&](int g, const float (&q)[8], float d) { store_fq8(dst + 8 * g, q, d, nat); });
-}
-template <int FMT>
-HX_DEV void fq_row_f32(const float* src, int K, uint16_t* dst, bool nat) {
-  quant_row<FMT>(K, [&](int g, float (&x)[8]) { load_f32x8(src + 8 * g, x); },
-                 [&](int g, const float (&q)[8], float d) { store_fq8(dst + 8 * g, q, d, nat); });
-}
-
 // ---------------------------------------------------------------- prefill
 // tokens (bf16) -> xq: the f16 operand of the m <= 64 expert calls, in the
 // order of xh (natural for Q4_K gate/up, else swizzled); one wave per token
+// and 512 elements (grid.y: the row's passes)
 template <int FMT>
 __global__ __launch_bounds__(256) void k_xq_fq(ExpertArgs a, int nat) {
   const int t = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
   if (t >= a.T) return;
-  fq_row_bf16<FMT>((const uint16_t*)a.x + (int64_t)t * a.H, a.H, a.xq + (int64_t)t * a.H, nat != 0);
+  const uint16_t* src = (const uint16_t*)a.x + (int64_t)t * a.H;
+  uint16_t* dst = a.xq + (int64_t)t * a.H;
+  quant_pass<FMT>(64 * (int)blockIdx.y, a.H / 8, [&](int g, float (&x)[8]) { load_bf16x8(src + 8 * g, x); },
+                  [&](int g, const float (&q)[8], float d) { store_fq8(dst + 8 * g, q, d, nat != 0); });
 }
 
 // rows of h (f32, written by the gate/up kernels for the m <= 64 expert calls)
-// -> hbf as f16 d q in the swizzled order; workgroup = one M tile of the
-// dispatch list (or, for the shared expert's own launch, of T), its waves
-// taking rows w, w + 4, ...; tiles of the f16 arm (m > 64) are skipped
+// -> hbf as f16 d q in the swizzled order; workgroup (x, y) = rows 4 y .. 4 y + 3
+// of M tile x of the dispatch list (or, for the shared expert's own launch,
+// of T), one row per wave; tiles of the f16 arm (m > 64) are skipped. (Placing
+// each tile's workgroups on the XCD of its gate/up and down workgroups was
+// measured slower: C3 15.5 -> 17.1 us.)
 template <int FMT>
 __global__ __launch_bounds__(256) void k_hq_fq(ExpertArgs a) {
-  const int tile = blockIdx.x;
+  const int tile = blockIdx.x, nt = blockIdx.y;
   int m, p0, rows, K;
   if (a.tsel == HX_TILES_SHARED) {
     const int m0 = tile * HX_TILE_M;
@@ -106,9 +104,12 @@ __global__ __launch_bounds__(256) void k_hq_fq(ExpertArgs a) {
     rows = a.tiles[4 * tile + 3];
     K = e == a.E ? a.Is : a.I;
   }
-  if (m > HX_QUANT_M) return;
-  for (int r = (int)(threadIdx.x >> 6); r < rows; r += 4)
-    fq_row_f32<FMT>(a.hbuf + (int64_t)(p0 + r) * a.hstride, K, a.hbf + (int64_t)(p0 + r) * a.hstride, false);
+  const int r = 4 * nt + (int)(threadIdx.x >> 6);
+  if (m > HX_QUANT_M || r >= rows) return;
+  const float* src = a.hbuf + (int64_t)(p0 + r) * a.hstride;
+  uint16_t* dst = a.hbf + (int64_t)(p0 + r) * a.hstride;
+  quant_row<FMT>(K, [&](int g, float (&x)[8]) { load_f32x8(src + 8 * g, x); },
+                 [&](int g, const float (&q)[8], float d) { store_fq8(dst + 8 * g, q, d, false); });
 }
 
 // ---------------------------------------------------------------- generic paths
@@ -191,7 +192,7 @@ __global__ __launch_bounds__(256) void k_actq_codes(const void* x, int xbf, int6
 bool gguf_fmt(int fmt) { return fmt == HX_Q8_0 || fmt == HX_Q4_K || fmt == HX_Q6_K; }
 
 hipError_t launch_xq_fq(const ExpertArgs& a, hipStream_t s) {
-  const dim3 g((unsigned)((a.T + 3) / 4));
+  const dim3 g((unsigned)((a.T + 3) / 4), (unsigned)((a.H + 511) / 512));
   const int nat = xh_natural(a.gate.fmt) ? 1 : 0;
 #define L(F) hipLaunchKernelGGL((k_xq_fq<F>), g, dim3(256), 0, s, a, nat)
   HX_VD_SWITCH(a.gate.fmt, L)
@@ -200,7 +201,7 @@ hipError_t launch_xq_fq(const ExpertArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_hq_fq(const ExpertArgs& a, int ntiles, hipStream_t s) {
-  const dim3 g((unsigned)ntiles);
+  const dim3 g((unsigned)ntiles, (unsigned)(HX_TILE_M / 4));
 #define L(F) hipLaunchKernelGGL((k_hq_fq<F>), g, dim3(256), 0, s, a)
   HX_VD_SWITCH(a.down.fmt, L)
 #undef L

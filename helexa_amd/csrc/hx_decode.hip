@@ -486,18 +486,26 @@ __global__ __launch_bounds__(256) void k_gate_up_plan(ExpertArgs a) {
 // the row in the canonical layout (group g of 8 in lane g % 64, register
 // g / 64), quantised to the vec_dot type of the down weights.
 // ----------------------------------------------------------------------------
-template <int FMT, int NG>
-HX_DEV void h_row_records(const float* hrow, uint32_t* rec) {
+template <int NG>
+HX_DEV void h_row_load(const float* hrow, float (&x)[NG][8]) {
   const int lane = lane_id();
-  float x[NG][8];
 #pragma unroll
   for (int i = 0; i < NG; i++) {
     const float4 p = *(const float4*)(hrow + 8 * (lane + 64 * i)), q = *(const float4*)(hrow + 8 * (lane + 64 * i) + 4);
     x[i][0] = p.x; x[i][1] = p.y; x[i][2] = p.z; x[i][3] = p.w;
     x[i][4] = q.x; x[i][5] = q.y; x[i][6] = q.z; x[i][7] = q.w;
   }
+}
+template <int FMT, int NG>
+HX_DEV void h_regs_records(const float (&x)[NG][8], uint32_t* rec) {
 #pragma unroll
-  for (int i = 0; i < NG; i++) group_to_record<FMT>(x[i], lane + 64 * i, rec);
+  for (int i = 0; i < NG; i++) group_to_record<FMT>(x[i], lane_id() + 64 * i, rec);
+}
+template <int FMT, int NG>
+HX_DEV void h_row_records(const float* hrow, uint32_t* rec) {
+  float x[NG][8];
+  h_row_load<NG>(hrow, x);
+  h_regs_records<FMT, NG>(x, rec);
 }
 
 // the rows of h of a forward (routed, then the shared expert's) into a.hrec
@@ -516,10 +524,12 @@ __global__ __launch_bounds__(256) void k_hrec(ExpertArgs a, int nrows) {
 // expert), as the reference's combine order; with several groups, the group's
 // partial sum, which k_down_reduce adds up in group order.
 // QH (one token, every row of h in one group): the workgroup quantises the
-// rows of h into chunk records in LDS itself -- after issuing its weight
-// loads, so the quantisation runs while the weights stream in; wave w takes
-// rows w, w + NW, ... Otherwise the records come from k_hrec and each wave
-// loads those of a row from memory right before its dot product.
+// rows of h into chunk records in LDS itself; wave w takes rows w, w + NW, ...
+// whose loads it issues first of all (they need no plan), so that the memory
+// counters let the quantisation start once they have arrived, while the
+// weight loads issued after them are still in flight. Otherwise the records
+// come from k_hrec and each wave loads those of a row from memory right
+// before its dot product.
 // ----------------------------------------------------------------------------
 template <int FMT, int LPR, int SPW, int NW, bool QH>
 __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
@@ -539,6 +549,13 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
   const int nh_all = a.F + (a.Is > 0 ? T : 0);   // rows of h in use
   const int h0 = blockIdx.y * ROWS;              // this workgroup's group of rows
   const int nh = min(nh_all - h0, ROWS);
+  float hx[QH ? SPW : 1][QH ? NG : 1][8];
+  if constexpr (QH) {
+    const int w = threadIdx.x >> 6;
+#pragma unroll
+    for (int s = 0; s < SPW; s++)   // rows past the group's end read its first row (not quantised)
+      h_row_load<NG>(a.hbuf + (int64_t)(h0 + (w + NW * s < nh ? w + NW * s : 0)) * a.hstride, hx[s]);
+  }
   {
     // thread 32 part + r < 96 loads row r's token (part 0), weight (1) or
     // expert (2); one load each, clamped to a valid row, so one round trip.
@@ -572,8 +589,9 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
   }
   if constexpr (QH) {
     __builtin_amdgcn_sched_barrier(0);   // the weight loads go out first
-    for (int hr = wave; hr < nh; hr += NW)
-      h_row_records<FMT, NG>(a.hbuf + (int64_t)(h0 + hr) * a.hstride, srec + hr * LPR * HX_XCV_WORDS);
+#pragma unroll
+    for (int s = 0; s < SPW; s++)
+      if (wave + NW * s < nh) h_regs_records<FMT, NG>(hx[s], srec + (wave + NW * s) * LPR * HX_XCV_WORDS);
     __syncthreads();
   }
 #pragma unroll

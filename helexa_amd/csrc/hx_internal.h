@@ -27,6 +27,20 @@
 
 namespace hx {
 
+// XCD-aware work mapping of the prefill kernels. Workgroups are dealt to the 8
+// XCDs round-robin by linear id (XCD = id % 8), each with its own L2. The
+// launch grid is (NX, tiles rounded up to 8); linear id L is mapped so that the
+// NX workgroups of one M tile land on the same XCD, XCD tile % 8: the tile's
+// gathered activation rows are fetched into one L2 and read from there by all
+// NX workgroups, and every kernel of a forward that works on a tile's rows
+// (gate/up, the quantisation of h, down) finds them in that L2.
+__device__ __forceinline__ void xcd_tile(int& nt, int& tile) {
+  const int NX = gridDim.x, L = blockIdx.y * NX + blockIdx.x;
+  const int group = L / (8 * NX), xcd = L & 7;
+  nt = (L >> 3) % NX;
+  tile = group * 8 + xcd;
+}
+
 struct DispatchArgs {
   int32_t* topk_idx;   // [T*k] (input)
   int T, k, E, F;
@@ -101,6 +115,11 @@ struct RouterArgs {
   // plane 0 is `logits`, plane z >= 1 at mplanes + (z - 1) T (E + 1)
   int msplit = 1;
   float* mplanes = nullptr;
+  // MFMA prefill routing: each routing wave also writes its token's xq (the
+  // f16 d q of its Q8 codes for the m <= 64 expert calls, ExpertArgs::xq):
+  // Q8_0 codes when xq_q80, else Q8_K; natural element order when xq_nat
+  uint16_t* xq = nullptr;
+  bool xq_q80 = false, xq_nat = false;
 };
 // most logit planes of the MFMA prefill router
 #define HX_RM_SPLITS 4

@@ -725,7 +725,15 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
       p.ea.tsel = HX_TILES_ROUTED;
       p.ea.shared_raw = true;
     }
-    if (mfma) HX_HIP(launch_xq_fq(p.ea, s));
+    // xq: written by the MFMA routing waves (which hold the token rows), else
+    // by its own kernel
+    if (mfma && xh_in_router) {
+      p.ra.xq = p.ea.xq;
+      p.ra.xq_q80 = p.ea.gate.fmt == HX_Q8_0;
+      p.ra.xq_nat = xh_natural(p.ea.gate.fmt);
+    } else if (mfma) {
+      HX_HIP(launch_xq_fq(p.ea, s));
+    }
     if ((rc = run_route_dispatch(m, p, s))) return rc;
     if (mfma) {
       tm_ext(m, SLOT_GATE_UP, s);

@@ -214,18 +214,6 @@ struct ARaw {
   }
 };
 
-// XCD-aware work mapping. Workgroups are dealt to the 8 XCDs round-robin by
-// linear id (XCD = id % 8), each with its own L2. The launch grid is
-// (NX, tiles rounded up to 8); linear id L is mapped so that the NX workgroups
-// of one M tile (its N tiles) land on the same XCD: the gathered activation
-// rows of the tile are then fetched into one L2 and read from there by all
-// NX workgroups.
-HX_DEV void xcd_tile(int& nt, int& tile) {
-  const int NX = gridDim.x, L = blockIdx.y * NX + blockIdx.x;
-  const int group = L / (8 * NX), xcd = L & 7;
-  nt = (L >> 3) % NX;
-  tile = group * 8 + xcd;
-}
 
 HX_DEV f16x8_t frag(const uint16_t* base) { return __builtin_bit_cast(f16x8_t, *(const uint4*)base); }
 
@@ -544,7 +532,7 @@ HX_DEV void q4k_main(const ExpertArgs& a, uint8_t* ring, const Q4kSrc<Q>& src, i
 #pragma unroll
       for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) ot[(16 * mt + 4 * kq + i) * OP + col] = siluf_(accg[mt][j][i]) * accu[mt][j][i];
+        for (int i = 0; i < 4; i++) ot[(16 * mt + 4 * kq + i) * OP + col] = silu_rcp(accg[mt][j][i]) * accu[mt][j][i];
     }
     __syncthreads();
     constexpr int PER_ROW = Q::COLS / 4;

@@ -66,18 +66,38 @@ HX_DEV void group_slot(int g, int& c, int& s) {
   }
 }
 
+// Reductions over a block of W consecutive lanes (W = 4 or 32) by register
+// moves, every lane of the wave taking part. Quads by DPP quad_perm (lane ^ 1,
+// lane ^ 2). A row of 16 by two DPP row rotations, 4 and then 8 lanes: after
+// the quad step each lane holds its quad's value, the rotation by 4 adds a
+// neighbouring quad and the rotation by 8 the other two, whichever way the
+// rotation turns. Two rows by permlane16_swap, whose two results hold the
+// values of rows 2i and 2i + 1 in both rows; the reduction takes both.
+template <typename Op>
+HX_DEV uint32_t lanes_reduce4(uint32_t v, Op op) {
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xf, 0xf, true));   // quad_perm [1,0,3,2]
+  return op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xf, 0xf, true));   // quad_perm [2,3,0,1]
+}
+template <typename Op>
+HX_DEV uint32_t lanes_reduce32(uint32_t v, Op op) {
+  v = lanes_reduce4(v, op);
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xf, 0xf, true));   // row_ror:4
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xf, 0xf, true));   // row_ror:8
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return op(r[0], r[1]);
+}
+
 // max over the W consecutive lanes of a block (W = 4 or 32)
 template <int W>
 HX_DEV float block_max(float v) {
-#pragma unroll
-  for (int off = 1; off < W; off <<= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  const auto op = [](uint32_t a, uint32_t b) { return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b))); };
+  const uint32_t u = __float_as_uint(v);
+  return __uint_as_float(W == 32 ? lanes_reduce32(u, op) : lanes_reduce4(u, op));
 }
 template <int W>
 HX_DEV int block_min(int v) {
-#pragma unroll
-  for (int off = 1; off < W; off <<= 1) v = min(v, __shfl_xor(v, off, 64));
-  return v;
+  const auto op = [](uint32_t a, uint32_t b) { return (uint32_t)min((int)a, (int)b); };
+  return (int)(W == 32 ? lanes_reduce32((uint32_t)v, op) : lanes_reduce4((uint32_t)v, op));
 }
 
 // Quantise one group of 8 (this lane's) of a block spread over consecutive

@@ -45,6 +45,7 @@
 //    this path requires: the softmax denominator cancels), within a few ulps
 //    of the reference's p_r / sum p.
 #include "hx_internal.h"
+#include "hx_quant.h"
 #include "hx_route_small.h"
 
 namespace hx {
@@ -292,6 +293,37 @@ struct alignas(16) RouteMfmaSmem {
 // 2^-126 times that
 #define HX_RM_ABS 0x1p-100f
 
+// the token's xq from its row in the canonical layout (group g of 8 in lane
+// g % 64, register g / 64): the Q8 codes of the m <= 64 expert calls (a Q8_K
+// block is 32 consecutive lanes of a register, a Q8_0 block 4), stored as f16
+// d q in xh's element order; lanes past the row hold whole zero blocks
+template <int FMT, int NG>
+HX_DEV void route_xq(const RouterArgs& a, const uint32_t (&xr)[NG][4], int t) {
+  const int G = a.H / 8, lane = lane_id();
+  uint16_t* dst = a.xq + (int64_t)t * a.H;
+#pragma unroll
+  for (int i = 0; i < NG; i++) {
+    const int g = lane + 64 * i;
+    float x[8], q[8], d;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      x[2 * j] = g < G ? __uint_as_float(xr[i][j] << 16) : 0.0f;
+      x[2 * j + 1] = g < G ? __uint_as_float(xr[i][j] & 0xffff0000u) : 0.0f;
+    }
+    quant_group<FMT>(x, q, d);
+    if (g < G) {
+      _Float16 h[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++) h[j] = fq_f16(q[j], d);
+      auto pk = [&](int u, int v) {
+        return (uint32_t)__builtin_bit_cast(uint16_t, h[u]) | ((uint32_t)__builtin_bit_cast(uint16_t, h[v]) << 16);
+      };
+      *(uint4*)(dst + 8 * g) = a.xq_nat ? make_uint4(pk(0, 1), pk(2, 3), pk(4, 5), pk(6, 7))
+                                        : make_uint4(pk(0, 2), pk(1, 3), pk(4, 6), pk(5, 7));
+    }
+  }
+}
+
 template <int EPL, int NG>
 __global__ __launch_bounds__(256) void k_route_mfma(RouterArgs a) {
   __shared__ RouteMfmaSmem sm;
@@ -353,6 +385,10 @@ __global__ __launch_bounds__(256) void k_route_mfma(RouterArgs a) {
     }
   }
   ss = wave_sum<64>(ss);
+  if (a.xq) {   // wave-uniform
+    if (a.xq_q80) route_xq<HX_Q8_0, NG>(a, xr, t);
+    else route_xq<HX_Q4_K, NG>(a, xr, t);
+  }
   const float nx = sqrtf(ss * (1.0f + 0x1p-16f)) * (1.0f + 0x1p-20f);
   float lsh = 0.0f;   // the shared expert's gate logit
   if (a.has_shared) {
