@@ -206,7 +206,7 @@ void launch_route_tokens(const RouterArgs& a, hipStream_t s);
 hipError_t launch_dispatch(const DispatchArgs& d, hipStream_t s, bool maps_ready = false);
 // prefill routing with the router GEMM on MFMA (bf16 tokens and router rows,
 // renormalised top-k): approximate logits, then per token the exact top-k
-bool route_mfma_ok(const RouterArgs& a, bool xbf, bool rbf);
+bool route_mfma_ok(const RouterArgs& a, bool xbf, bool rbf, bool gfx950);
 int route_mfma_splits(const RouterArgs& a);
 // also writes the f16 tokens for the MFMA expert kernels when xh is not null,
 // and clears the dispatch histogram and bitmap that launch_route_mfma fills

@@ -101,6 +101,7 @@ struct Timing {
 struct hx_moe {
   hx_moe_config cfg{};
   int device = 0;
+  bool gfx950 = false;   // the device's architecture, checked at creation
   int E1 = 0;
   int rdt = HX_F32;   // dtype of the combined router rows
   void* router = nullptr;
@@ -357,8 +358,17 @@ extern "C" int hx_moe_create(const hx_moe_config* cfg, const hx_moe_weights* w, 
       return fail(HX_ERR_UNSUPPORTED, "intermediate size too large");
   }
   if (hipSetDevice(device) != hipSuccess) return fail(HX_ERR_DEVICE, "hipSetDevice(%d) failed", device);
+  // the library holds gfx950 code objects only, and the MFMA routing's error
+  // bound rests on gfx950's f16 MFMA accumulation
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess)
+    return fail(HX_ERR_DEVICE, "hipGetDeviceProperties(%d) failed", device);
+  const bool gfx950 = strncmp(prop.gcnArchName, "gfx950", 6) == 0 &&
+                      (prop.gcnArchName[6] == '\0' || prop.gcnArchName[6] == ':');
+  if (!gfx950) return fail(HX_ERR_UNSUPPORTED, "device %d is %s; libhxmoe is built for gfx950 only", device, prop.gcnArchName);
   if ((rc = scratch_init(device))) return rc;
   hx_moe* m = new hx_moe();
+  m->gfx950 = gfx950;
   m->cfg = c;
   m->device = device;
   // the fork / join events order work of two streams on this one device: a
@@ -552,7 +562,7 @@ static void tm_ext_done(hx_moe* m, int slot) {
 
 // the prefill routing on MFMA (approximate logits, exact top-k per token)
 static bool route_mfma(const hx_moe* m, const Plan& p) {
-  return route_mfma_ok(p.ra, m->cfg.act_dtype == HX_BF16, m->rdt == HX_BF16);
+  return route_mfma_ok(p.ra, m->cfg.act_dtype == HX_BF16, m->rdt == HX_BF16, m->gfx950);
 }
 
 // xh: where the MFMA router also writes the f16 tokens (or null)

@@ -568,12 +568,14 @@ __global__ __launch_bounds__(256) void k_row_norms(const uint16_t* R, int E1, in
   if (lane == 0) out[row] = __double2float_ru(sqrt(s) * (1.0 + 0x1p-40));
 }
 
-bool route_mfma_ok(const RouterArgs& a, bool xbf, bool rbf) {
+// gfx950: the device is gfx950, whose v_mfma_f32_16x16x32_f16 accumulation
+// the logit error bound (alpha) was measured on; any other target is refused
+bool route_mfma_ok(const RouterArgs& a, bool xbf, bool rbf, bool gfx950) {
   const int ngr = a.H / (32 * RM_GROUP);   // accumulation groups of 128 (two K steps of 64)
   const bool shape = a.H % (32 * RM_GROUP) == 0 &&
                      (ngr == 1 || ngr == 2 || ngr == 3 || ngr == 4 || ngr == 6 || ngr == 8 || ngr == 12 ||
                       ngr == 16 || ngr == 24 || ngr == 32);
-  return shape && xbf && rbf && a.rnorm && a.norm && a.T > HX_DECODE_MAX_T && a.H <= 4096 &&
+  return gfx950 && shape && xbf && rbf && a.rnorm && a.norm && a.T > HX_DECODE_MAX_T && a.H <= 4096 &&
          a.E >= 1 && a.E <= 1024 && a.k >= 1 && a.k <= 64 && a.k <= a.E;
 }
 

@@ -18,6 +18,98 @@ def test_header_declares_the_python_export_list():
     assert declared_functions() == sorted(EXPORTS)
 
 
+# C scalar types of the header and their Rust spellings in hx-moe-sys
+C_TO_RUST = {"int": "c_int", "int32_t": "i32", "int64_t": "i64", "int8_t": "i8", "size_t": "usize", "float": "f32",
+             "double": "f64", "char": "c_char", "void": "c_void"}
+
+
+def strip_c_comments(text):
+    return re.sub(r"//[^\n]*", "", re.sub(r"/\*.*?\*/", "", text, flags=re.S))
+
+
+def c_type_to_rust(ctype):
+    """a C parameter or return type of the header spelled the way a Rust
+    binding declares it: `const T*` -> `*const T`, `T*` -> `*mut T`, `T**` ->
+    `*mut *mut T`, scalars by C_TO_RUST, the library's own types unchanged"""
+    const = bool(re.match(r"\s*const\b", ctype))
+    base = re.sub(r"\bconst\b|\*", " ", ctype).split()
+    assert len(base) == 1, ctype
+    depth = ctype.count("*")
+    out = C_TO_RUST.get(base[0], base[0])
+    for level in range(depth):
+        out = ("*const " if const and level == 0 else "*mut ") + out
+    return out
+
+
+def header_functions():
+    """{name: (return type, [(param name, Rust type)])} for every function
+    declared in include/hx_moe.h, types translated by c_type_to_rust"""
+    text = strip_c_comments(open(os.path.join(ROOT, "include", "hx_moe.h")).read())
+    out = {}
+    for ret, name, params in re.findall(r"((?:const\s+)?\w+\s*\**)\s*\b(hx_\w+)\s*\(([^)]*)\)\s*;", text):
+        args = []
+        for p in [p.strip() for p in params.split(",")]:
+            if p in ("", "void"):
+                continue
+            m = re.match(r"(.*?)(\w+)$", p, re.S)
+            args.append((m.group(2), c_type_to_rust(m.group(1))))
+        out[name] = (c_type_to_rust(ret), args)
+    return out
+
+
+def rust_functions():
+    """the same map for the extern "C" block of crates/hx-moe-sys/src/lib.rs"""
+    text = open(os.path.join(ROOT, "crates", "hx-moe-sys", "src", "lib.rs")).read()
+    block = re.search(r'extern "C" \{(.*?)\n\}', text, re.S).group(1)
+    out = {}
+    for name, params, ret in re.findall(r"pub fn (hx_\w+)\(([^)]*)\)\s*(?:->\s*([^;]+))?;", block):
+        args = []
+        for p in [p.strip() for p in params.split(",") if p.strip()]:
+            pname, ptype = p.split(":", 1)
+            args.append((pname.strip(), " ".join(ptype.split())))
+        out[name] = (" ".join(ret.split()) if ret else "()", args)
+    return out
+
+
+def test_rust_sys_crate_declares_every_header_function_with_its_signature():
+    """crates/hx-moe-sys/src/lib.rs is the raw binding a helexa maintainer
+    adds: every function of the header, same argument names, order and types
+    (pointer constness included), same return types; nothing more"""
+    c, r = header_functions(), rust_functions()
+    assert sorted(c) == sorted(declared_functions())
+    assert sorted(r) == sorted(c), (sorted(set(c) ^ set(r)))
+    for name in c:
+        assert r[name] == c[name], (name, c[name], r[name])
+
+
+def test_c_type_translation_spot_checks():
+    """the translation the signature test relies on, on the header's shapes"""
+    assert c_type_to_rust("const hx_moe_config*") == "*const hx_moe_config"
+    assert c_type_to_rust("hx_moe**") == "*mut *mut hx_moe"
+    assert c_type_to_rust("const void* ") == "*const c_void"
+    assert c_type_to_rust("size_t") == "usize"
+    assert c_type_to_rust("const char*") == "*const c_char"
+    assert c_type_to_rust("int64_t*") == "*mut i64"
+
+
+def test_rust_sys_crate_constants_and_structs_match_the_header():
+    """#define values and the field order / types of hx_moe_config and
+    hx_moe_weights, the layouts #[repr(C)] must reproduce"""
+    htext = strip_c_comments(open(os.path.join(ROOT, "include", "hx_moe.h")).read())
+    rtext = open(os.path.join(ROOT, "crates", "hx-moe-sys", "src", "lib.rs")).read()
+    defines = dict(re.findall(r"#define (HX_\w+) (\d+)\b", htext))
+    consts = dict(re.findall(r"pub const (HX_\w+): \w+ = (\d+);", rtext))
+    assert defines and defines == consts
+    assert re.search(r"HX_NOALLOC_SCRATCH_BYTES \(\(size_t\)64 << 20\)", htext)
+    assert re.search(r"HX_NOALLOC_SCRATCH_BYTES: usize = 64 << 20;", rtext)
+    for struct in ("hx_moe_config", "hx_moe_weights"):
+        body = re.search(r"typedef struct %s \{(.*?)\}" % struct, htext, re.S).group(1)
+        cfields = [(n, c_type_to_rust(t)) for t, n in re.findall(r"((?:const\s+)?\w+\s*\**)\s*(\w+);", body)]
+        rbody = re.search(r"pub struct %s \{(.*?)\n\}" % struct, rtext, re.S).group(1)
+        rfields = [(n, " ".join(t.split())) for n, t in re.findall(r"pub (\w+): ([^,]+),", rbody)]
+        assert cfields == rfields, struct
+
+
 def test_library_exports_every_declared_symbol():
     import ctypes
     from helexa_amd.moe import LIB_PATH
