@@ -342,6 +342,61 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
 }
 
 // ----------------------------------------------------------------------------
+// The routing and decode plan of one token, written by the wave that routed it
+// straight from its registers (lane j < k: rank j's expert e, weight w and
+// dispatch position pos): the words publish_route writes from RouteSmem for
+// T = 1. The k experts are distinct, so each is a slot of one row at its
+// dispatch position, and offsets[x] is the number of them below x.
+// ----------------------------------------------------------------------------
+HX_DEV void publish_one_token(const DispatchArgs& d, float* topk_w, float* sgw, int e, float w, int pos, float sg) {
+  const int lane = lane_id(), k = d.k, E = d.E;
+  const bool all = !d.plan_only;
+  const int tok0 = 4 + 4 * d.max_slots, w0 = tok0 + k + 1, e0 = w0 + k + 1;   // F = k, T = 1
+  if (lane < k) {
+    if (all) {
+      d.topk_idx[lane] = e;
+      topk_w[lane] = w;
+      d.perm[pos] = lane;
+      if (d.inv) d.inv[lane] = pos;
+      d.slots[3 * pos + 0] = e;
+      d.slots[3 * pos + 1] = pos;
+      d.slots[3 * pos + 2] = 1;
+    }
+    d.plan[tok0 + pos] = 0;
+    d.plan[w0 + pos] = __float_as_int(w);
+    d.plan[e0 + pos] = e;
+    *(int4*)(d.plan + 4 + 4 * pos) = make_int4(e, pos, 1, 0);
+  }
+  if (lane == 0) {
+    if (all) sgw[0] = sg;
+    d.plan[tok0 + k] = 0;
+    d.plan[w0 + k] = __float_as_int(sg);
+    d.plan[e0 + k] = E;
+    if (d.has_shared) {
+      if (all) {
+        d.slots[3 * k + 0] = E;
+        d.slots[3 * k + 1] = k;
+        d.slots[3 * k + 2] = 1;
+      }
+      *(int4*)(d.plan + 4 + 4 * k) = make_int4(E, k, 1, 0);
+    }
+    const int ns = k + (d.has_shared ? 1 : 0);
+    if (all) {
+      d.counts[0] = ns;
+      d.counts[1] = 0;
+    }
+    d.plan[0] = ns;
+  }
+  if (all) {
+    for (int x = lane; x <= E; x += 64) {
+      int c = 0;
+      for (int j = 0; j < k; j++) c += __builtin_amdgcn_readlane(e, j) < x;
+      d.offsets[x] = c;
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
 // K2 for one token with H = 64 chunks of 32 and k = KR: a wave owns one row
 // of the gate or of the up projection (waves 2i and 2i + 1: row 2b + i of
 // workgroup b) for the KR routed experts and the shared expert. Every wave
@@ -351,15 +406,16 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
 // shared expert's row and the token's chunk record are loaded before routing
 // starts. The KR + 1 dot products of a wave are summed by one reduce-scatter,
 // and wave 2i combines them with wave 2i + 1's into h = silu(gate) * up,
-// stored (f32) at the row of h of the expert's dispatch position. Workgroup 0
-// also publishes the plan (and, unless the forward asks for the plan only,
-// the routing).
+// stored (f32) at the row of h of the expert's dispatch position. Wave 0 of
+// workgroup 0 also publishes the plan (and, unless the forward asks for the
+// plan only, the routing) from its registers as soon as the selection ends
+// (measured on MI355X: 0.4 us shorter than a whole-workgroup publication
+// after the dot products).
 // ----------------------------------------------------------------------------
 template <int FMT, int EPL, int KR>
 __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a) {
   using D = DChunk<FMT>;
   static_assert(KR < 16, "the rank-r sums and the shared one fit 16 values");
-  __shared__ RouteSmem sm;
   __shared__ float sums[4][16];
   const int wave = threadIdx.x >> 6, lane = lane_id();
   const int mat = wave & 1;                       // 0: gate, 1: up
@@ -405,6 +461,8 @@ __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a
   int pos = 0;
 #pragma unroll
   for (int j = 0; j < KR; j++) pos += __builtin_amdgcn_readlane(my_e, j) < my_e;
+  if (blockIdx.x == 0 && wave == 0)
+    publish_one_token(r.d, r.topk_w, r.sgw, my_e, my_w, pos, r.has_shared ? sigmoidf_(sg) : 0.0f);
   uint32_t xp[D::NX];
   float xs[D::NS], dx;
   unpack_record<D>(xr, xp, xs, dx);
@@ -417,23 +475,6 @@ __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a
   for (int j = KR + 1; j < 16; j++) v[j] = 0.f;
   rs_vals64<16>(v);   // lane l: value l / 4
   if ((lane & 3) == 0) sums[wave][lane >> 2] = v[0];
-  const bool publisher = blockIdx.x == 0;
-  if (publisher && wave == 0) {
-    if (lane < KR) {
-      sm.idx[lane] = my_e;
-      sm.w[lane] = my_w;
-      sm.pos[lane] = pos;
-      sm.perm[pos] = lane;
-      sm.first[lane] = 1;
-      sm.slots[3 * pos + 0] = my_e;
-      sm.slots[3 * pos + 1] = pos;
-      sm.slots[3 * pos + 2] = 1;
-    }
-    if (lane == 0) {
-      sm.sgw[0] = r.has_shared ? sigmoidf_(sg) : 0.0f;
-      sm.nroute = KR;
-    }
-  }
   __syncthreads();
   if (mat == 0 && lane <= KR) {
     const float g = sums[wave][lane], u = sums[wave + 1][lane];
@@ -441,7 +482,6 @@ __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a
     if (lane < KR && rrow) a.hbuf[(int64_t)pos * a.hstride + row] = h;
     if (lane == KR && shrow) a.hbuf[(int64_t)a.F * a.hstride + row] = h;
   }
-  if (publisher) publish_route(r.d, r.topk_w, r.sgw, sm);
 }
 
 // ----------------------------------------------------------------------------
@@ -687,11 +727,18 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe(ExpertArgs a) {
   const int n0 = blockIdx.x * RG, row = n0 + rg;
   Raw ra[SPW], rb[SPW];
   u32x4v xv[REC];   // a native vector type, so the array stays in registers across the loop
-  // loads of group g: the wave's SPW weight rows (rows past the end read
-  // row 0 of the group, dropped later) and this thread's chunk record (item
-  // q = thread: row q / NC, chunk q % NC; past the end, the group's last row)
+  // loads of group g: this thread's chunk record (item q = thread: row
+  // q / NC, chunk q % NC; past the end, the group's last row), then the
+  // wave's SPW weight rows (rows past the end read row 0 of the group,
+  // dropped later). The record goes first: the memory counter retires loads
+  // in issue order, so staging the record waits for it alone and the
+  // weights stay in flight until the group's dot products.
   auto issue = [&](int g, Raw(&raw)[SPW]) __attribute__((always_inline)) {
     const int h0 = g * ROWS, nh = min(nh_all - h0, ROWS);
+    {
+      const int q = min((int)threadIdx.x, nh * NC - 1), hr = q / NC, cc = q % NC;
+      load_record((const u32x4v*)(a.hrec + ((int64_t)(h0 + hr) * NC + cc) * HX_XCV_WORDS), xv);
+    }
 #pragma unroll
     for (int s = 0; s < SPW; s++) {
       const int hr = wave + NW * s, hq = hr < nh ? hr : 0;
@@ -700,8 +747,6 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe(ExpertArgs a) {
       const int K = sh ? a.Is : a.I;
       D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row < a.H ? row : 0, c < K / 32 ? c : 0, raw[s]);
     }
-    const int q = min((int)threadIdx.x, nh * NC - 1), hr = q / NC, cc = q % NC;
-    load_record((const u32x4v*)(a.hrec + ((int64_t)(h0 + hr) * NC + cc) * HX_XCV_WORDS), xv);
   };
   // records past the group's rows land in slots that are not read
   auto stage = [&](int g) __attribute__((always_inline)) {
