@@ -7,18 +7,17 @@
 // reference quantises each activation row to the weight type's vec_dot type
 // (Q8_0 or Q8_K, hx_quant.h) and sums integer products of codes per block.
 //
-// Arithmetic: the activation codes (integers in [-128, 127]) come as f16 pairs
-// in chunk records (hx_quant.h): the tokens' records are written by the router
+// Arithmetic: the activation codes (integers in [-128, 127]) come as int8 in
+// chunk records (hx_quant.h): the tokens' records are written by the router
 // kernel, those of the SwiGLU rows h (stored as f32) by the down kernel itself
-// (one token) or by k_hrec. Each quantised weight is turned into the f16 value
-// 1024 + u, where u is its unsigned code (Q8_0: q + 128; Q4_K: the nibble;
-// Q6_K: the 6-bit code), by writing u under the f16 pattern 0x6400 -- exact,
-// one v_perm or v_and_or per two weights -- and v_dot2_f32_f16 forms the pair
-// products into f32. All of these are integers below 2^24, so the sums are
-// exact: sum((1024 + u) q) - (1024 + bias) sum(q) = sum((u - bias) q), the
-// integer block dot product of the reference. Per chunk the float steps
-// follow: Q8_0 (d_w isum) d_x; Q4_K (d_w d_x) S - (dmin_w d_x) M with S the
-// scaled sums and M the mins times the code sums; Q6_K (d_w d_x) S.
+// (one token) or by k_hrec. Each quantised weight becomes an int8 byte -- Q8_0
+// its code, Q4_K its nibble, Q6_K its 6-bit code (unsigned), assembled four at
+// a time by masks -- and v_dot4_i32_i8 sums four products into an int32, so
+// the block dot products are exact integers, as in the reference:
+// sum((u - bias) q) = sum(u q) - bias sum(q) with the record's code sums. Per
+// chunk the float steps follow: Q8_0 (d_w isum) d_x; Q4_K (d_w d_x) S -
+// (dmin_w d_x) M with S the scaled sums and M the mins times the code sums;
+// Q6_K (d_w d_x) S, S the int32 sum of the scaled sub-block sums.
 #include "hx_internal.h"
 #include "hx_quant.h"
 #include "hx_route_small.h"
@@ -26,17 +25,11 @@
 
 namespace hx {
 
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-
-HX_DEV half2_t as_h2(uint32_t v) { return __builtin_bit_cast(half2_t, v); }
-HX_DEV float dot2(uint32_t w, uint32_t x, float acc) { return __builtin_amdgcn_fdot2(as_h2(w), as_h2(x), acc, false); }
-
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) u32x4v lds_v4;
 
-// 4 bytes b0..b3 (already offset to unsigned) -> f16 pairs (1024+b0, 1024+b2), (1024+b1, 1024+b3)
-HX_DEV uint32_t bytes02(uint32_t q) { return __builtin_amdgcn_perm(q, 0x64646464u, 0x00060004u); }
-HX_DEV uint32_t bytes13(uint32_t q) { return __builtin_amdgcn_perm(q, 0x64646464u, 0x00070005u); }
+// v_dot4_i32_i8: acc + the sum of the four products of the signed bytes of w and x
+HX_DEV int dot4(uint32_t w, uint32_t x, int acc) { return __builtin_amdgcn_sdot4((int)w, (int)x, acc, false); }
 
 // DChunk<FMT>: one lane's chunk of 32 weights of a row and its dot product
 // with the chunk's activation codes. xp: the record's 16 f16 code pairs; xs:
@@ -49,33 +42,29 @@ struct DChunk;
 // Q8_0 planar: chunk = one 32-weight block: 32 int8 + f16 scale
 template <>
 struct DChunk<HX_Q8_0> {
-  static constexpr int NX = 16;  // f16 pairs of activation codes per chunk
-  static constexpr int NS = 1;   // code sums per chunk
+  static constexpr int NX = 8;   // words of activation codes per chunk
+  static constexpr int NS = 1;   // code sums per chunk (unused: the weights are signed)
   using Raw = Chunk<HX_Q8_0>::Raw;
   HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
     Chunk<HX_Q8_0>::load(mat, R, K, row, c, r);
   }
-  // activation positions: elements 32c .. 32c+31; slot g of 8 -> pairs xp[4g ..]
+  // activation positions: elements 32c .. 32c+31; slot g of 8 -> words xp[2g ..]
   HX_DEV static int x_group_off(int c, int g) { return 32 * c + 8 * g; }
-  HX_DEV static void rec_sums(const float (&s)[4], float* xs) { xs[0] = (s[0] + s[1]) + (s[2] + s[3]); }
-  // isum = sum((q + 128 + 1024) x) - 1152 sum(x), exact; then (d_w isum) d_x
-  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs, float dx) {
+  HX_DEV static void rec_sums(const int (&s)[4], int* xs) { xs[0] = (s[0] + s[1]) + (s[2] + s[3]); }
+  // isum = sum(q x) over the block, exact; then (d_w isum) d_x
+  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const int* xs, float dx) {
     const uint32_t q[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
-    float acc = 0.f;
+    int acc = 0;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-      const uint32_t u = q[j] ^ 0x80808080u;  // int8 -> q + 128
-      acc = dot2(bytes02(u), xp[2 * j], acc);
-      acc = dot2(bytes13(u), xp[2 * j + 1], acc);
-    }
-    return (f16_to_f32((uint16_t)r.d) * (acc - 1152.0f * xs[0])) * dx;
+    for (int j = 0; j < 8; j++) acc = dot4(q[j], xp[j], acc);
+    return (f16_to_f32((uint16_t)r.d) * (float)acc) * dx;
   }
 };
 
 // Q4_K (GGUF): chunk = 16 bytes of nibbles: low run (sub-block 2p) and high run (2p+1)
 template <>
 struct DChunk<HX_Q4_K> {
-  static constexpr int NX = 16, NS = 2;
+  static constexpr int NX = 8, NS = 2;
   using Raw = Chunk<HX_Q4_K>::Raw;
   HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
     Chunk<HX_Q4_K>::load(mat, R, K, row, c, r);
@@ -85,28 +74,23 @@ struct DChunk<HX_Q4_K> {
     const int sb = c >> 3, cc = c & 7, p = cc >> 1, h = cc & 1;
     return sb * 256 + 64 * p + 16 * h + 8 * (g & 1) + 32 * (g >> 1);
   }
-  HX_DEV static void rec_sums(const float (&s)[4], float* xs) {
+  HX_DEV static void rec_sums(const int (&s)[4], int* xs) {
     xs[0] = s[0] + s[1];
     xs[1] = s[2] + s[3];
   }
-  // low nibbles (the low run) as 1024 + u, high nibbles masked in place as
-  // 1024 + 16 u (exact in f16: < 2048), so no shift separates them; the 1/16
-  // goes into the high run's scale (exact). Scales and mins of the two runs
-  // without branches (the lanes of a wave hold different sub-blocks).
-  // S = sc0 D0 + sc1 D1 and M = m0 X0 + m1 X1 are exact integers (D the code
-  // dot products, X the code sums of the two runs); the reference's
-  // superblock step is (d d_x) sum S - (dmin d_x) sum M.
-  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs, float dx) {
-    const uint32_t kmagic = vconst<0x64006400u>(), klo = vconst<0x000F000Fu>(), khi = vconst<0x00F000F0u>();
+  // byte i of the chunk: low nibble = low-run element i, high nibble =
+  // high-run element i. Scales and mins of the two runs without branches (the
+  // lanes of a wave hold different sub-blocks). S = sc0 D0 + sc1 D1 and
+  // M = m0 X0 + m1 X1 are exact integers (D the code dot products, X the code
+  // sums of the two runs); the reference's superblock step is
+  // (d d_x) sum S - (dmin d_x) sum M.
+  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const int* xs, float dx) {
     const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
-    float lo = 0.f, hi = 0.f;
+    int lo = 0, hi = 0;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      const uint32_t t = q[j] >> 8;
-      lo = dot2(and_or(q[j], klo, kmagic), xp[2 * j], lo);
-      lo = dot2(and_or(t, klo, kmagic), xp[2 * j + 1], lo);
-      hi = dot2(and_or(q[j], khi, kmagic), xp[8 + 2 * j], hi);
-      hi = dot2(and_or(t, khi, kmagic), xp[8 + 2 * j + 1], hi);
+      lo = dot4(q[j] & 0x0F0F0F0Fu, xp[j], lo);
+      hi = dot4((q[j] >> 4) & 0x0F0F0F0Fu, xp[4 + j], hi);
     }
     const float d = f16_to_f32((uint16_t)(r.hdr.x & 0xffffu)), dmin = f16_to_f32((uint16_t)(r.hdr.x >> 16));
     // sub-blocks 2p, 2p + 1: bytes (2p) & 3, +1 of the 6-bit fields (p < 2), or
@@ -116,18 +100,18 @@ struct DChunk<HX_Q4_K> {
     const uint32_t a0 = r.hdr.y >> sh, a1 = r.hdr.z >> sh, a2 = r.hdr.w >> sh;
     const uint32_t scp = p < 2 ? a0 & 0x3F3Fu : (a2 & 0x0F0Fu) | ((a0 >> 2) & 0x3030u);
     const uint32_t mp = p < 2 ? a1 & 0x3F3Fu : ((a2 >> 4) & 0x0F0Fu) | ((a1 >> 2) & 0x3030u);
-    const float sc0 = (float)(scp & 0xffu), sc1 = (float)((scp >> 8) & 0xffu);
-    const float m0 = (float)(mp & 0xffu), m1 = (float)((mp >> 8) & 0xffu);
-    const float S = sc0 * (lo - 1024.0f * xs[0]) + (sc1 * 0.0625f) * (hi - 1024.0f * xs[1]);
-    const float M = m0 * xs[0] + m1 * xs[1];
-    return (d * dx) * S - (dmin * dx) * M;
+    const int sc0 = (int)(scp & 0xffu), sc1 = (int)((scp >> 8) & 0xffu);
+    const int m0 = (int)(mp & 0xffu), m1 = (int)((mp >> 8) & 0xffu);
+    const int S = sc0 * lo + sc1 * hi;
+    const int M = m0 * xs[0] + m1 * xs[1];
+    return (d * dx) * (float)S - (dmin * dx) * (float)M;
   }
 };
 
 // Q6_K planar: chunk = quarters 0..3 of l = 8a .. 8a+7 in half n of a superblock
 template <>
 struct DChunk<HX_Q6_K> {
-  static constexpr int NX = 16, NS = 4;
+  static constexpr int NX = 8, NS = 4;
   using Raw = Chunk<HX_Q6_K>::Raw;
   HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int c, Raw& r) {
     Chunk<HX_Q6_K>::load(mat, R, K, row, c, r);
@@ -137,65 +121,54 @@ struct DChunk<HX_Q6_K> {
     const int sb = c >> 3, cc = c & 7, n = cc >> 2, a = cc & 3;
     return sb * 256 + 128 * n + 8 * a + 32 * g;
   }
-  HX_DEV static void rec_sums(const float (&s)[4], float* xs) {
+  HX_DEV static void rec_sums(const int (&s)[4], int* xs) {
 #pragma unroll
     for (int q = 0; q < 4; q++) xs[q] = s[q];
   }
-  // quarters 0, 1: code = low nibble | qh bits << 4 as 1024 + code; quarters
-  // 2, 3: high nibble masked in place, qh bits placed above it, as
-  // 1024 + 16 code (exact in f16: < 2048), the 1/16 going into the scale.
-  // One v_and_or_b32 per merge. S = sum of sc (code - 32) . x over the four
-  // quarters, an exact integer; the reference's step is (d d_x) S.
-  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const float* xs, float dx) {
-    const uint32_t kmagic = vconst<0x64006400u>(), klo = vconst<0x000F000Fu>(), khi = vconst<0x00F000F0u>();
-    const uint32_t k30 = vconst<0x00300030u>(), k300 = vconst<0x03000300u>();
+  // the unsigned 6-bit code of quarter q, four elements a byte: its low
+  // nibble (ql of quarters 0 / 1: low nibble, 2 / 3: high nibble) and the two
+  // qh bits of the quarter (bits 2q, 2q + 1) moved to bits 4, 5. Per quarter
+  // the int32 sum of (code - 32) x = D - 32 X; S = sum of sc (D - 32 X) is
+  // the reference's exact integer, and its step (d d_x) S.
+  HX_DEV static float dot(const Raw& r, const uint32_t* xp, const int* xs, float dx) {
     const uint32_t l0[2] = {r.l0.x, r.l0.y}, l1[2] = {r.l1.x, r.l1.y}, hh[2] = {r.h.x, r.h.y};
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    int acc[4] = {0, 0, 0, 0};
 #pragma unroll
     for (int w = 0; w < 2; w++) {
-#pragma unroll
-      for (int par = 0; par < 2; par++) {   // byte pairs (0,2) then (1,3)
-        const int sh = 8 * par;
-        const uint32_t a0 = l0[w] >> sh, a1 = l1[w] >> sh, h = hh[w] >> sh;
-        const uint32_t h4 = h << 4, h2 = h << 2;
-        const uint32_t q0 = and_or(h4, k30, and_or(a0, klo, kmagic));
-        const uint32_t q1 = and_or(h2, k30, and_or(a1, klo, kmagic));
-        const uint32_t q2 = and_or(h4, k300, and_or(a0, khi, kmagic));
-        const uint32_t q3 = and_or(h2, k300, and_or(a1, khi, kmagic));
-        acc[0] = dot2(q0, xp[0 + 2 * w + par], acc[0]);
-        acc[1] = dot2(q1, xp[4 + 2 * w + par], acc[1]);
-        acc[2] = dot2(q2, xp[8 + 2 * w + par], acc[2]);
-        acc[3] = dot2(q3, xp[12 + 2 * w + par], acc[3]);
-      }
+      const uint32_t h = hh[w];
+      const uint32_t q0 = (l0[w] & 0x0F0F0F0Fu) | ((h << 4) & 0x30303030u);
+      const uint32_t q1 = (l1[w] & 0x0F0F0F0Fu) | ((h << 2) & 0x30303030u);
+      const uint32_t q2 = ((l0[w] >> 4) & 0x0F0F0F0Fu) | (h & 0x30303030u);
+      const uint32_t q3 = ((l1[w] >> 4) & 0x0F0F0F0Fu) | ((h >> 2) & 0x30303030u);
+      acc[0] = dot4(q0, xp[0 + w], acc[0]);
+      acc[1] = dot4(q1, xp[2 + w], acc[1]);
+      acc[2] = dot4(q2, xp[4 + w], acc[2]);
+      acc[3] = dot4(q3, xp[6 + w], acc[3]);
     }
-    // sum((code - 32) x) = acc - 1056 sum(x) for quarters 0, 1 and
-    // (acc - 1536 sum(x)) / 16 for quarters 2, 3
-    float s = 0.f;
+    int S = 0;
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      const float sc = (float)(int8_t)((r.sc >> (8 * q)) & 0xffu);
-      s = q < 2 ? __builtin_fmaf(sc, acc[q] - 1056.0f * xs[q], s) : __builtin_fmaf(sc * 0.0625f, acc[q] - 1536.0f * xs[q], s);
-    }
-    return (f16_to_f32((uint16_t)r.d) * dx) * s;
+    for (int q = 0; q < 4; q++) S += (int)(int8_t)((r.sc >> (8 * q)) & 0xffu) * (acc[q] - 32 * xs[q]);
+    return (f16_to_f32((uint16_t)r.d) * dx) * (float)S;
   }
 };
 
-// one chunk record (5 x 16 bytes, hx_quant.h) -> the dot's code pairs, sums and d
+// one chunk record (HX_REC_VECS x 16 bytes, hx_quant.h) -> the dot's code
+// words, sums and d
 template <class D>
-HX_DEV void unpack_record(const u32x4v (&v)[5], uint32_t* xp, float* xs, float& dx) {
+HX_DEV void unpack_record(const u32x4v (&v)[HX_REC_VECS], uint32_t* xp, int* xs, float& dx) {
 #pragma unroll
-  for (int g = 0; g < 4; g++) {
+  for (int g = 0; g < 2; g++) {
     xp[4 * g] = v[g][0]; xp[4 * g + 1] = v[g][1]; xp[4 * g + 2] = v[g][2]; xp[4 * g + 3] = v[g][3];
   }
-  const uint32_t t[4] = {v[4][0], v[4][1], v[4][2], v[4][3]};
-  float s[4];
+  const uint32_t t[4] = {v[2][0], v[2][1], v[2][2], v[2][3]};
+  int s[4];
   record_tail(t, s, dx);
   D::rec_sums(s, xs);
 }
 template <class P>
-HX_DEV void load_record(P src, u32x4v (&v)[5]) {
+HX_DEV void load_record(P src, u32x4v (&v)[HX_REC_VECS]) {
 #pragma unroll
-  for (int g = 0; g < 5; g++) v[g] = src[g];
+  for (int g = 0; g < HX_REC_VECS; g++) v[g] = src[g];
 }
 
 // the decode plan, pulled into LDS by the whole workgroup in one pass
@@ -223,7 +196,7 @@ HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U
   }
   // token j's record is loaded before token j - 1's dot products (token 0's
   // together with the weights), so each load overlaps work
-  u32x4v xr[5];
+  u32x4v xr[HX_REC_VECS];
   auto xload = [&](int t) __attribute__((always_inline)) {
     load_record((const u32x4v*)(a.xcv + ((int64_t)t * (K / 32) + c) * HX_XCV_WORDS), xr);
   };
@@ -231,7 +204,8 @@ HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U
   __builtin_amdgcn_sched_barrier(0);   // no weight arithmetic above these loads
   for (int j = 0; j < count; j++) {
     uint32_t xp[D::NX];
-    float xs[D::NS], dx;
+    int xs[D::NS];
+    float dx;
     unpack_record<D>(xr, xp, xs, dx);
     if (j + 1 < count) xload(tok[j + 1]);
 #pragma unroll
@@ -425,7 +399,7 @@ __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a
   float lv[EPL];
   route_logits_load<EPL>(r.logits, r.E, lv);
   const float sg = r.has_shared ? r.logits[r.E] : 0.f;
-  u32x4v xr[5];
+  u32x4v xr[HX_REC_VECS];
   load_record((const u32x4v*)(a.xcv + (int64_t)lane * HX_XCV_WORDS), xr);
   const bool shrow = a.Is > 0 && row < a.Is, rrow = row < a.I;
   // loads are unconditional (out-of-range rows read row 0 and are dropped at
@@ -464,7 +438,8 @@ __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a
   if (blockIdx.x == 0 && wave == 0)
     publish_one_token(r.d, r.topk_w, r.sgw, my_e, my_w, pos, r.has_shared ? sigmoidf_(sg) : 0.0f);
   uint32_t xp[D::NX];
-  float xs[D::NS], dx;
+  int xs[D::NS];
+  float dx;
   unpack_record<D>(xr, xp, xs, dx);
   float v[16];
 #pragma unroll
@@ -644,11 +619,12 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
     const int K = sexp[hr] == a.E ? a.Is : a.I;
     float p = 0.f;
     if (c < K / 32) {
-      u32x4v v[5];
+      u32x4v v[HX_REC_VECS];
       if constexpr (QH) load_record((const lds_v4*)(srec + (hr * LPR + c) * HX_XCV_WORDS), v);
       else load_record((const u32x4v*)(a.hrec + ((int64_t)(h0 + hr) * LPR + c) * HX_XCV_WORDS), v);
       uint32_t xp[D::NX];
-      float xs[D::NS], dx;
+      int xs[D::NS];
+    float dx;
       unpack_record<D>(v, xp, xs, dx);
       p = D::dot(raw[s], xp, xs, dx);
     }
@@ -769,7 +745,8 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe(ExpertArgs a) {
         u32x4v v[REC];
         load_record(xb + (hr * NC + c) * REC, v);
         uint32_t xp[D::NX];
-        float xs[D::NS], dx;
+        int xs[D::NS];
+    float dx;
         unpack_record<D>(v, xp, xs, dx);
         p = D::dot(raw[s], xp, xs, dx);
       }

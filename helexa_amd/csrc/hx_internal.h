@@ -195,7 +195,7 @@ struct ExpertArgs {
 
 // words of a chunk record (hx_quant.h); rows of h one decode down workgroup
 // takes (4 waves x 6 rows each)
-constexpr int HX_XCV_WORDS = 20;
+constexpr int HX_XCV_WORDS = 12;
 constexpr int HX_DOWN_ROWS = 24;
 __host__ __device__ inline int down_groups(int F, int T) { return (F + T + HX_DOWN_ROWS - 1) / HX_DOWN_ROWS; }
 

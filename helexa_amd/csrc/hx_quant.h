@@ -16,16 +16,14 @@
 //
 // Chunk records. The decode GEMV kernels give each lane chunks of 32 weights
 // of a row (Chunk<FMT>::pos) and need the 32 matching activation codes as the
-// f16 pairs their v_dot2_f32_f16 products take. A record holds one chunk:
-//   words 0..15  the codes as f16 pairs, slot s (elements x_group_off(c, s) ..
-//                + 7, see hx_decode.hip) in words 4 s .. 4 s + 3, paired
-//                (e0, e2) (e1, e3) (e4, e6) (e5, e7); codes are integers in
-//                [-128, 127], exact in f16, so the dot products of the codes
-//                are exact integer sums in f32;
-//   words 16, 17 the sums of the eight codes of slots 0, 1 | 2, 3 as f16
-//                (|sum| <= 1024: exact);
-//   word 18      the block's d (f32; Q8_0: its f16 value);
-//   word 19      0.
+// int8 bytes their v_dot4_i32_i8 products take. A record holds one chunk:
+//   words 0..7   the codes as int8, slot s (elements x_group_off(c, s) .. + 7,
+//                see hx_decode.hip) in words 2 s, 2 s + 1, in element order;
+//                every product sum of codes and weights is an exact int32;
+//   words 8, 9   the sums of the eight codes of slots 0, 1 | 2, 3 as int16
+//                (|sum| <= 1024);
+//   word 10      the block's d (f32; Q8_0: its f16 value);
+//   word 11      0.
 // Every chunk lies inside one quantisation block (Q8_0: the chunk is the
 // block; Q8_K: chunk c is in superblock c / 8).
 //
@@ -38,7 +36,9 @@
 
 namespace hx {
 
-constexpr int HX_REC_SUMS = 16, HX_REC_D = 18;
+constexpr int HX_REC_SUMS = 8, HX_REC_D = 10;
+constexpr int HX_REC_VECS = HX_XCV_WORDS / 4;   // 16-byte words per record
+static_assert(HX_XCV_WORDS == 12, "record layout: 8 code words, 2 sum words, d, 0");
 
 // round half away from zero, for |y| <= 130: trunc(y + copysign(pred(0.5), y))
 // equals roundf(y) on every f32 in that range (checked exhaustively); the
@@ -139,7 +139,12 @@ HX_DEV void quant_group(const float (&x)[8], float (&q)[8], float& d) {
   }
 }
 
-HX_DEV uint32_t pk_f16(float a, float b) { return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b)); }
+// four codes (exact integers in [-128, 127], as floats) -> one word of int8
+HX_DEV uint32_t pk_i8(float a, float b, float c, float d) {
+  const uint32_t lo = ((uint32_t)(int)a & 0xffu) | (((uint32_t)(int)b & 0xffu) << 8);
+  const uint32_t hi = ((uint32_t)(int)c & 0xffu) | ((uint32_t)(int)d << 8);
+  return lo | (hi << 16);
+}
 
 // quantise group g (this lane's 8 values) and write its part of the record of
 // its chunk into rec (the row's records, HX_XCV_WORDS words each)
@@ -150,22 +155,18 @@ HX_DEV void group_to_record(const float (&x)[8], int g, uint32_t* rec) {
   int c, s;
   group_slot<FMT>(g, c, s);
   uint32_t* r = rec + (int64_t)c * HX_XCV_WORDS;
-  *(uint4*)(r + 4 * s) = make_uint4(pk_f16(q[0], q[2]), pk_f16(q[1], q[3]), pk_f16(q[4], q[6]), pk_f16(q[5], q[7]));
+  *(uint2*)(r + 2 * s) = make_uint2(pk_i8(q[0], q[1], q[2], q[3]), pk_i8(q[4], q[5], q[6], q[7]));
   const float sum = ((q[0] + q[1]) + (q[2] + q[3])) + ((q[4] + q[5]) + (q[6] + q[7]));   // exact integers
-  ((_Float16*)(r + HX_REC_SUMS))[s] = (_Float16)sum;
+  ((int16_t*)(r + HX_REC_SUMS))[s] = (int16_t)(int)sum;
   if (s == 0) *(uint2*)(r + HX_REC_D) = make_uint2(__float_as_uint(d), 0u);
 }
 
 // the four slot sums and d of a record's last four words
-HX_DEV void record_tail(const uint32_t (&w)[4], float (&s)[4], float& d) {
-  const _Float16 a = __builtin_bit_cast(_Float16, (uint16_t)(w[0] & 0xffffu));
-  const _Float16 b = __builtin_bit_cast(_Float16, (uint16_t)(w[0] >> 16));
-  const _Float16 c = __builtin_bit_cast(_Float16, (uint16_t)(w[1] & 0xffffu));
-  const _Float16 e = __builtin_bit_cast(_Float16, (uint16_t)(w[1] >> 16));
-  s[0] = (float)a;
-  s[1] = (float)b;
-  s[2] = (float)c;
-  s[3] = (float)e;
+HX_DEV void record_tail(const uint32_t (&w)[4], int (&s)[4], float& d) {
+  s[0] = (int)(int16_t)(w[0] & 0xffffu);
+  s[1] = (int)w[0] >> 16;
+  s[2] = (int)(int16_t)(w[1] & 0xffffu);
+  s[3] = (int)w[1] >> 16;
   d = __uint_as_float(w[2]);
 }
 
