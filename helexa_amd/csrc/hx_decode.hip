@@ -537,26 +537,20 @@ __global__ __launch_bounds__(256) void k_hrec(ExpertArgs a, int nrows) {
 // contribution w * (row . h) goes to LDS, and each token's output is the sum
 // of its rows in row order (slots by ascending expert, then the shared
 // expert), as the reference's combine order; with several groups, the group's
-// partial sum, which k_down_reduce adds up in group order.
-// QH (one token, every row of h in one group): the workgroup quantises the
-// rows of h into chunk records in LDS itself; wave w takes rows w, w + NW, ...
-// whose loads it issues first of all (they need no plan), so that the memory
-// counters let the quantisation start once they have arrived, while the
-// weight loads issued after them are still in flight. Otherwise the records
-// come from k_hrec and each wave loads those of a row from memory right
+// partial sum, which k_down_reduce adds up in group order. The chunk records
+// of the rows of h come from k_hrec; each wave loads those of a row right
 // before its dot product.
 // ----------------------------------------------------------------------------
-template <int FMT, int LPR, int SPW, int NW, bool QH>
+template <int FMT, int LPR, int SPW, int NW>
 __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
   using D = DChunk<FMT>;
-  constexpr int RG = 64 / LPR, NG = LPR / 16;   // K = 32 LPR: groups of 8 per lane of a row
+  constexpr int RG = 64 / LPR;
   constexpr int ROWS = NW * SPW;   // rows of h per group (one pass per wave)
   static_assert(ROWS <= HX_DOWN_ROWS, "groups of at most HX_DOWN_ROWS rows of h");
-  // LDS: (QH) the group's chunk records [ROWS][LPR]; then per row its token,
-  // weight and expert; then the contributions [ROWS][RG]
+  // LDS: per row of h its token, weight and expert; then the contributions
+  // [ROWS][RG]
   extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
-  uint32_t* srec = (uint32_t*)xl;
-  int* stok = (int*)(srec + (QH ? ROWS * LPR * HX_XCV_WORDS : 0));
+  int* stok = (int*)xl;
   float* swt = (float*)(stok + ROWS);
   int* sexp = (int*)(swt + ROWS);
   float* contrib = (float*)(sexp + ROWS);
@@ -564,13 +558,6 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
   const int nh_all = a.F + (a.Is > 0 ? T : 0);   // rows of h in use
   const int h0 = blockIdx.y * ROWS;              // this workgroup's group of rows
   const int nh = min(nh_all - h0, ROWS);
-  float hx[QH ? SPW : 1][QH ? NG : 1][8];
-  if constexpr (QH) {
-    const int w = threadIdx.x >> 6;
-#pragma unroll
-    for (int s = 0; s < SPW; s++)   // rows past the group's end read its first row (not quantised)
-      h_row_load<NG>(a.hbuf + (int64_t)(h0 + (w + NW * s < nh ? w + NW * s : 0)) * a.hstride, hx[s]);
-  }
   {
     // thread 32 part + r < 96 loads row r's token (part 0), weight (1) or
     // expert (2); one load each, clamped to a valid row, so one round trip.
@@ -602,13 +589,6 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
     const int cc = c < K / 32 ? c : 0;
     D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row < a.H ? row : 0, cc, raw[s]);
   }
-  if constexpr (QH) {
-    __builtin_amdgcn_sched_barrier(0);   // the weight loads go out first
-#pragma unroll
-    for (int s = 0; s < SPW; s++)
-      if (wave + NW * s < nh) h_regs_records<FMT, NG>(hx[s], srec + (wave + NW * s) * LPR * HX_XCV_WORDS);
-    __syncthreads();
-  }
 #pragma unroll
   for (int s = 0; s < SPW; s++) {
     const int hr = wave + NW * s;
@@ -620,8 +600,7 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
     float p = 0.f;
     if (c < K / 32) {
       u32x4v v[HX_REC_VECS];
-      if constexpr (QH) load_record((const lds_v4*)(srec + (hr * LPR + c) * HX_XCV_WORDS), v);
-      else load_record((const u32x4v*)(a.hrec + ((int64_t)(h0 + hr) * LPR + c) * HX_XCV_WORDS), v);
+      load_record((const u32x4v*)(a.hrec + ((int64_t)(h0 + hr) * LPR + c) * HX_XCV_WORDS), v);
       uint32_t xp[D::NX];
       int xs[D::NS];
     float dx;
@@ -652,6 +631,107 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
 }
 
 // ----------------------------------------------------------------------------
+// down + combine for one token with at most 12 rows of h (k <= 11): OG groups
+// of four waves per workgroup, group o owning output rows RG o .. + RG - 1 of
+// the workgroup's RG OG; wave q of a group takes rows of h q, q + 4, q + 8.
+// The workgroup quantises each row of h once into chunk records in LDS (wave
+// w rows w, w + 4 OG), whose loads it issues first of all (they need no plan)
+// so the quantisation can start once they have arrived while the weight loads
+// issued after them are still in flight; more output rows per workgroup read
+// and quantise the rows of h fewer times over the grid. Each output is the sum
+// of its rows' contributions in row order (slots by ascending expert, then the
+// shared expert), as the reference's combine order.
+// ----------------------------------------------------------------------------
+template <int FMT, int LPR, int OG>
+__global__ __launch_bounds__(256 * OG) void k_down_one(ExpertArgs a) {
+  using D = DChunk<FMT>;
+  constexpr int RG = 64 / LPR, NG = LPR / 16;   // K = 32 LPR: groups of 8 per lane of a row
+  constexpr int NW = 4 * OG, ROWS = 12, SPW = 3, QS = (ROWS + NW - 1) / NW;
+  constexpr int NO = RG * OG;   // output rows of the workgroup
+  // LDS: chunk records [ROWS][LPR]; per row its token, weight and expert; the
+  // contributions [ROWS][NO]
+  extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
+  uint32_t* srec = (uint32_t*)xl;
+  int* stok = (int*)(srec + ROWS * LPR * HX_XCV_WORDS);
+  float* swt = (float*)(stok + ROWS);
+  int* sexp = (int*)(swt + ROWS);
+  float* contrib = (float*)(sexp + ROWS);
+  const int NH = a.F + 1;
+  const int nh = a.F + (a.Is > 0 ? 1 : 0);   // rows of h in use (<= ROWS)
+  const int w = threadIdx.x >> 6;
+  float hx[QS][NG][8];
+#pragma unroll
+  for (int s = 0; s < QS; s++)   // rows past the end read row 0 (not quantised)
+    h_row_load<NG>(a.hbuf + (int64_t)(w + NW * s < nh ? w + NW * s : 0) * a.hstride, hx[s]);
+  {
+    // thread 32 part + r < 96 loads row r's token (part 0), weight (1) or
+    // expert (2); rows r in [nh, ROWS) get token -1 (no token's row)
+    const int tok0 = 4 + 4 * a.max_slots;
+    const int i = threadIdx.x, part = i >> 5, r = i & 31;
+    if (i < 96) {
+      const int v = a.plan[tok0 + part * NH + min(r, nh - 1)];
+      int* dst = part == 0 ? stok : part == 1 ? (int*)swt : sexp;
+      if (r < nh) dst[r] = v;
+      else if (part == 0 && r < ROWS) dst[r] = -1;
+    }
+  }
+  __syncthreads();
+  const int lane = lane_id(), og = w >> 2, wq = w & 3, rg = lane / LPR, c = lane % LPR;
+  const int row = (blockIdx.x * OG + og) * RG + rg;
+  // every weight load of the wave, unconditional (rows past the end, and
+  // chunks past a shorter shared expert's K, read valid data that is dropped)
+  typename D::Raw raw[SPW];
+#pragma unroll
+  for (int s = 0; s < SPW; s++) {
+    const int hr = wq + 4 * s, hq = hr < nh ? hr : 0;
+    const int e = sexp[hq];
+    const bool sh = e == a.E;
+    const int K = sh ? a.Is : a.I;
+    D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row < a.H ? row : 0, c < K / 32 ? c : 0, raw[s]);
+  }
+  __builtin_amdgcn_sched_barrier(0);   // the weight loads go out before the quantisation
+#pragma unroll
+  for (int s = 0; s < QS; s++)
+    if (w + NW * s < nh) h_regs_records<FMT, NG>(hx[s], srec + (w + NW * s) * LPR * HX_XCV_WORDS);
+  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < SPW; s++) {
+    const int hr = wq + 4 * s;
+    if (hr >= nh) {   // every contribution slot is defined (zero past the rows of h)
+      if (c == 0) contrib[hr * NO + og * RG + rg] = 0.f;
+      continue;
+    }
+    const int K = sexp[hr] == a.E ? a.Is : a.I;
+    float p = 0.f;
+    if (c < K / 32) {
+      u32x4v v[HX_REC_VECS];
+      load_record((const lds_v4*)(srec + (hr * LPR + c) * HX_XCV_WORDS), v);
+      uint32_t xp[D::NX];
+      int xs[D::NS];
+      float dx;
+      unpack_record<D>(v, xp, xs, dx);
+      p = D::dot(raw[s], xp, xs, dx);
+    }
+    p = wave_sum<LPR>(p);
+    if (c == 0) contrib[hr * NO + og * RG + rg] = swt[hr] * p;
+  }
+  __syncthreads();
+  const int i = threadIdx.x;
+  const int n = blockIdx.x * NO + i;
+  if (i < NO && n < a.H) {
+    float y = 0.f;
+#pragma unroll
+    for (int hr = 0; hr < ROWS; hr++) y += contrib[hr * NO + i] * (stok[hr] == 0 ? 1.f : 0.f);
+    if (a.resid) {
+      uint16_t* px = a.resid + n;
+      *px = f32_to_bf16(bf16_to_f32(*px) + bf16_to_f32(f32_to_bf16(y)));
+    } else {
+      ((uint16_t*)a.y)[n] = f32_to_bf16(y);
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
 // down + combine for T > 1 and K = 512, pipelined: workgroup = RG output rows
 // over every row of h, taken in groups of 24 (24 / NW per wave; NW = 8 keeps
 // the registers under 128, so 4 waves share each SIMD). The weights of
@@ -662,6 +742,9 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
 // the shared expert), written directly, with no partial sums to reduce.
 // ----------------------------------------------------------------------------
 constexpr int DP_K = 512;
+// output groups of four waves per workgroup of k_down_one (measured on MI355X,
+// paired: 2 against 1 saves 1.1 us a layer at C2 and 1.3 at C4 B = 1; 4 less)
+constexpr int HX_DOWN_ONE_OG = 2;
 template <int FMT, int LPR, int NW>
 __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe(ExpertArgs a) {
   using D = DChunk<FMT>;
@@ -889,13 +972,13 @@ static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
   }
 #define DD(LPR)                                                                                       \
   {                                                                                                   \
-    constexpr int RG = 64 / LPR;                                                                      \
+    constexpr int RG = 64 / LPR, OG = HX_DOWN_ONE_OG;                                                 \
     if (qh) {                                                                                         \
-      const size_t lds = (size_t)12 * LPR * HX_XCV_WORDS * 4 + (size_t)12 * (3 + RG) * 4;             \
-      hx_launch(k_down_dec<FMT, LPR, 3, 4, true>, dim3((a.H + RG - 1) / RG, 1), dim3(256), (uint32_t)lds, s, a); \
+      const size_t lds = (size_t)12 * LPR * HX_XCV_WORDS * 4 + (size_t)12 * (3 + RG * OG) * 4;        \
+      hx_launch(k_down_one<FMT, LPR, OG>, dim3((a.H + RG * OG - 1) / (RG * OG)), dim3(256 * OG), (uint32_t)lds, s, a); \
     } else {                                                                                          \
       const size_t lds = (size_t)HX_DOWN_ROWS * (3 + RG) * 4;                                         \
-      hipLaunchKernelGGL((k_down_dec<FMT, LPR, 6, 4, false>), dim3((a.H + RG - 1) / RG, groups), dim3(256), lds, s, a); \
+      hipLaunchKernelGGL((k_down_dec<FMT, LPR, 6, 4>), dim3((a.H + RG - 1) / RG, groups), dim3(256), lds, s, a); \
     }                                                                                                 \
   }
   if (nch == 64) DD(64) else if (nch == 32) DD(32) else DD(16)

@@ -636,8 +636,10 @@ static int forward_impl(hx_moe* m, const void* x, int64_t T, void* y, void* ws, 
   const bool bf = m->cfg.act_dtype == HX_BF16;
   const int H = m->cfg.hidden_size;
   uint16_t* xn = (uint16_t*)((uint8_t*)ws + L.xn);
-  if (fz && fast && T == 1 && H <= 8 * 256) {
-    // RMSNorm inside the router kernel, residual inside the down kernel
+  if (fz && fast && H <= 8 * 256) {
+    // RMSNorm inside the router kernel (the router waves and the token-record
+    // waves normalise each token with the same arithmetic, so both see the
+    // same bits), residual inside the down kernel
     p.ra.norm_w = fz->norm_w;
     p.ra.eps = fz->eps;
     p.ra.xn_out = xn;
