@@ -255,7 +255,10 @@ __global__ __launch_bounds__(256) void k_router_dec(RouterArgs r, ExpertArgs a, 
   const int wave = threadIdx.x >> 6;
   if ((int)blockIdx.x < nrb) {
     constexpr int RTE = TT > 4 ? 2 : 1;   // router rows per wave
-    router_rows<true, RBF, TT, RTE>(r, (blockIdx.x * 4 + wave) * RTE, 0);
+    if (TT > 1 && r.norm_w && (r.H & 7) == 0 && r.H <= 8 * 256)   // at most 4 groups of 8 a lane
+      router_rows_norm<RBF, TT, RTE, 4>(r, (blockIdx.x * 4 + wave) * RTE);
+    else
+      router_rows<true, RBF, TT, RTE>(r, (blockIdx.x * 4 + wave) * RTE, 0);
     return;
   }
   const int t = 4 * ((int)blockIdx.x - nrb) + wave;

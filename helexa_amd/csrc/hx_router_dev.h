@@ -46,7 +46,8 @@ HX_DEV void load8(const void* base, int64_t row_elems, int64_t row, int h0, int 
 // router does the same arithmetic, so all hold the same rows; wave 0 of
 // workgroup 0 writes them to xn_out.
 template <int TT, int NG>
-HX_DEV void rmsnorm_regs(const RouterArgs& a, uint32_t (&xr)[TT][NG][4], int t0) {
+HX_DEV void rmsnorm_regs(const RouterArgs& a, uint32_t (&xr)[TT][NG][4], int t0,
+                         bool writer = blockIdx.x == 0 && threadIdx.x < 64) {
   const int lane = lane_id(), H = a.H, G = H / 8;
   float w[NG][8];
 #pragma unroll
@@ -56,27 +57,35 @@ HX_DEV void rmsnorm_regs(const RouterArgs& a, uint32_t (&xr)[TT][NG][4], int t0)
     w[i][0] = w0.x; w[i][1] = w0.y; w[i][2] = w0.z; w[i][3] = w0.w;
     w[i][4] = w1.x; w[i][5] = w1.y; w[i][6] = w1.z; w[i][7] = w1.w;
   }
-  const bool writer = blockIdx.x == 0 && threadIdx.x < 64;
+  // the tokens' sums of squares, their wave reductions and scales in three
+  // passes, so the TT dependent chains run side by side; per token the same
+  // operations in the same order as for one token
+  float ss[TT], inv[TT];
 #pragma unroll
   for (int t = 0; t < TT; t++) {
-    float ss = 0.f;
+    ss[t] = 0.f;
 #pragma unroll
     for (int i = 0; i < NG; i++) {
       if (lane + 64 * i >= G) break;
 #pragma unroll
       for (int q = 0; q < 8; q++) {
         const float v = __uint_as_float(q & 1 ? xr[t][i][q / 2] & 0xffff0000u : xr[t][i][q / 2] << 16);
-        ss = __builtin_fmaf(v, v, ss);
+        ss[t] = __builtin_fmaf(v, v, ss[t]);
       }
     }
-    ss = wave_sum<64>(ss);
-    const float inv = 1.0f / sqrtf(ss / (float)H + a.eps);
+  }
+#pragma unroll
+  for (int t = 0; t < TT; t++) ss[t] = wave_sum<64>(ss[t]);
+#pragma unroll
+  for (int t = 0; t < TT; t++) inv[t] = 1.0f / sqrtf(ss[t] / (float)H + a.eps);
+#pragma unroll
+  for (int t = 0; t < TT; t++) {
 #pragma unroll
     for (int i = 0; i < NG; i++) {
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const float lo = __uint_as_float(xr[t][i][q] << 16) * inv * (1.0f + w[i][2 * q]);
-        const float hi = __uint_as_float(xr[t][i][q] & 0xffff0000u) * inv * (1.0f + w[i][2 * q + 1]);
+        const float lo = __uint_as_float(xr[t][i][q] << 16) * inv[t] * (1.0f + w[i][2 * q]);
+        const float hi = __uint_as_float(xr[t][i][q] & 0xffff0000u) * inv[t] * (1.0f + w[i][2 * q + 1]);
         xr[t][i][q] = (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
       }
       if (writer && t0 + t < a.T && lane + 64 * i < G)
@@ -157,6 +166,97 @@ HX_DEV void router_rows_u(const RouterArgs& a, int e0, int t0) {
         if (XBF) v = bf16_to_f32(f32_to_bf16(v));
         if (a.bias && e < a.E) v = v + a.bias[e];
         a.logits[(int64_t)tt * a.E1 + e] = v;
+      }
+    }
+}
+
+// router_rows_u for bf16 tokens with the decoder RMSNorm and TT > 1, all four
+// waves of the workgroup taking part: wave w normalises tokens w, w + 4, ..
+// (the arithmetic of rmsnorm_regs for one token, so the bits the record waves
+// compute) into LDS, and after one barrier every wave reads the TT normalised
+// rows from there for its router rows. Each token is normalised once per
+// workgroup instead of once per wave (the waves run one per SIMD, so the
+// repeated normalisation was serial VALU work on the kernel's critical path).
+// Same multiply-add order per logit as router_rows_u.
+template <bool RBF, int TT, int TE, int NG>
+HX_DEV void router_rows_norm(const RouterArgs& a, int e0) {
+  constexpr int RW = RBF ? 4 : 8, TW = (TT + 3) / 4;
+  __shared__ uint4 sxn[TT][NG][64];   // normalised rows, canonical layout
+  const int lane = lane_id(), wave = threadIdx.x >> 6;
+  const int H = a.H, G = H / 8;
+  uint32_t wr[TE][NG][RW], xr[TW][NG][4];
+#pragma unroll
+  for (int i = 0; i < NG; i++) {
+    const int g = min(lane + 64 * i, G - 1);
+#pragma unroll
+    for (int j = 0; j < TE; j++) {
+      const int64_t row = min(e0 + j, a.E1 - 1);
+      const uint4* p = (const uint4*)((const uint8_t*)a.R + (row * H + 8 * g) * (RBF ? 2 : 4));
+#pragma unroll
+      for (int q = 0; q < RW / 4; q++) {
+        const uint4 v = p[q];
+        wr[j][i][4 * q] = v.x; wr[j][i][4 * q + 1] = v.y; wr[j][i][4 * q + 2] = v.z; wr[j][i][4 * q + 3] = v.w;
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < TW; s++) {
+      const int64_t tok = min(wave + 4 * s, a.T - 1);
+      const uint4 v = *(const uint4*)((const uint16_t*)a.x + tok * H + 8 * g);
+      xr[s][i][0] = v.x; xr[s][i][1] = v.y; xr[s][i][2] = v.z; xr[s][i][3] = v.w;
+    }
+  }
+#pragma unroll
+  for (int s = 0; s < TW; s++) {
+    const int t = wave + 4 * s;
+    if (t >= TT) continue;   // wave-uniform
+    uint32_t one[1][NG][4];
+#pragma unroll
+    for (int i = 0; i < NG; i++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) one[0][i][q] = xr[s][i][q];
+    rmsnorm_regs<1, NG>(a, one, t, blockIdx.x == 0 && t < a.T);
+#pragma unroll
+    for (int i = 0; i < NG; i++) sxn[t][i][lane] = make_uint4(one[0][i][0], one[0][i][1], one[0][i][2], one[0][i][3]);
+  }
+  __syncthreads();
+  float acc[TT][TE];
+#pragma unroll
+  for (int t = 0; t < TT; t++)
+#pragma unroll
+    for (int j = 0; j < TE; j++) acc[t][j] = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NG; i++) {
+    if (lane + 64 * i >= G) break;   // this lane's remaining groups are past the end
+    uint32_t xg[TT][4];
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+      const uint4 v = sxn[t][i][lane];
+      xg[t][0] = v.x; xg[t][1] = v.y; xg[t][2] = v.z; xg[t][3] = v.w;
+    }
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+#pragma unroll
+      for (int t = 0; t < TT; t++) {
+        const float xv = __uint_as_float(q & 1 ? xg[t][q / 2] & 0xffff0000u : xg[t][q / 2] << 16);
+#pragma unroll
+        for (int j = 0; j < TE; j++) {
+          const float wv = RBF ? __uint_as_float(q & 1 ? wr[j][i][q / 2] & 0xffff0000u : wr[j][i][q / 2] << 16)
+                               : __uint_as_float(wr[j][i][q]);
+          acc[t][j] = __builtin_fmaf(xv, wv, acc[t][j]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < TT; t++)
+#pragma unroll
+    for (int j = 0; j < TE; j++) {
+      float v = wave_sum<64>(acc[t][j]);
+      const int e = e0 + j;
+      if (lane == t * TE + j && t < a.T && e < a.E1) {
+        v = bf16_to_f32(f32_to_bf16(v));
+        if (a.bias && e < a.E) v = v + a.bias[e];
+        a.logits[(int64_t)t * a.E1 + e] = v;
       }
     }
 }
