@@ -871,6 +871,132 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe(ExpertArgs a) {
   }
 }
 
+// ----------------------------------------------------------------------------
+// down + combine for T > 1, K = 512 and at most DP3_ROWS rows of h: like
+// k_down_pipe, but every chunk record of the rows of h is moved into LDS once
+// in the prologue (with the plan), so the loop over groups of 24 rows streams
+// only weights, three register buffers deep: group g + 2's weights are issued
+// before group g's dot products, and the loop has no barrier. (k_down_pipe
+// stages each group's records through registers; the memory counter retires
+// loads in issue order, so a record load issued behind a deeper weight
+// prefetch would wait for it.)
+// ----------------------------------------------------------------------------
+constexpr int DP3_ROWS = 96;
+template <int FMT, int LPR, int NW>
+__global__ __launch_bounds__(64 * NW, 4) void k_down_pipe3(ExpertArgs a) {
+  using D = DChunk<FMT>;
+  using Raw = typename D::Raw;
+  constexpr int ROWS = 24, SPW = ROWS / NW, RG = 64 / LPR, NC = DP_K / 32, REC = HX_REC_VECS;
+  static_assert(SPW * NW == ROWS, "the waves split a group's rows of h evenly");
+  constexpr int MAXR = (DP3_ROWS * NC * REC + 64 * NW - 1) / (64 * NW);   // 16-byte record pieces a thread moves
+  // LDS: the records of every row of h [nh_all][NC], then per row its token,
+  // weight and expert, then the contributions [rows of h][RG]
+  extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
+  const int T = a.T, NH = a.F + T;
+  const int nh_all = a.F + (a.Is > 0 ? T : 0);
+  const int ng = (nh_all + ROWS - 1) / ROWS;
+  lds_v4* const rec = (lds_v4*)xl;
+  int* stok = (int*)((uint8_t*)xl + (size_t)nh_all * NC * HX_XCV_WORDS * 4);
+  float* swt = (float*)(stok + nh_all);
+  int* sexp = (int*)(swt + nh_all);
+  float* contrib = (float*)(sexp + nh_all);
+  const int tid = threadIdx.x;
+  u32x4v rv[MAXR];
+  {
+    // the plan's tokens, weights and experts of all rows (PL loads a thread),
+    // then the records (MAXR 16-byte pieces a thread), all issued before any
+    // is stored; the plan's loads first, so storing them waits for them alone
+    constexpr int PL = (3 * DP3_ROWS + 64 * NW - 1) / (64 * NW);
+    const int tok0 = 4 + 4 * a.max_slots, n3 = 3 * nh_all, n16 = nh_all * NC * REC;
+    int v[PL];
+#pragma unroll
+    for (int b = 0; b < PL; b++) {
+      const int i = min(b * 64 * NW + tid, n3 - 1), part = i / nh_all, r = i - part * nh_all;
+      v[b] = a.plan[tok0 + part * NH + r];
+    }
+#pragma unroll
+    for (int b = 0; b < MAXR; b++) rv[b] = ((const u32x4v*)a.hrec)[min(b * 64 * NW + tid, n16 - 1)];
+#pragma unroll
+    for (int b = 0; b < PL; b++) {
+      const int i = b * 64 * NW + tid, part = i / nh_all, r = i - part * nh_all;
+      if (i < n3) (part == 0 ? stok : part == 1 ? (int*)swt : sexp)[r] = v[b];
+    }
+  }
+  __syncthreads();
+  const int lane = lane_id(), wave = tid >> 6, rg = lane / LPR, c = lane % LPR;
+  const int n0 = blockIdx.x * RG, row = n0 + rg;
+  Raw ra[SPW], rb[SPW], rc[SPW];
+  // the wave's SPW weight rows of group g (rows past the end read row 0 of
+  // the group, dropped later)
+  auto issue = [&](int g, Raw(&raw)[SPW]) __attribute__((always_inline)) {
+    const int h0 = g * ROWS, nh = min(nh_all - h0, ROWS);
+#pragma unroll
+    for (int s = 0; s < SPW; s++) {
+      const int hr = wave + NW * s, hq = hr < nh ? hr : 0;
+      const int e = sexp[h0 + hq];
+      const bool sh = e == a.E;
+      const int K = sh ? a.Is : a.I;
+      D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row < a.H ? row : 0, c < K / 32 ? c : 0, raw[s]);
+    }
+  };
+  issue(0, ra);
+  if (ng > 1) issue(1, rb);
+  {
+    const int n16 = nh_all * NC * REC;
+#pragma unroll
+    for (int b = 0; b < MAXR; b++) {
+      const int i = b * 64 * NW + tid;
+      if (i < n16) rec[i] = rv[b];
+    }
+  }
+  __syncthreads();
+  auto compute = [&](int g, const Raw(&raw)[SPW]) __attribute__((always_inline)) {
+    const int h0 = g * ROWS, nh = min(nh_all - h0, ROWS);
+#pragma unroll
+    for (int s = 0; s < SPW; s++) {
+      const int hr = wave + NW * s;
+      if (hr >= nh) continue;
+      const int K = sexp[h0 + hr] == a.E ? a.Is : a.I;
+      float p = 0.f;
+      if (c < K / 32) {
+        u32x4v v[REC];
+        load_record(rec + ((h0 + hr) * NC + c) * REC, v);
+        uint32_t xp[D::NX];
+        int xs[D::NS];
+        float dx;
+        unpack_record<D>(v, xp, xs, dx);
+        p = D::dot(raw[s], xp, xs, dx);
+      }
+      p = wave_sum<LPR>(p);
+      if (c == 0 && row < a.H) contrib[(h0 + hr) * RG + rg] = swt[h0 + hr] * p;
+    }
+  };
+  for (int g = 0; g < ng; g += 3) {
+    if (g + 2 < ng) issue(g + 2, rc);
+    compute(g, ra);
+    if (g + 1 >= ng) break;
+    if (g + 3 < ng) issue(g + 3, ra);
+    compute(g + 1, rb);
+    if (g + 2 >= ng) break;
+    if (g + 4 < ng) issue(g + 4, rb);
+    compute(g + 2, rc);
+  }
+  __syncthreads();
+  for (int i = tid; i < T * RG; i += 64 * NW) {
+    const int t = i / RG, r = i % RG;
+    if (n0 + r >= a.H) continue;
+    float y = 0.f;
+#pragma unroll 8
+    for (int hr = 0; hr < nh_all; hr++) y += contrib[hr * RG + r] * (stok[hr] == t ? 1.f : 0.f);
+    if (a.resid) {
+      uint16_t* px = a.resid + (int64_t)t * a.H + n0 + r;
+      *px = f32_to_bf16(bf16_to_f32(*px) + bf16_to_f32(f32_to_bf16(y)));
+    } else {
+      ((uint16_t*)a.y)[(int64_t)t * a.H + n0 + r] = f32_to_bf16(y);
+    }
+  }
+}
+
 // sum of the down kernel's per-group partials, in group order, for T tokens
 __global__ __launch_bounds__(256) void k_down_reduce(ExpertArgs a, int groups) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
@@ -966,7 +1092,17 @@ static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
   }
   // every row of h in one workgroup per RG output rows, pipelined over groups
   // (measured on MI355X at T = 4 and 8: faster than the grouped kernel + the
-  // partial-sum pass); the plan of all rows is read in one pass (3 rows <= 512)
+  // partial-sum pass, and than one workgroup per (slot, output rows) writing
+  // per-row results that a second pass sums per token: +4.0 / +2.9 us a layer
+  // at B = 4 / 8); up to DP3_ROWS rows of h with every record in LDS and the
+  // weights three groups deep, else the plan of all rows in one pass
+  // (3 rows <= 512) and records staged per group
+  if (a.T > 1 && nch == DP_K / 32 && nh_all <= DP3_ROWS) {
+    constexpr int LPR = DP_K / 32, RG = 64 / LPR;
+    const size_t lds = (size_t)nh_all * (DP_K / 32) * HX_XCV_WORDS * 4 + (size_t)nh_all * (3 + RG) * 4;
+    hipLaunchKernelGGL((k_down_pipe3<FMT, LPR, 8>), dim3((a.H + RG - 1) / RG), dim3(512), lds, s, a);
+    return hipGetLastError();
+  }
   if (a.T > 1 && nch == DP_K / 32 && 3 * nh_all <= 512) {
     constexpr int LPR = DP_K / 32, RG = 64 / LPR;
     const size_t lds = (size_t)2 * 24 * (DP_K / 32) * HX_XCV_WORDS * 4 + (size_t)nh_all * (3 + RG) * 4;
