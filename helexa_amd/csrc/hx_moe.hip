@@ -5,12 +5,17 @@
 // TpQwen3_5MoeBlock::{load, forward_fused, forward}
 // (crates/neuron/src/harness/tp/tp_qwen3_5.rs:1060-1275).
 //
-// Decode (T <= HX_DECODE_MAX_T, bf16 activations, GGUF experts) runs three
-// kernels: router logits + the shared expert's gate/up; the routed gate/up,
-// each workgroup re-deriving the (small) routing from the logits; down +
-// combine. Other decode cases route in a separate one-workgroup kernel.
-// Prefill runs router, per-token routing, dispatch, gate/up, down (weighted
-// rows) and combine.
+// Decode (T <= HX_DECODE_MAX_T, bf16 activations, GGUF experts; every expert
+// call takes the reference's quantised arm): one token runs three kernels --
+// router logits + the token's chunk records; routed + shared gate/up, each
+// workgroup re-deriving the (small) routing from the logits; down + combine,
+// which quantises the rows of h itself. Several tokens: router + records; one
+// workgroup routes the tokens and publishes the plan; gate/up per slot of the
+// plan (the shared expert's first); the records of the rows of h; down +
+// combine. Prefill runs router (which also writes the f16 tokens), per-token
+// routing (which also writes the Q8 operand of the quantised-arm tiles),
+// dispatch, gate/up, the quantisation of h for the quantised-arm tiles, down
+// (weighted rows) and combine.
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
