@@ -222,13 +222,16 @@ HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U
 
 // ----------------------------------------------------------------------------
 // K1: router logits (blocks [0, nrb)) and the tokens' chunk records (blocks
-// nrb.., one wave per token): the token row in the router's canonical layout
-// -- with the decoder RMSNorm applied by the same code as in the router waves
-// when it is fused (one token), so the normalised row is the same bits --
-// quantised to the vec_dot type of the expert weights (hx_quant.h).
+// nrb.., one workgroup per token, wave w quantising elements 512 w .. 512 w +
+// 511, whole Q8_0 / Q8_K blocks): the token row in the router's canonical
+// layout -- with the decoder RMSNorm applied by the same code as in the
+// router waves when it is fused, so the normalised row is the same bits --
+// quantised to the vec_dot type of the expert weights (hx_quant.h). (One
+// wave per token quantising the whole row was the kernel's last wave to
+// finish.)
 // ----------------------------------------------------------------------------
 template <int FMT, int NG>
-HX_DEV void x_records(const RouterArgs& r, const ExpertArgs& a, int t) {
+HX_DEV void x_records(const RouterArgs& r, const ExpertArgs& a, int t, int part) {
   const int lane = lane_id(), H = r.H;
   uint32_t xr[1][NG][4];
 #pragma unroll
@@ -240,6 +243,7 @@ HX_DEV void x_records(const RouterArgs& r, const ExpertArgs& a, int t) {
   uint32_t* rec = a.xcv + (int64_t)t * (H / 32) * HX_XCV_WORDS;
 #pragma unroll
   for (int i = 0; i < NG; i++) {
+    if (i != part) continue;   // wave-uniform: this wave's 512 elements (whole Q8_0 / Q8_K blocks)
     float x[8];
 #pragma unroll
     for (int q = 0; q < 4; q++) {
@@ -261,12 +265,14 @@ __global__ __launch_bounds__(256) void k_router_dec(RouterArgs r, ExpertArgs a, 
       router_rows<true, RBF, TT, RTE>(r, (blockIdx.x * 4 + wave) * RTE, 0);
     return;
   }
-  const int t = 4 * ((int)blockIdx.x - nrb) + wave;
-  if (t >= a.T) return;
+  // one workgroup per token: wave w quantises the token's elements 512 w ..
+  // 512 w + 511 (each wave holds the whole row for the RMSNorm's sum)
+  const int t = (int)blockIdx.x - nrb;
+  if (t >= a.T || wave >= (a.H >> 9)) return;
   switch (a.H >> 9) {   // groups of 8 per lane: H / 512 (H = 512, 1024, 2048)
-    case 1: x_records<FMT, 1>(r, a, t); break;
-    case 2: x_records<FMT, 2>(r, a, t); break;
-    default: x_records<FMT, 4>(r, a, t); break;
+    case 1: x_records<FMT, 1>(r, a, t, wave); break;
+    case 2: x_records<FMT, 2>(r, a, t, wave); break;
+    default: x_records<FMT, 4>(r, a, t, wave); break;
   }
 }
 
@@ -1027,11 +1033,11 @@ template <int FMT>
 static hipError_t router_dec_fmt(const RouterArgs& r, const ExpertArgs& a, bool rbf, hipStream_t s) {
   // Above 4 tokens (about 300 registers: one workgroup per CU) each wave
   // takes two router rows, so the grid fits the 256 CUs at once. The blocks
-  // after the router's quantise the tokens (one wave each).
+  // after the router's quantise the tokens (one workgroup each).
 #define RD(RB, TT)                                                                          \
   {                                                                                         \
     constexpr int RTE = TT > 4 ? 2 : 1;                                                     \
-    const int nrb = (r.E1 + 4 * RTE - 1) / (4 * RTE), ncb = (a.T + 3) / 4;                  \
+    const int nrb = (r.E1 + 4 * RTE - 1) / (4 * RTE), ncb = a.T;                            \
     hx_launch(k_router_dec<FMT, RB, TT>, dim3(nrb + ncb), dim3(256), 0, s, r, a, nrb);      \
   }
 #define RD_T(RB) { if (r.T <= 1) RD(RB, 1) else if (r.T <= 2) RD(RB, 2) else if (r.T <= 4) RD(RB, 4) else RD(RB, 8) }
