@@ -110,6 +110,52 @@ def test_rust_sys_crate_constants_and_structs_match_the_header():
         assert cfields == rfields, struct
 
 
+def _calls(text, prefix):
+    """(name, top-level argument count) of every prefix + name(...) call in text"""
+    out = []
+    for m in re.finditer(re.escape(prefix) + r"(\w+)\(", text):
+        depth, i, args, start = 1, m.end(), 0, m.end()
+        nonempty = False
+        while depth:
+            ch = text[i]
+            if ch in "([{":
+                depth += 1
+            elif ch in ")]}":
+                depth -= 1
+            elif ch == "," and depth == 1:
+                args += 1
+            if depth and not ch.isspace():
+                nonempty = True
+            i += 1
+        out.append((m.group(1), args + 1 if nonempty else 0))
+        del start
+    return out
+
+
+def test_neuron_module_calls_match_the_sys_crate():
+    """crates/hx-moe-neuron/hx_moe.rs (the drop-in block compiled inside
+    neuron) calls only functions the sys crate declares, each with the
+    declared number of arguments, uses only its constants, and fills every
+    field of the two #[repr(C)] structs"""
+    text = open(os.path.join(ROOT, "crates", "hx-moe-neuron", "hx_moe.rs")).read()
+    rlib = open(os.path.join(ROOT, "crates", "hx-moe-sys", "src", "lib.rs")).read()
+    decl = rust_functions()
+    calls = _calls(text, "sys::")
+    assert calls
+    for name, n in calls:
+        assert name in decl, name
+        assert n == len(decl[name][1]), (name, n, len(decl[name][1]))
+    consts = set(re.findall(r"pub const (HX_\w+):", rlib))
+    used = set(re.findall(r"sys::(HX_\w+)", text))
+    assert used and used <= consts, used - consts
+    for struct in ("hx_moe_config", "hx_moe_weights"):
+        rbody = re.search(r"pub struct %s \{(.*?)\n\}" % struct, rlib, re.S).group(1)
+        fields = re.findall(r"pub (\w+):", rbody)
+        lit = re.search(r"sys::%s \{(.*?)\n        \};" % struct, text, re.S).group(1)
+        set_fields = re.findall(r"(?<![:\w])(\w+):(?!:)", lit)   # field: value, not a::b paths
+        assert sorted(set_fields) == sorted(fields), struct
+
+
 def test_library_exports_every_declared_symbol():
     import ctypes
     from helexa_amd.moe import LIB_PATH
