@@ -83,7 +83,8 @@ __global__ __launch_bounds__(256) void k_xq_fq(ExpertArgs a, int nat) {
 // of M tile x of the dispatch list (or, for the shared expert's own launch,
 // of T), one row per wave; tiles of the f16 arm (m > 64) are skipped. (Placing
 // each tile's workgroups on the XCD of its gate/up and down workgroups was
-// measured slower: C3 15.5 -> 17.1 us.)
+// measured slower: C3 15.5 -> 17.1 us; so were four rows a wave with their
+// loads issued together, a quarter of the workgroups: C3 +4.1 us paired.)
 template <int FMT>
 __global__ __launch_bounds__(256) void k_hq_fq(ExpertArgs a) {
   const int tile = blockIdx.x, nt = blockIdx.y;
