@@ -651,11 +651,12 @@ __global__ __launch_bounds__(64 * NW) void k_down_dec(ExpertArgs a) {
 // of its rows' contributions in row order (slots by ascending expert, then the
 // shared expert), as the reference's combine order.
 // ----------------------------------------------------------------------------
-template <int FMT, int LPR, int OG>
-__global__ __launch_bounds__(256 * OG) void k_down_one(ExpertArgs a) {
+template <int FMT, int LPR, int OG, int WPG>
+__global__ __launch_bounds__(64 * WPG * OG) void k_down_one(ExpertArgs a) {
   using D = DChunk<FMT>;
   constexpr int RG = 64 / LPR, NG = LPR / 16;   // K = 32 LPR: groups of 8 per lane of a row
-  constexpr int NW = 4 * OG, ROWS = 12, SPW = 3, QS = (ROWS + NW - 1) / NW;
+  constexpr int NW = WPG * OG, ROWS = 12, SPW = ROWS / WPG, QS = (ROWS + NW - 1) / NW;
+  static_assert(ROWS % WPG == 0, "each wave of a group takes ROWS / WPG rows of h");
   constexpr int NO = RG * OG;   // output rows of the workgroup
   // LDS: chunk records [ROWS][LPR]; per row its token, weight and expert; the
   // contributions [ROWS][NO]
@@ -685,14 +686,14 @@ __global__ __launch_bounds__(256 * OG) void k_down_one(ExpertArgs a) {
     }
   }
   __syncthreads();
-  const int lane = lane_id(), og = w >> 2, wq = w & 3, rg = lane / LPR, c = lane % LPR;
+  const int lane = lane_id(), og = w / WPG, wq = w % WPG, rg = lane / LPR, c = lane % LPR;
   const int row = (blockIdx.x * OG + og) * RG + rg;
   // every weight load of the wave, unconditional (rows past the end, and
   // chunks past a shorter shared expert's K, read valid data that is dropped)
   typename D::Raw raw[SPW];
 #pragma unroll
   for (int s = 0; s < SPW; s++) {
-    const int hr = wq + 4 * s, hq = hr < nh ? hr : 0;
+    const int hr = wq + WPG * s, hq = hr < nh ? hr : 0;
     const int e = sexp[hq];
     const bool sh = e == a.E;
     const int K = sh ? a.Is : a.I;
@@ -705,7 +706,7 @@ __global__ __launch_bounds__(256 * OG) void k_down_one(ExpertArgs a) {
   __syncthreads();
 #pragma unroll
   for (int s = 0; s < SPW; s++) {
-    const int hr = wq + 4 * s;
+    const int hr = wq + WPG * s;
     if (hr >= nh) {   // every contribution slot is defined (zero past the rows of h)
       if (c == 0) contrib[hr * NO + og * RG + rg] = 0.f;
       continue;
@@ -741,6 +742,156 @@ __global__ __launch_bounds__(256 * OG) void k_down_one(ExpertArgs a) {
 }
 
 // ----------------------------------------------------------------------------
+// Q6_K down rows read two chunks a lane: chunks 2 p and 2 p + 1 of a row (the
+// same superblock half, l-blocks a and a + 1 with a even) share their scale
+// bytes and d, and their ql / qh pieces are adjacent, 16-byte aligned: one
+// lane loads both in five loads (ql 2 x 16 B, qh 16 B, the half's 8 scale
+// bytes, d) instead of ten.
+// ----------------------------------------------------------------------------
+struct Q6Pair {
+  uint4 l0, l1, h;
+  uint32_t sc, d;
+  HX_DEV static void load(const uint8_t* mat, int R, int K, int row, int p, Q6Pair& r) {
+    const int c = 2 * p, sb = c >> 3, cc = c & 7, n = cc >> 2, a = cc & 3;   // a even
+    const int o = sb * 128 + 64 * n + 8 * a;
+    const uint2 sc8 = *(const uint2*)q6k_sc(mat, R, K, row, sb * 16 + 8 * n);
+    r.l0 = *(const uint4*)q6k_ql(mat, R, K, row, o);
+    r.l1 = *(const uint4*)q6k_ql(mat, R, K, row, o + 32);
+    r.h = *(const uint4*)q6k_qh(mat, R, K, row, sb * 64 + 32 * n + 8 * a);
+    r.sc = __builtin_amdgcn_perm(sc8.y, sc8.x, 0x06040200u + 0x01010101u * (uint32_t)(a >> 1));
+    r.d = *((const uint16_t*)(mat + (int64_t)R * (K / 2 + K / 4 + K / 16)) + (int64_t)row * (K / 256) + sb);
+  }
+  // the two chunks as the one-chunk form DChunk<HX_Q6_K> takes
+  HX_DEV void split(Chunk<HX_Q6_K>::Raw& c0, Chunk<HX_Q6_K>::Raw& c1) const {
+    c0.l0 = make_uint2(l0.x, l0.y); c0.l1 = make_uint2(l1.x, l1.y); c0.h = make_uint2(h.x, h.y);
+    c1.l0 = make_uint2(l0.z, l0.w); c1.l1 = make_uint2(l1.z, l1.w); c1.h = make_uint2(h.z, h.w);
+    c0.sc = c1.sc = sc;
+    c0.d = c1.d = d;
+  }
+};
+
+// k_down_one for Q6_K down weights with K = 512, two chunks a lane (Q6Pair):
+// 8 lanes a row, the workgroup's 8 output rows in every wave, NW waves a
+// workgroup, wave w taking rows of h w, w + NW, .. (12 / NW of them) and
+// quantising the same rows; otherwise as k_down_one (each row of h quantised
+// once a workgroup into records in LDS; row-order sums per token, the lane's
+// two chunks added first)
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void k_down_one_q6p(ExpertArgs a) {
+  using D = DChunk<HX_Q6_K>;
+  constexpr int LPR = 8, RG = 8, NG = 1, ROWS = 12, SPW = ROWS / NW, QS = SPW, NC = 16;
+  extern __shared__ __attribute__((aligned(16))) uint16_t xl[];
+  uint32_t* srec = (uint32_t*)xl;
+  int* stok = (int*)(srec + ROWS * NC * HX_XCV_WORDS);
+  float* swt = (float*)(stok + ROWS);
+  int* sexp = (int*)(swt + ROWS);
+  float* contrib = (float*)(sexp + ROWS);
+  const int NH = a.F + 1;
+  const int nh = a.F + (a.Is > 0 ? 1 : 0);
+  const int w = threadIdx.x >> 6;
+  float hx[QS][NG][8];
+#pragma unroll
+  for (int s = 0; s < QS; s++)
+    h_row_load<NG>(a.hbuf + (int64_t)(w + NW * s < nh ? w + NW * s : 0) * a.hstride, hx[s]);
+  {
+    const int tok0 = 4 + 4 * a.max_slots;
+    const int i = threadIdx.x, part = i >> 5, r = i & 31;
+    if (i < 96) {
+      const int v = a.plan[tok0 + part * NH + min(r, nh - 1)];
+      int* dst = part == 0 ? stok : part == 1 ? (int*)swt : sexp;
+      if (r < nh) dst[r] = v;
+      else if (part == 0 && r < ROWS) dst[r] = -1;
+    }
+  }
+  __syncthreads();
+  const int lane = lane_id(), rg = lane / LPR, pc = lane % LPR;
+  const int row = blockIdx.x * RG + rg;
+  Q6Pair raw[SPW];
+#pragma unroll
+  for (int s = 0; s < SPW; s++) {
+    const int hr = w + NW * s, hq = hr < nh ? hr : 0;
+    const int e = sexp[hq];
+    const bool sh = e == a.E;
+    const int K = sh ? a.Is : a.I;
+    Q6Pair::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row < a.H ? row : 0, 2 * pc < K / 32 ? pc : 0, raw[s]);
+  }
+  __builtin_amdgcn_sched_barrier(0);   // the weight loads go out before the quantisation
+#pragma unroll
+  for (int s = 0; s < QS; s++)
+    if (w + NW * s < nh) h_regs_records<HX_Q6_K, NG>(hx[s], srec + (w + NW * s) * NC * HX_XCV_WORDS);
+  __syncthreads();
+#pragma unroll
+  for (int s = 0; s < SPW; s++) {
+    const int hr = w + NW * s;
+    if (hr >= nh) {
+      if (pc == 0) contrib[hr * RG + rg] = 0.f;
+      continue;
+    }
+    const int K = sexp[hr] == a.E ? a.Is : a.I;
+    float p = 0.f;
+    if (2 * pc < K / 32) {
+      Chunk<HX_Q6_K>::Raw c0, c1;
+      raw[s].split(c0, c1);
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        u32x4v v[HX_REC_VECS];
+        load_record((const lds_v4*)(srec + (hr * NC + 2 * pc + h) * HX_XCV_WORDS), v);
+        uint32_t xp[D::NX];
+        int xs[D::NS];
+        float dx;
+        unpack_record<D>(v, xp, xs, dx);
+        p += D::dot(h ? c1 : c0, xp, xs, dx);
+      }
+    }
+    p = wave_sum<LPR>(p);
+    if (pc == 0) contrib[hr * RG + rg] = swt[hr] * p;
+  }
+  __syncthreads();
+  const int i = threadIdx.x;
+  const int n = blockIdx.x * RG + i;
+  if (i < RG && n < a.H) {
+    float y = 0.f;
+#pragma unroll
+    for (int hr = 0; hr < ROWS; hr++) y += contrib[hr * RG + i] * (stok[hr] == 0 ? 1.f : 0.f);
+    if (a.resid) {
+      uint16_t* px = a.resid + n;
+      *px = f32_to_bf16(bf16_to_f32(*px) + bf16_to_f32(f32_to_bf16(y)));
+    } else {
+      ((uint16_t*)a.y)[n] = f32_to_bf16(y);
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------
+// The rows of h of each token as bit masks (row hr of token t: bit hr % 64 of
+// word hr / 64 of m[t]), built by ballots, wave w taking tokens w, w + waves;
+// and a token's sum of its rows' contributions (column r of RG) in row order
+// from them: the same additions as summing contrib * (token == t) over every
+// row, without the products by zero.
+// ----------------------------------------------------------------------------
+template <int NWORD>
+HX_DEV void token_row_masks(const int* stok, int nh, int T, unsigned long long (*m)[NWORD]) {
+  const int wave = threadIdx.x >> 6, lane = lane_id();
+  for (int t = wave; t < T; t += blockDim.x >> 6) {
+#pragma unroll
+    for (int q = 0; q < NWORD; q++) {
+      const int hr = 64 * q + lane;
+      const unsigned long long b = __ballot(hr < nh && stok[hr < nh ? hr : 0] == t);
+      if (lane == 0) m[t][q] = b;
+    }
+  }
+}
+template <int NWORD>
+HX_DEV float token_row_sum(const float* contrib, int RG, int r, const unsigned long long (&m)[NWORD]) {
+  float y = 0.f;
+#pragma unroll
+  for (int q = 0; q < NWORD; q++) {
+    for (unsigned long long b = m[q]; b; b &= b - 1) y += contrib[(64 * q + __builtin_ctzll(b)) * RG + r];
+  }
+  return y;
+}
+
+// ----------------------------------------------------------------------------
 // down + combine for T > 1 and K = 512, pipelined: workgroup = RG output rows
 // over every row of h, taken in groups of 24 (24 / NW per wave; NW = 8 keeps
 // the registers under 128, so 4 waves share each SIMD). The weights of
@@ -754,6 +905,11 @@ constexpr int DP_K = 512;
 // output groups of four waves per workgroup of k_down_one (measured on MI355X,
 // paired: 2 against 1 saves 1.1 us a layer at C2 and 1.3 at C4 B = 1; 4 less)
 constexpr int HX_DOWN_ONE_OG = 2;
+// waves per output group of k_down_one: 12 (one row of h a wave) measured no
+// faster for Q4_K and 0.3 us a layer slower at C2 (Q8_0), in groups of one or
+// two; k_down_one_q6p's single group of 12 waves is 1.1 us a layer faster at
+// C4 B = 1 than that kernel with 4 waves (and 6 no faster than 4)
+constexpr int HX_DOWN_ONE_WPG = 4, HX_DOWN_Q6P_NW = 12;
 template <int FMT, int LPR, int NW>
 __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe(ExpertArgs a) {
   using D = DChunk<FMT>;
@@ -791,6 +947,8 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe(ExpertArgs a) {
     }
   }
   __syncthreads();
+  __shared__ unsigned long long smask[HX_DECODE_MAX_T][3];   // nh_all <= 170
+  token_row_masks<3>(stok, nh_all, T, smask);   // read after the loop's last barrier
   const int lane = lane_id(), wave = threadIdx.x >> 6, rg = lane / LPR, c = lane % LPR;
   const int n0 = blockIdx.x * RG, row = n0 + rg;
   Raw ra[SPW], rb[SPW];
@@ -865,9 +1023,7 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe(ExpertArgs a) {
   for (int i = threadIdx.x; i < T * RG; i += 64 * NW) {
     const int t = i / RG, r = i % RG;
     if (n0 + r >= a.H) continue;
-    float y = 0.f;
-#pragma unroll 8
-    for (int hr = 0; hr < nh_all; hr++) y += contrib[hr * RG + r] * (stok[hr] == t ? 1.f : 0.f);
+    const float y = token_row_sum<3>(contrib, RG, r, smask[t]);
     if (a.resid) {
       uint16_t* px = a.resid + (int64_t)t * a.H + n0 + r;
       *px = f32_to_bf16(bf16_to_f32(*px) + bf16_to_f32(f32_to_bf16(y)));
@@ -888,6 +1044,7 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe(ExpertArgs a) {
 // prefetch would wait for it.)
 // ----------------------------------------------------------------------------
 constexpr int DP3_ROWS = 96;
+static_assert(DP3_ROWS <= 128, "two mask words a token");
 template <int FMT, int LPR, int NW>
 __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe3(ExpertArgs a) {
   using D = DChunk<FMT>;
@@ -929,6 +1086,8 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe3(ExpertArgs a) {
     }
   }
   __syncthreads();
+  __shared__ unsigned long long smask[HX_DECODE_MAX_T][2];   // nh_all <= DP3_ROWS <= 128
+  token_row_masks<2>(stok, nh_all, T, smask);   // read after the loop's last barrier
   const int lane = lane_id(), wave = tid >> 6, rg = lane / LPR, c = lane % LPR;
   const int n0 = blockIdx.x * RG, row = n0 + rg;
   Raw ra[SPW], rb[SPW], rc[SPW];
@@ -991,9 +1150,7 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe3(ExpertArgs a) {
   for (int i = tid; i < T * RG; i += 64 * NW) {
     const int t = i / RG, r = i % RG;
     if (n0 + r >= a.H) continue;
-    float y = 0.f;
-#pragma unroll 8
-    for (int hr = 0; hr < nh_all; hr++) y += contrib[hr * RG + r] * (stok[hr] == t ? 1.f : 0.f);
+    const float y = token_row_sum<2>(contrib, RG, r, smask[t]);
     if (a.resid) {
       uint16_t* px = a.resid + (int64_t)t * a.H + n0 + r;
       *px = f32_to_bf16(bf16_to_f32(*px) + bf16_to_f32(f32_to_bf16(y)));
@@ -1087,6 +1244,7 @@ static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
   const int nh_all = a.F + (a.Is > 0 ? a.T : 0);
   const int groups = down_groups(a.F, a.Is > 0 ? a.T : 0);
   if (a.hstride != K) return hipErrorInvalidValue;   // rows of h contiguous
+  if (a.T > HX_DECODE_MAX_T) return hipErrorInvalidValue;   // the per-token row masks
   // one token with at most 12 rows of h (k <= 11): the workgroup quantises the
   // rows of h itself; otherwise k_hrec writes their records first
   const bool qh = a.T == 1 && nh_all <= 12;
@@ -1118,9 +1276,12 @@ static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
 #define DD(LPR)                                                                                       \
   {                                                                                                   \
     constexpr int RG = 64 / LPR, OG = HX_DOWN_ONE_OG;                                                 \
-    if (qh) {                                                                                         \
+    if (qh && FMT == HX_Q6_K && LPR == 16) {                                                          \
+      const size_t lds = (size_t)12 * 16 * HX_XCV_WORDS * 4 + (size_t)12 * (3 + 8) * 4;               \
+      hx_launch(k_down_one_q6p<HX_DOWN_Q6P_NW>, dim3((a.H + 7) / 8), dim3(64 * HX_DOWN_Q6P_NW), (uint32_t)lds, s, a); \
+    } else if (qh) {                                                                                  \
       const size_t lds = (size_t)12 * LPR * HX_XCV_WORDS * 4 + (size_t)12 * (3 + RG * OG) * 4;        \
-      hx_launch(k_down_one<FMT, LPR, OG>, dim3((a.H + RG * OG - 1) / (RG * OG)), dim3(256 * OG), (uint32_t)lds, s, a); \
+      hx_launch(k_down_one<FMT, LPR, OG, HX_DOWN_ONE_WPG>, dim3((a.H + RG * OG - 1) / (RG * OG)), dim3(64 * HX_DOWN_ONE_WPG * OG), (uint32_t)lds, s, a); \
     } else {                                                                                          \
       const size_t lds = (size_t)HX_DOWN_ROWS * (3 + RG) * 4;                                         \
       hipLaunchKernelGGL((k_down_dec<FMT, LPR, 6, 4>), dim3((a.H + RG - 1) / RG, groups), dim3(256), lds, s, a); \
