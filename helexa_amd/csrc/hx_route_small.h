@@ -14,8 +14,12 @@ namespace hx {
 
 constexpr int HX_SMALL_F = HX_DECODE_MAX_T * HX_MAX_TOPK;
 
+constexpr int HX_SMALL_W = HX_MAX_EXPERTS / 64;   // expert-mask words
 struct alignas(16) RouteSmem {
-  unsigned long long ball[2];  // dispatch of up to 128 entries: each wave's slot starts
+  unsigned long long emask[HX_DECODE_MAX_T][HX_SMALL_W];   // token t's experts: bit e % 64 of word e / 64
+  unsigned long long wuni[HX_SMALL_W];   // the union over the tokens
+  int wpre[HX_SMALL_W];                  // entries in the words below, over the tokens
+  int upre[HX_SMALL_W];                  // distinct experts in the words below
   int idx[HX_SMALL_F];       // expert of flat entry f = t*k + j
   float w[HX_SMALL_F];       // routing weight of entry f
   int pos[HX_SMALL_F];       // permuted position of entry f
@@ -268,6 +272,10 @@ HX_DEV void route_token_lds_t(const float* lg, int E, int k, bool norm, bool wan
     sm.w[t * k + lane] = w;
   }
   if (lane == 0) sm.sgw[t] = want_sgw ? sigmoidf_(sg) : 0.0f;
+  // the token's expert mask: cleared, then one bit per selected expert (the
+  // wave's LDS operations take effect in program order)
+  if (lane < HX_SMALL_W) sm.emask[t][lane] = 0ull;
+  if (lane < k) atomicOr(&sm.emask[t][e >> 6], 1ull << (e & 63));
 }
 
 // One token in wave 0 of the workgroup, dispatch included: the k experts of a
@@ -326,127 +334,64 @@ HX_DEV void route_small_lds(const float* logits, int E1, int E, int k, bool norm
     return;
   }
   const int nw = blockDim.x >> 6, nt = blockDim.x;
-  if (tid == 0) sm.nroute = 0;
   for (int t = wave; t < T; t += nw) route_token_lds(logits + (int64_t)t * E1, E, k, norm, want_sgw, t, sm);
   __syncthreads();
-  if (F <= 128) {
-    // entry f in lane f % 64 of wave f / 64. Stable sort by key (expert, f):
-    // position = number of smaller keys, counted from the keys in LDS (4 per
-    // read, all reads independent). Then, in sorted order, a position starts a
-    // slot when its expert differs from the previous one: the slot index is the
-    // number of starts at or before it (ballot + mbcnt, plus wave 0's count for
-    // wave 1) and the slot ends at the next start.
-    const int F4 = (F + 3) & ~3;
-    if (tid < F4) sm.perm[tid] = tid < F ? (sm.idx[tid] << 7) | tid : 0x7fffffff;   // experts < 2^24
-    __syncthreads();
-    const int lane = lane_id(), f0 = 64 * wave + lane;
-    const bool mine = wave < 2 && f0 < F;
-    int pos = 0;
-    if (wave < 2) {
-      const int key = mine ? sm.perm[f0] : 0x7fffffff;
-      for (int j = 0; j < F4; j += 4) {
-        const int4 q = *(const int4*)(sm.perm + j);
-        pos += (q.x < key) + (q.y < key) + (q.z < key) + (q.w < key);
-      }
-    }
-    __syncthreads();   // every read of the keys precedes the writes below
-    if (mine) {
-      sm.pos[f0] = pos;
-      sm.perm[pos] = f0;
-    }
-    __syncthreads();
-    int f = 0, e = -1;
-    bool start = false;
-    if (mine) {   // sorted position f0
-      f = sm.perm[f0];
-      e = sm.idx[f];
-      start = f0 == 0 || e != sm.idx[sm.perm[f0 - 1]];
-    }
-    const unsigned long long sb = __ballot(start);
-    if (wave < 2 && lane == 0) sm.ball[wave] = sb;
-    __syncthreads();
-    if (wave < 2) {
-      const unsigned long long b0 = sm.ball[0], b1 = F > 64 ? sm.ball[1] : 0ull;
-      if (mine) sm.first[f] = start;
-      if (start) {
-        const int slot = (wave ? __popcll(b0) : 0) +
-                         (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(sb >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)sb, 0u));
-        const unsigned long long later = sb & ~((2ull << lane) - 1ull);
-        const int next = later ? 64 * wave + __ffsll((long long)later) - 1 : (wave == 0 && b1 ? 64 + __ffsll((long long)b1) - 1 : F);
-        sm.slots[3 * slot + 0] = e;
-        sm.slots[3 * slot + 1] = f0;
-        sm.slots[3 * slot + 2] = next - f0;
-      }
-      if (tid == 0) sm.nroute = __popcll(b0) + __popcll(b1);
-    }
-    __syncthreads();
-    return;
-  }
-  // stable sort by expert, one entry per thread: key = (expert, f), position =
-  // number of smaller keys; an entry opens a slot when no earlier entry has its
-  // expert; its slot is the number of distinct experts below it. Inner loops
-  // unrolled by 8 so the LDS reads of a thread are in flight together.
-  // (callers launch >= 256 threads, so a thread holds at most RPT entries)
-  constexpr int RPT = (HX_SMALL_F + 255) / 256;
-  for (int f = tid; f < F; f += nt) sm.perm[f] = (sm.idx[f] << 16) | f;   // keys (perm reused)
-  __syncthreads();
-  int my_pos[RPT], my_cnt[RPT];
-  bool my_first[RPT];
+  // dispatch from the tokens' expert masks (a token's k experts are distinct):
+  // entry f = (token t, expert e) goes to position pos = (entries with a
+  // smaller expert) + (tokens before t that also chose e) -- the stable sort
+  // by (expert, f); expert e's slot is the number of distinct experts below
+  // it, starting at the position of its first entry, with one row per token
+  // that chose it
+  static_assert(HX_SMALL_W <= 16, "the word scan runs in one row of 16 lanes");
+  if (wave == 0) {
+    // lane q < 16: word q's union and entry count, then exclusive prefix sums
+    // over the words (inclusive scans along row 0 by DPP row_shr)
+    const int q = tid, NWD = (E + 63) >> 6;
+    unsigned long long u = 0ull;
+    int c = 0;
 #pragma unroll
-  for (int r = 0; r < RPT; r++) {
-    const int f = tid + r * nt;
-    my_pos[r] = my_cnt[r] = 0;
-    my_first[r] = false;
-    if (f >= F) continue;
-    const int key = sm.perm[f], e = key >> 16;
-    int pos = 0, cnt = 0, before = 0;
-    int j = 0;
-    for (; j + 8 <= F; j += 8) {
-      int kj[8];
-#pragma unroll
-      for (int q = 0; q < 8; q++) kj[q] = sm.perm[j + q];
-#pragma unroll
-      for (int q = 0; q < 8; q++) {
-        pos += kj[q] < key;
-        const bool same = (kj[q] >> 16) == e;
-        cnt += same;
-        before += same && (j + q) < f;
-      }
+    for (int t = 0; t < HX_DECODE_MAX_T; t++) {
+      const unsigned long long m = q < NWD && t < T ? sm.emask[t][q] : 0ull;
+      u |= m;
+      c += __popcll(m);
     }
-    for (; j < F; j++) {
-      const int kj = sm.perm[j];
-      pos += kj < key;
-      const bool same = (kj >> 16) == e;
-      cnt += same;
-      before += same && j < f;
+    const int cu = __popcll(u);
+    int ic = c, iu = cu;
+#define HX_SCAN(CTRL)                                                       \
+    ic += __builtin_amdgcn_update_dpp(0, ic, CTRL, 0xf, 0xf, true);         \
+    iu += __builtin_amdgcn_update_dpp(0, iu, CTRL, 0xf, 0xf, true);
+    HX_SCAN(0x111) HX_SCAN(0x112) HX_SCAN(0x114) HX_SCAN(0x118)
+#undef HX_SCAN
+    if (q < HX_SMALL_W) {
+      sm.wuni[q] = u;
+      sm.wpre[q] = ic - c;
+      sm.upre[q] = iu - cu;
     }
-    my_pos[r] = pos;
-    my_cnt[r] = cnt;
-    my_first[r] = before == 0;
+    if (q == 15) sm.nroute = iu;
   }
   __syncthreads();
+  for (int f = tid; f < F; f += nt) {
+    const int t = f / k, e = sm.idx[f], wd = e >> 6, b = e & 63;
+    const unsigned long long below = (1ull << b) - 1ull;
+    int less = sm.wpre[wd], before = 0, cnt = 0;
+    const int slot = sm.upre[wd] + __popcll(sm.wuni[wd] & below);
 #pragma unroll
-  for (int r = 0; r < RPT; r++) {
-    const int f = tid + r * nt;
-    if (f < F) {
-      sm.pos[f] = my_pos[r];
-      sm.first[f] = my_first[r];
+    for (int u = 0; u < HX_DECODE_MAX_T; u++) {
+      const unsigned long long m = u < T ? sm.emask[u][wd] : 0ull;
+      const int bit = (int)((m >> b) & 1ull);
+      less += __popcll(m & below);
+      cnt += bit;
+      before += u < t ? bit : 0;
     }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int r = 0; r < RPT; r++) {
-    const int f = tid + r * nt;
-    if (f >= F) continue;
-    sm.perm[my_pos[r]] = f;
-    if (!my_first[r]) continue;
-    const int e = sm.idx[f];
-    int slot = 0;
-    for (int j = 0; j < F; j++) slot += sm.first[j] & (sm.idx[j] < e);
-    sm.slots[3 * slot + 0] = e;
-    sm.slots[3 * slot + 1] = my_pos[r];
-    sm.slots[3 * slot + 2] = my_cnt[r];
-    atomicAdd(&sm.nroute, 1);
+    const int pos = less + before;
+    sm.pos[f] = pos;
+    sm.perm[pos] = f;
+    sm.first[f] = before == 0;
+    if (before == 0) {
+      sm.slots[3 * slot + 0] = e;
+      sm.slots[3 * slot + 1] = pos;
+      sm.slots[3 * slot + 2] = cnt;
+    }
   }
   __syncthreads();
 }

@@ -178,7 +178,7 @@ def test_router_logits_bit_exact(router_case, T):
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
 
 
-@pytest.mark.parametrize("T", [1, 2, 8, 9, 64, 1000, 2048, 3000])
+@pytest.mark.parametrize("T", [1, 2, 4, 5, 8, 9, 64, 1000, 2048, 3000])
 def test_routing_and_dispatch_bit_exact(router_case, T):
     """Above 8 tokens the MFMA router splits K over 4 logit planes up to 1,984
     tokens and over 2 from there (2048, and the ragged 3000) at 512 experts; the
