@@ -178,8 +178,9 @@ HX_DEV void router_rows_u(const RouterArgs& a, int e0, int t0) {
 // workgroup instead of once per wave (the waves run one per SIMD, so the
 // repeated normalisation was serial VALU work on the kernel's critical path).
 // Same multiply-add order per logit as router_rows_u.
+// Tokens t0 .. t0 + TT - 1; writer: this workgroup writes the normalised rows.
 template <bool RBF, int TT, int TE, int NG>
-HX_DEV void router_rows_norm(const RouterArgs& a, int e0) {
+HX_DEV void router_rows_norm(const RouterArgs& a, int e0, int t0, bool writer) {
   constexpr int RW = RBF ? 4 : 8, TW = (TT + 3) / 4;
   __shared__ uint4 sxn[TT][NG][64];   // normalised rows, canonical layout
   const int lane = lane_id(), wave = threadIdx.x >> 6;
@@ -200,7 +201,7 @@ HX_DEV void router_rows_norm(const RouterArgs& a, int e0) {
     }
 #pragma unroll
     for (int s = 0; s < TW; s++) {
-      const int64_t tok = min(wave + 4 * s, a.T - 1);
+      const int64_t tok = min(t0 + wave + 4 * s, a.T - 1);
       const uint4 v = *(const uint4*)((const uint16_t*)a.x + tok * H + 8 * g);
       xr[s][i][0] = v.x; xr[s][i][1] = v.y; xr[s][i][2] = v.z; xr[s][i][3] = v.w;
     }
@@ -214,7 +215,7 @@ HX_DEV void router_rows_norm(const RouterArgs& a, int e0) {
     for (int i = 0; i < NG; i++)
 #pragma unroll
       for (int q = 0; q < 4; q++) one[0][i][q] = xr[s][i][q];
-    rmsnorm_regs<1, NG>(a, one, t, blockIdx.x == 0 && t < a.T);
+    rmsnorm_regs<1, NG>(a, one, t0 + t, writer && t0 + t < a.T);
 #pragma unroll
     for (int i = 0; i < NG; i++) sxn[t][i][lane] = make_uint4(one[0][i][0], one[0][i][1], one[0][i][2], one[0][i][3]);
   }
@@ -253,10 +254,10 @@ HX_DEV void router_rows_norm(const RouterArgs& a, int e0) {
     for (int j = 0; j < TE; j++) {
       float v = wave_sum<64>(acc[t][j]);
       const int e = e0 + j;
-      if (lane == t * TE + j && t < a.T && e < a.E1) {
+      if (lane == t * TE + j && t0 + t < a.T && e < a.E1) {
         v = bf16_to_f32(f32_to_bf16(v));
         if (a.bias && e < a.E) v = v + a.bias[e];
-        a.logits[(int64_t)t * a.E1 + e] = v;
+        a.logits[(int64_t)(t0 + t) * a.E1 + e] = v;
       }
     }
 }
