@@ -414,6 +414,22 @@ def test_forward_c2_decode_repeated_tokens(c2, pattern):
     assert rel_err(got, c2.ref(x_np(x))) <= TOL_BF16
 
 
+@pytest.mark.parametrize("T", [2, 8])
+def test_decode_tokens_isolated_from_an_overflowing_token(c2, T):
+    """a token whose activations are huge (1e38: its gate / up products and
+    down rows overflow to inf / NaN) leaves the other tokens' outputs finite
+    and bit for bit what they are beside an ordinary token: each token's
+    output sums its own rows only"""
+    x = c2.x(T, seed=31)
+    y0 = c2.block.forward(x).float().cpu().numpy()
+    xb = x.clone()
+    xb[T - 1] = 1e38
+    y1 = c2.block.forward(xb).float().cpu().numpy()
+    assert np.isfinite(y1[:T - 1]).all()
+    assert np.array_equal(y1[:T - 1].view(np.uint32), y0[:T - 1].view(np.uint32))
+    assert not np.isfinite(y1[T - 1]).all()   # the overflow did happen
+
+
 @pytest.mark.parametrize("T", [1, 4])
 def test_route_after_forward_publishes_everything(c2, T):
     """a decode forward writes only its plan into the handle's workspace; a
