@@ -47,6 +47,7 @@ Method
     graph of the 48 layers per B, 50 replays after 10 warm-up ones).
 
     python bench.py [--steps K] [--warmup W] [--layers L] [--no-cpu] [--no-prefill] [--no-c4] [--no-c5]
+    python bench.py --c4-only B      (one line: the C4 stack at batch B, for profiling)
 """
 from __future__ import annotations
 
@@ -604,6 +605,8 @@ def main():
     ap.add_argument("--c5-only", action="store_true", help="only the C5 skewed prefill line (for profiling)")
     ap.add_argument("--no-c4", action="store_true", help="skip the 48-layer stack line")
     ap.add_argument("--no-c5", action="store_true", help="skip the skewed 4096-token prefill line")
+    ap.add_argument("--c4-only", type=int, default=0, metavar="B",
+                    help="only the C4 stack line at batch B (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (expert parallelism would "
@@ -622,6 +625,9 @@ def main():
         return
     if args.c5_only:
         print(json.dumps(bench_c5()), flush=True)
+        return
+    if args.c4_only:
+        print(json.dumps(bench_c4(batches=(args.c4_only,))), flush=True)
         return
     out, blocks, host0, xs = bench_decode(args)
     log(f"[bench] decode {out['value']} us/layer; kernels {out['layer']['kernel_us']}")
