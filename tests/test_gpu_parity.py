@@ -622,13 +622,14 @@ def test_forward_skewed_routing_prefill(c2):
 # ------------------------------------------------------------------ C4 / C5 shapes
 def test_c4_stack_layers_q4_k_m():
     """Two Q4_K_M layers of the C4 stack (x <- x + moe(rmsnorm(x)), the (1 + w)
-    RMSNorm scaling with a per-channel weight, attention skipped) at B = 1, 4, 8:
-    each layer's output against the oracle applied to that layer's bf16 input."""
+    RMSNorm scaling with a per-channel weight, attention skipped) at B = 1, 3, 4,
+    7, 8 (an odd B leaves the router's last token pair one token): each layer's
+    output against the oracle applied to that layer's bf16 input."""
     _, synth = _hx()
     layers = [Case(synth.A3B, synth.FMT_Q4_K_M, 40 + i, O.BF16) for i in range(2)]
     w = torch.linspace(-0.5, 0.5, synth.A3B.hidden_size, device="cuda")   # per-channel norm weights
     wn = w.cpu().numpy()
-    for B in (1, 4, 8):
+    for B in (1, 3, 4, 7, 8):
         x = layers[0].x(B, seed=20 + B)
         for c in layers:
             xin = x_np(x)
