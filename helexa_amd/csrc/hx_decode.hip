@@ -1194,8 +1194,9 @@ static hipError_t router_dec_fmt(const RouterArgs& r, const ExpertArgs& a, bool 
   // workgroups after the previous pair's, so 8 tokens take 4 x 129 workgroups
   // (measured on MI355X, paired: 3.4 us a layer less at 8 tokens than 65
   // workgroups of two rows x 8 tokens a wave; pairs 0.4-0.6 us less than
-  // groups of 4 at 4 and 8 tokens). The blocks after the router's quantise
-  // the tokens (one workgroup each).
+  // groups of 4 at 4 and 8 tokens, and 0.3-1.3 us less than one token a
+  // group). The blocks after the router's quantise the tokens (one workgroup
+  // each).
 #define RD(RB, TT)                                                                          \
   {                                                                                         \
     const int nrb = (r.E1 + 3) / 4, ng = (a.T + TT - 1) / TT, ncb = a.T;                    \
