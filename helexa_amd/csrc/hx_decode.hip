@@ -671,6 +671,10 @@ __global__ __launch_bounds__(64 * WPG * OG) void k_down_one(ExpertArgs a) {
   const int NH = a.F + 1;
   const int nh = a.F + (a.Is > 0 ? 1 : 0);   // rows of h in use (<= ROWS)
   const int w = threadIdx.x >> 6;
+  // the residual this thread adds in the epilogue, loaded first (the
+  // epilogue then waits on no memory round trip)
+  const int n_out = blockIdx.x * NO + (int)threadIdx.x;
+  const uint16_t rx = a.resid && threadIdx.x < NO && n_out < a.H ? a.resid[n_out] : 0;
   float hx[QS][NG][8];
 #pragma unroll
   for (int s = 0; s < QS; s++)   // rows past the end read row 0 (not quantised)
@@ -735,8 +739,7 @@ __global__ __launch_bounds__(64 * WPG * OG) void k_down_one(ExpertArgs a) {
 #pragma unroll
     for (int hr = 0; hr < ROWS; hr++) y += contrib[hr * NO + i] * (stok[hr] == 0 ? 1.f : 0.f);
     if (a.resid) {
-      uint16_t* px = a.resid + n;
-      *px = f32_to_bf16(bf16_to_f32(*px) + bf16_to_f32(f32_to_bf16(y)));
+      a.resid[n] = f32_to_bf16(bf16_to_f32(rx) + bf16_to_f32(f32_to_bf16(y)));
     } else {
       ((uint16_t*)a.y)[n] = f32_to_bf16(y);
     }
@@ -791,6 +794,8 @@ __global__ __launch_bounds__(64 * NW) void k_down_one_q6p(ExpertArgs a) {
   const int NH = a.F + 1;
   const int nh = a.F + (a.Is > 0 ? 1 : 0);
   const int w = threadIdx.x >> 6;
+  const int n_out = blockIdx.x * RG + (int)threadIdx.x;   // the epilogue's residual, loaded first
+  const uint16_t rx = a.resid && threadIdx.x < RG && n_out < a.H ? a.resid[n_out] : 0;
   float hx[QS][NG][8];
 #pragma unroll
   for (int s = 0; s < QS; s++)
@@ -856,8 +861,7 @@ __global__ __launch_bounds__(64 * NW) void k_down_one_q6p(ExpertArgs a) {
 #pragma unroll
     for (int hr = 0; hr < ROWS; hr++) y += contrib[hr * RG + i] * (stok[hr] == 0 ? 1.f : 0.f);
     if (a.resid) {
-      uint16_t* px = a.resid + n;
-      *px = f32_to_bf16(bf16_to_f32(*px) + bf16_to_f32(f32_to_bf16(y)));
+      a.resid[n] = f32_to_bf16(bf16_to_f32(rx) + bf16_to_f32(f32_to_bf16(y)));
     } else {
       ((uint16_t*)a.y)[n] = f32_to_bf16(y);
     }
@@ -1066,6 +1070,12 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe3(ExpertArgs a) {
   int* sexp = (int*)(swt + nh_all);
   float* contrib = (float*)(sexp + nh_all);
   const int tid = threadIdx.x;
+  // thread t RG + r adds token t's residual at output row n0 + r in the
+  // epilogue; loaded first, so the epilogue waits on no memory round trip
+  static_assert(HX_DECODE_MAX_T * RG <= 64 * NW, "one epilogue output a thread");
+  const int n0 = blockIdx.x * RG;
+  const bool out_thread = tid < T * RG && n0 + tid % RG < a.H;
+  const uint16_t rx = a.resid && out_thread ? a.resid[(int64_t)(tid / RG) * a.H + n0 + tid % RG] : 0;
   u32x4v rv[MAXR];
   {
     // the plan's tokens, weights and experts of all rows (PL loads a thread),
@@ -1091,7 +1101,7 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe3(ExpertArgs a) {
   __shared__ unsigned long long smask[HX_DECODE_MAX_T][2];   // nh_all <= DP3_ROWS <= 128
   token_row_masks<2>(stok, nh_all, T, smask);   // read after the loop's last barrier
   const int lane = lane_id(), wave = tid >> 6, rg = lane / LPR, c = lane % LPR;
-  const int n0 = blockIdx.x * RG, row = n0 + rg;
+  const int row = n0 + rg;
   Raw ra[SPW], rb[SPW], rc[SPW];
   // the wave's SPW weight rows of group g (rows past the end read row 0 of
   // the group, dropped later)
@@ -1149,16 +1159,12 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe3(ExpertArgs a) {
     compute(g + 2, rc);
   }
   __syncthreads();
-  for (int i = tid; i < T * RG; i += 64 * NW) {
-    const int t = i / RG, r = i % RG;
-    if (n0 + r >= a.H) continue;
+  if (out_thread) {
+    const int t = tid / RG, r = tid % RG;
     const float y = token_row_sum<2>(contrib, RG, r, smask[t]);
-    if (a.resid) {
-      uint16_t* px = a.resid + (int64_t)t * a.H + n0 + r;
-      *px = f32_to_bf16(bf16_to_f32(*px) + bf16_to_f32(f32_to_bf16(y)));
-    } else {
-      ((uint16_t*)a.y)[(int64_t)t * a.H + n0 + r] = f32_to_bf16(y);
-    }
+    const int64_t o = (int64_t)t * a.H + n0 + r;
+    if (a.resid) a.resid[o] = f32_to_bf16(bf16_to_f32(rx) + bf16_to_f32(f32_to_bf16(y)));
+    else ((uint16_t*)a.y)[o] = f32_to_bf16(y);
   }
 }
 
