@@ -180,10 +180,12 @@ HX_DEV void load_plan(const ExpertArgs& a, int32_t* splan) {
 
 // NR (gate, up) row pairs of one expert for a list of tokens: the tokens'
 // chunk records come from a.xcv (written by the router kernel); h = silu(g) u
-// is stored as f32 for the down kernels' quantisation
-template <int FMT, int LPR, int NR>
-HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U, int rows, int row0, int count,
-                         const int* tok, const int* hrow) {
+// is stored as f32 for the down kernels' quantisation. tok_of(j) is token j of
+// the list (tok_of(0) known before any load); pre() issues whatever loads
+// tok_of(j > 0) reads, after the weight loads and before token 0's record.
+template <int FMT, int LPR, int NR, class TokF, class PreF>
+HX_DEV void gate_up_rows_f(const ExpertArgs& a, const uint8_t* G, const uint8_t* U, int rows, int row0, int count,
+                           TokF tok_of, PreF pre, const int* hrow) {
   using D = DChunk<FMT>;
   constexpr int RG = 64 / LPR;
   const int c = lane_id() % LPR, K = a.H;
@@ -194,20 +196,21 @@ HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U
     D::load(G, rows, K, row, c, rgt[g]);
     D::load(U, rows, K, row, c, rup[g]);
   }
+  pre();
   // token j's record is loaded before token j - 1's dot products (token 0's
   // together with the weights), so each load overlaps work
   u32x4v xr[HX_REC_VECS];
   auto xload = [&](int t) __attribute__((always_inline)) {
     load_record((const u32x4v*)(a.xcv + ((int64_t)t * (K / 32) + c) * HX_XCV_WORDS), xr);
   };
-  xload(tok[0]);
+  xload(tok_of(0));
   __builtin_amdgcn_sched_barrier(0);   // no weight arithmetic above these loads
   for (int j = 0; j < count; j++) {
     uint32_t xp[D::NX];
     int xs[D::NS];
     float dx;
     unpack_record<D>(xr, xp, xs, dx);
-    if (j + 1 < count) xload(tok[j + 1]);
+    if (j + 1 < count) xload(tok_of(j + 1));
 #pragma unroll
     for (int g = 0; g < NR; g++) {
       const int row = row0 + g * RG;
@@ -218,6 +221,11 @@ HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U
       if (c == 0 && row < rows) a.hbuf[(int64_t)hrow[j] * a.hstride + row] = siluf_(pg) * pu;
     }
   }
+}
+template <int FMT, int LPR, int NR>
+HX_DEV void gate_up_rows(const ExpertArgs& a, const uint8_t* G, const uint8_t* U, int rows, int row0, int count,
+                         const int* tok, const int* hrow) {
+  gate_up_rows_f<FMT, LPR, NR>(a, G, U, rows, row0, count, [&](int j) { return tok[j]; }, [] {}, hrow);
 }
 
 // ----------------------------------------------------------------------------
@@ -480,31 +488,38 @@ __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a
 template <int FMT, int LPR, int NR>
 __global__ __launch_bounds__(256) void k_gate_up_plan(ExpertArgs a) {
   constexpr int RG = 64 / LPR;
-  const int nslots = a.plan[0];
-  int u = blockIdx.y;
-  if (a.Is > 0) {
-    u = blockIdx.y == 0 ? nslots - 1 : (int)blockIdx.y - 1;
-    if (blockIdx.y > 0 && u >= nslots - 1) return;
-  } else if (u >= nslots) {
-    return;
+  // the shared expert's slot needs no plan: expert E, rows F .. F + T - 1 of
+  // h, row F + t for token t; a routed slot's record is read together with
+  // the slot count (one round trip before the weight loads, not two)
+  const bool sh = a.Is > 0 && blockIdx.y == 0;
+  int4 sr = make_int4(a.E, a.F, a.T, 0);   // expert, first row, rows, first row's token
+  if (!sh) {
+    const int u = (int)blockIdx.y - (a.Is > 0 ? 1 : 0);   // < max_slots - 1: a record of the plan
+    const int nslots = a.plan[0];
+    sr = *(const int4*)(a.plan + 4 + 4 * u);
+    if (u >= nslots - (a.Is > 0 ? 1 : 0)) return;
   }
-  const int4 sr = *(const int4*)(a.plan + 4 + 4 * u);   // expert, first row, rows, first row's token
   const int e = sr.x, start = sr.y, count = sr.z;
-  const bool sh = e == a.E;
   const int tok0 = 4 + 4 * a.max_slots;
-  int tok[HX_DECODE_MAX_T], hrow[HX_DECODE_MAX_T];
-  tok[0] = sr.w;
-  hrow[0] = start;
-  for (int j = 1; j < count; j++) {
-    hrow[j] = start + j;
-    tok[j] = a.plan[tok0 + start + j];
-  }
+  int hrow[HX_DECODE_MAX_T];
+  for (int j = 0; j < count; j++) hrow[j] = start + j;
   const int rows = sh ? a.Is : a.I;
   const int wave = threadIdx.x >> 6;
   const int row0 = (blockIdx.x * 4 + wave) * (RG * NR) + lane_id() / LPR;
+  // a routed slot's tokens after the first: one vector load (lane j holds
+  // token j), issued behind the weight loads, so neither waits for the other
+  // (a loop of dependent scalar loads here delayed the weight stream by a
+  // round trip per token)
+  int tl = 0;
+  auto tok_of = [&](int j) __attribute__((always_inline)) {
+    return sh ? j : j == 0 ? sr.w : __builtin_amdgcn_readlane(tl, j);
+  };
+  auto pre = [&]() __attribute__((always_inline)) {
+    if (!sh && count > 1) tl = a.plan[tok0 + start + min(lane_id(), count - 1)];
+  };
   if (row0 - lane_id() / LPR < rows)
-    gate_up_rows<FMT, LPR, NR>(a, sh ? a.sgate.base : a.gate.mat(e), sh ? a.sup.base : a.up.mat(e), rows, row0, count,
-                               tok, hrow);
+    gate_up_rows_f<FMT, LPR, NR>(a, sh ? a.sgate.base : a.gate.mat(e), sh ? a.sup.base : a.up.mat(e), rows, row0, count,
+                                 tok_of, pre, hrow);
 }
 
 // ----------------------------------------------------------------------------
