@@ -557,6 +557,15 @@ __global__ __launch_bounds__(256) void k_hrec(ExpertArgs a, int nrows) {
   h_row_records<FMT, NG>(a.hbuf + (int64_t)row * a.hstride, a.hrec + (int64_t)row * (16 * NG) * HX_XCV_WORDS);
 }
 
+// the residual element a down kernel loaded at its start, as f32 in its
+// epilogue: the empty asm keeps the conversion (and so the wait for the load)
+// from being hoisted up to the load
+HX_DEV float resid_f32(uint16_t rx) {
+  uint32_t v = rx;
+  asm volatile("" : "+v"(v));
+  return __uint_as_float(v << 16);
+}
+
 // ----------------------------------------------------------------------------
 // down + combine: block = RG output rows; the NW waves take the group's rows
 // of h SPW at a time (groups of ROWS = NW SPW rows, grid.y of them); each row's
@@ -688,8 +697,11 @@ __global__ __launch_bounds__(64 * WPG * OG) void k_down_one(ExpertArgs a) {
   const int w = threadIdx.x >> 6;
   // the residual this thread adds in the epilogue, loaded first (the
   // epilogue then waits on no memory round trip)
+  // (every thread loads an in-bounds element, so no lane-dependent branch
+  // makes the wave wait for the load where it is issued; only the epilogue's
+  // threads use theirs)
   const int n_out = blockIdx.x * NO + (int)threadIdx.x;
-  const uint16_t rx = a.resid && threadIdx.x < NO && n_out < a.H ? a.resid[n_out] : 0;
+  const uint16_t rx = a.resid ? a.resid[min(n_out, a.H - 1)] : 0;
   float hx[QS][NG][8];
 #pragma unroll
   for (int s = 0; s < QS; s++)   // rows past the end read row 0 (not quantised)
@@ -754,7 +766,7 @@ __global__ __launch_bounds__(64 * WPG * OG) void k_down_one(ExpertArgs a) {
 #pragma unroll
     for (int hr = 0; hr < ROWS; hr++) y += contrib[hr * NO + i] * (stok[hr] == 0 ? 1.f : 0.f);
     if (a.resid) {
-      a.resid[n] = f32_to_bf16(bf16_to_f32(rx) + bf16_to_f32(f32_to_bf16(y)));
+      a.resid[n] = f32_to_bf16(resid_f32(rx) + bf16_to_f32(f32_to_bf16(y)));
     } else {
       ((uint16_t*)a.y)[n] = f32_to_bf16(y);
     }
@@ -809,8 +821,10 @@ __global__ __launch_bounds__(64 * NW) void k_down_one_q6p(ExpertArgs a) {
   const int NH = a.F + 1;
   const int nh = a.F + (a.Is > 0 ? 1 : 0);
   const int w = threadIdx.x >> 6;
-  const int n_out = blockIdx.x * RG + (int)threadIdx.x;   // the epilogue's residual, loaded first
-  const uint16_t rx = a.resid && threadIdx.x < RG && n_out < a.H ? a.resid[n_out] : 0;
+  // the epilogue's residual, loaded first (an in-bounds element for every
+  // thread: no lane-dependent branch around the load)
+  const int n_out = blockIdx.x * RG + (int)threadIdx.x;
+  const uint16_t rx = a.resid ? a.resid[min(n_out, a.H - 1)] : 0;
   float hx[QS][NG][8];
 #pragma unroll
   for (int s = 0; s < QS; s++)
@@ -876,7 +890,7 @@ __global__ __launch_bounds__(64 * NW) void k_down_one_q6p(ExpertArgs a) {
 #pragma unroll
     for (int hr = 0; hr < ROWS; hr++) y += contrib[hr * RG + i] * (stok[hr] == 0 ? 1.f : 0.f);
     if (a.resid) {
-      a.resid[n] = f32_to_bf16(bf16_to_f32(rx) + bf16_to_f32(f32_to_bf16(y)));
+      a.resid[n] = f32_to_bf16(resid_f32(rx) + bf16_to_f32(f32_to_bf16(y)));
     } else {
       ((uint16_t*)a.y)[n] = f32_to_bf16(y);
     }
@@ -1085,12 +1099,17 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe3(ExpertArgs a) {
   int* sexp = (int*)(swt + nh_all);
   float* contrib = (float*)(sexp + nh_all);
   const int tid = threadIdx.x;
-  // thread t RG + r adds token t's residual at output row n0 + r in the
-  // epilogue; loaded first, so the epilogue waits on no memory round trip
-  static_assert(HX_DECODE_MAX_T * RG <= 64 * NW, "one epilogue output a thread");
+  // thread t RG + r (wave 0) adds token t's residual at output row n0 + r in
+  // the epilogue; wave 0 moves the dwords holding them into LDS first (an
+  // LDS-DMA: no register held across the loop, no wait until the epilogue)
+  static_assert(HX_DECODE_MAX_T * RG <= 64, "the epilogue's outputs in wave 0");
   const int n0 = blockIdx.x * RG;
   const bool out_thread = tid < T * RG && n0 + tid % RG < a.H;
-  const uint16_t rx = a.resid && out_thread ? a.resid[(int64_t)(tid / RG) * a.H + n0 + tid % RG] : 0;
+  uint32_t* const rsl = (uint32_t*)(contrib + nh_all * RG);   // 64 dwords
+  if (a.resid && tid < 64) {
+    const int64_t i = (int64_t)min(tid / RG, T - 1) * a.H + min(n0 + tid % RG, a.H - 1);   // H even
+    dma4(a.resid + (i & ~(int64_t)1), (uint32_t)(uintptr_t)(lds_u8*)rsl);
+  }
   u32x4v rv[MAXR];
   {
     // the plan's tokens, weights and experts of all rows (PL loads a thread),
@@ -1173,13 +1192,19 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe3(ExpertArgs a) {
     if (g + 4 < ng) issue(g + 4, rb);
     compute(g + 2, rc);
   }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // wave 0's residual DMA has landed
   __syncthreads();
   if (out_thread) {
     const int t = tid / RG, r = tid % RG;
     const float y = token_row_sum<2>(contrib, RG, r, smask[t]);
     const int64_t o = (int64_t)t * a.H + n0 + r;
-    if (a.resid) a.resid[o] = f32_to_bf16(bf16_to_f32(rx) + bf16_to_f32(f32_to_bf16(y)));
-    else ((uint16_t*)a.y)[o] = f32_to_bf16(y);
+    if (a.resid) {
+      const uint32_t w = rsl[tid];
+      const float rx = __uint_as_float((o & 1) ? (w & 0xffff0000u) : (w << 16));
+      a.resid[o] = f32_to_bf16(rx + bf16_to_f32(f32_to_bf16(y)));
+    } else {
+      ((uint16_t*)a.y)[o] = f32_to_bf16(y);
+    }
   }
 }
 
@@ -1289,7 +1314,7 @@ static hipError_t down_dec_fmt(const ExpertArgs& a, hipStream_t s) {
   // (3 rows <= 512) and records staged per group
   if (a.T > 1 && nch == DP_K / 32 && nh_all <= DP3_ROWS) {
     constexpr int LPR = DP_K / 32, RG = 64 / LPR;
-    const size_t lds = (size_t)nh_all * (DP_K / 32) * HX_XCV_WORDS * 4 + (size_t)nh_all * (3 + RG) * 4;
+    const size_t lds = (size_t)nh_all * (DP_K / 32) * HX_XCV_WORDS * 4 + (size_t)nh_all * (3 + RG) * 4 + 64 * 4;
     hipLaunchKernelGGL((k_down_pipe3<FMT, LPR, 8>), dim3((a.H + RG - 1) / RG), dim3(512), lds, s, a);
     return hipGetLastError();
   }

@@ -30,6 +30,12 @@ HX_DEV void dma16(const void* g, uint32_t lds_base) {
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
                : "=&s"(save) : "v"(g), "s"(lds_base) : "memory");
 }
+// global_load_lds_dword: lane l's 4 bytes at g land at LDS byte lds_base + 4 l
+HX_DEV void dma4(const void* g, uint32_t lds_base) {
+  uint32_t save;
+  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+               : "=&s"(save) : "v"(g), "s"(lds_base) : "memory");
+}
 
 // v_and_or_b32 with its two constants in registers (a VOP3 instruction on this
 // target takes no literal operand; left to itself the compiler splits the

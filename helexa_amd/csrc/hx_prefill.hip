@@ -641,11 +641,6 @@ constexpr int DQ_NST = 3;
 constexpr int DQ_K = 512;
 constexpr int DQ_NC = DQ_K / 64;
 
-HX_DEV void dma4(const void* g, uint32_t lds_base) {
-  uint32_t save;
-  asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
-               : "=&s"(save) : "v"(g), "s"(lds_base) : "memory");
-}
 
 // first K column of chunk c: 256 (c >> 2) + 128 ((c >> 1) & 1) + 32 (c & 1)
 HX_DEV int dq_col(int c) { return 256 * (c >> 2) + 128 * ((c >> 1) & 1) + 32 * (c & 1); }
