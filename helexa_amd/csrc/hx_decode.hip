@@ -172,6 +172,17 @@ HX_DEV void load_record(P src, u32x4v (&v)[HX_REC_VECS]) {
 }
 
 // the decode plan, pulled into LDS by the whole workgroup in one pass
+// the plan's first per-row word, 4 + 4 max_slots, taken from the kernel
+// arguments at the kernel's start, together with the others (left to itself
+// the compiler read max_slots only where the plan's rows are addressed: one
+// more scalar round trip ahead of the plan loads and the weight loads that
+// wait for them)
+HX_DEV int plan_rows_at(const ExpertArgs& a) {
+  int v = 4 + 4 * a.max_slots;
+  asm volatile("" : "+s"(v));
+  return v;
+}
+
 HX_DEV void load_plan(const ExpertArgs& a, int32_t* splan) {
   const int np = plan_ints(a.max_slots, a.F, a.T);
   for (int i = threadIdx.x; i < np; i += blockDim.x) splan[i] = a.plan[i];
@@ -692,6 +703,7 @@ __global__ __launch_bounds__(64 * WPG * OG) void k_down_one(ExpertArgs a) {
   float* swt = (float*)(stok + ROWS);
   int* sexp = (int*)(swt + ROWS);
   float* contrib = (float*)(sexp + ROWS);
+  const int tok0 = plan_rows_at(a);
   const int NH = a.F + 1;
   const int nh = a.F + (a.Is > 0 ? 1 : 0);   // rows of h in use (<= ROWS)
   const int w = threadIdx.x >> 6;
@@ -709,7 +721,6 @@ __global__ __launch_bounds__(64 * WPG * OG) void k_down_one(ExpertArgs a) {
   {
     // thread 32 part + r < 96 loads row r's token (part 0), weight (1) or
     // expert (2); rows r in [nh, ROWS) get token -1 (no token's row)
-    const int tok0 = 4 + 4 * a.max_slots;
     const int i = threadIdx.x, part = i >> 5, r = i & 31;
     if (i < 96) {
       const int v = a.plan[tok0 + part * NH + min(r, nh - 1)];
@@ -818,6 +829,7 @@ __global__ __launch_bounds__(64 * NW) void k_down_one_q6p(ExpertArgs a) {
   float* swt = (float*)(stok + ROWS);
   int* sexp = (int*)(swt + ROWS);
   float* contrib = (float*)(sexp + ROWS);
+  const int tok0 = plan_rows_at(a);
   const int NH = a.F + 1;
   const int nh = a.F + (a.Is > 0 ? 1 : 0);
   const int w = threadIdx.x >> 6;
@@ -830,7 +842,6 @@ __global__ __launch_bounds__(64 * NW) void k_down_one_q6p(ExpertArgs a) {
   for (int s = 0; s < QS; s++)
     h_row_load<NG>(a.hbuf + (int64_t)(w + NW * s < nh ? w + NW * s : 0) * a.hstride, hx[s]);
   {
-    const int tok0 = 4 + 4 * a.max_slots;
     const int i = threadIdx.x, part = i >> 5, r = i & 31;
     if (i < 96) {
       const int v = a.plan[tok0 + part * NH + min(r, nh - 1)];
@@ -1099,6 +1110,7 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe3(ExpertArgs a) {
   int* sexp = (int*)(swt + nh_all);
   float* contrib = (float*)(sexp + nh_all);
   const int tid = threadIdx.x;
+  const int tok0 = plan_rows_at(a);
   // thread t RG + r (wave 0) adds token t's residual at output row n0 + r in
   // the epilogue; wave 0 moves the dwords holding them into LDS first (an
   // LDS-DMA: no register held across the loop, no wait until the epilogue)
@@ -1116,13 +1128,14 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe3(ExpertArgs a) {
     // then the records (MAXR 16-byte pieces a thread), all issued before any
     // is stored; the plan's loads first, so storing them waits for them alone
     constexpr int PL = (3 * DP3_ROWS + 64 * NW - 1) / (64 * NW);
-    const int tok0 = 4 + 4 * a.max_slots, n3 = 3 * nh_all, n16 = nh_all * NC * REC;
+    const int n3 = 3 * nh_all, n16 = nh_all * NC * REC;
     int v[PL];
 #pragma unroll
     for (int b = 0; b < PL; b++) {
       const int i = min(b * 64 * NW + tid, n3 - 1), part = i / nh_all, r = i - part * nh_all;
       v[b] = a.plan[tok0 + part * NH + r];
     }
+    __builtin_amdgcn_sched_barrier(0);   // the plan's loads go out before the records'
 #pragma unroll
     for (int b = 0; b < MAXR; b++) rv[b] = ((const u32x4v*)a.hrec)[min(b * 64 * NW + tid, n16 - 1)];
 #pragma unroll
@@ -1131,27 +1144,41 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe3(ExpertArgs a) {
       if (i < n3) (part == 0 ? stok : part == 1 ? (int*)swt : sexp)[r] = v[b];
     }
   }
-  __syncthreads();
+  // the records stay in flight across this barrier: the weight loads behind
+  // it wait for the plan alone
+  lds_barrier();
   __shared__ unsigned long long smask[HX_DECODE_MAX_T][2];   // nh_all <= DP3_ROWS <= 128
-  token_row_masks<2>(stok, nh_all, T, smask);   // read after the loop's last barrier
   const int lane = lane_id(), wave = tid >> 6, rg = lane / LPR, c = lane % LPR;
   const int row = n0 + rg;
   Raw ra[SPW], rb[SPW], rc[SPW];
   // the wave's SPW weight rows of group g (rows past the end read row 0 of
   // the group, dropped later)
-  auto issue = [&](int g, Raw(&raw)[SPW]) __attribute__((always_inline)) {
+  // the experts of group g's rows (LDS reads), then their weight loads
+  auto experts = [&](int g, int (&ev)[SPW]) __attribute__((always_inline)) {
     const int h0 = g * ROWS, nh = min(nh_all - h0, ROWS);
 #pragma unroll
     for (int s = 0; s < SPW; s++) {
-      const int hr = wave + NW * s, hq = hr < nh ? hr : 0;
-      const int e = sexp[h0 + hq];
+      const int hr = wave + NW * s;
+      ev[s] = sexp[h0 + (hr < nh ? hr : 0)];
+    }
+  };
+  auto issue_e = [&](const int (&ev)[SPW], Raw(&raw)[SPW]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < SPW; s++) {
+      const int e = ev[s];
       const bool sh = e == a.E;
       const int K = sh ? a.Is : a.I;
       D::load(sh ? a.sdown.base : a.down.mat(e), a.H, K, row < a.H ? row : 0, c < K / 32 ? c : 0, raw[s]);
     }
   };
+  auto issue = [&](int g, Raw(&raw)[SPW]) __attribute__((always_inline)) {
+    int ev[SPW];
+    experts(g, ev);
+    issue_e(ev, raw);
+  };
   issue(0, ra);
   if (ng > 1) issue(1, rb);
+  token_row_masks<2>(stok, nh_all, T, smask);   // read after the loop's last barrier
   {
     const int n16 = nh_all * NC * REC;
 #pragma unroll
@@ -1160,7 +1187,7 @@ __global__ __launch_bounds__(64 * NW, 4) void k_down_pipe3(ExpertArgs a) {
       if (i < n16) rec[i] = rv[b];
     }
   }
-  __syncthreads();
+  lds_barrier();   // the first groups' weight loads stay in flight
   auto compute = [&](int g, const Raw(&raw)[SPW]) __attribute__((always_inline)) {
     const int h0 = g * ROWS, nh = min(nh_all - h0, ROWS);
 #pragma unroll

@@ -30,6 +30,14 @@ HX_DEV void dma16(const void* g, uint32_t lds_base) {
   asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
                : "=&s"(save) : "v"(g), "s"(lds_base) : "memory");
 }
+// a workgroup barrier that orders LDS accesses only: global loads still in
+// flight stay in flight across it (__syncthreads' fence waits for all of them)
+HX_DEV void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // global_load_lds_dword: lane l's 4 bytes at g land at LDS byte lds_base + 4 l
 HX_DEV void dma4(const void* g, uint32_t lds_base) {
   uint32_t save;
