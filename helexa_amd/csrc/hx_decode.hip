@@ -563,9 +563,15 @@ HX_DEV void h_row_records(const float* hrow, uint32_t* rec) {
 // the rows of h of a forward (routed, then the shared expert's) into a.hrec
 template <int FMT, int NG>
 __global__ __launch_bounds__(256) void k_hrec(ExpertArgs a, int nrows) {
+  // the kernel arguments all read in one round trip before the bound check
+  // (which otherwise split them in two, ahead of the row's loads)
+  const float* hb = a.hbuf;
+  uint32_t* hr = a.hrec;
+  int hs = a.hstride;
+  asm volatile("" : "+s"(hb), "+s"(hr), "+s"(hs));
   const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
   if (row >= nrows) return;
-  h_row_records<FMT, NG>(a.hbuf + (int64_t)row * a.hstride, a.hrec + (int64_t)row * (16 * NG) * HX_XCV_WORDS);
+  h_row_records<FMT, NG>(hb + (int64_t)row * hs, hr + (int64_t)row * (16 * NG) * HX_XCV_WORDS);
 }
 
 // the residual element a down kernel loaded at its start, as f32 in its
