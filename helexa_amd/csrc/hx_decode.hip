@@ -327,7 +327,7 @@ __global__ __launch_bounds__(256) void k_gate_up_dec(RouterArgs r, ExpertArgs a)
     }
   }
   if (publisher && blockIdx.x > 0) return;
-  route_small_lds(r.logits, r.E1, r.E, r.k, r.norm, publisher && r.has_shared, r.T, sm);
+  route_small_lds(r.logits, r.E1, r.E, r.k, r.norm, publisher && r.has_shared, r.T, sm, 256);
   if (publisher) {
     publish_route(r.d, r.topk_w, r.sgw, sm);
     return;

@@ -254,7 +254,7 @@ __global__ __launch_bounds__(256) void k_router88(RouterArgs a) {
 // token up to 8), published to global memory
 __global__ __launch_bounds__(512) void k_route_small(RouterArgs a) {
   __shared__ RouteSmem sm;
-  route_small_lds(a.logits, a.E1, a.E, a.k, a.norm, a.has_shared, a.T, sm);
+  route_small_lds(a.logits, a.E1, a.E, a.k, a.norm, a.has_shared, a.T, sm, route_small_threads(a.T));
   publish_route(a.d, a.topk_w, a.sgw, sm);
 }
 
@@ -286,7 +286,7 @@ void launch_router(const RouterArgs& a, bool xbf, bool rbf, hipStream_t s) {
 }
 
 void launch_route_small(const RouterArgs& a, hipStream_t s) {
-  hx_launch(k_route_small, dim3(1), dim3(a.T > 4 ? 512 : 256), 0, s, a);
+  hx_launch(k_route_small, dim3(1), dim3(route_small_threads(a.T)), 0, s, a);
 }
 
 void launch_route_tokens(const RouterArgs& a, hipStream_t s) {

@@ -260,9 +260,18 @@ HX_DEV void route_token_core_hook(float* v, int E, bool norm, int& out_e, float&
   out_w = norm ? my_p / tot : my_p;
 }
 
+// a value loaded early and used late: the empty asm keeps the compiler from
+// starting its arithmetic (and so waiting for its load) where it is loaded
+HX_DEV float sg_late(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
 template <int EPL>
 HX_DEV void route_token_lds_t(const float* lg, int E, int k, bool norm, bool want_sgw, int t, RouteSmem& sm) {
-  const float sg = want_sgw ? lg[E] : 0.0f;   // issued with the logits, used at the end
+  // the shared gate's logit, issued with the logits (no branch around the
+  // load) and used at the end (sg_late: its sigmoid is not started at the load)
+  const float sg = lg[want_sgw ? E : 0];
   int e;
   float w;
   route_token_core<EPL>(lg, E, k, norm, e, w);
@@ -271,7 +280,7 @@ HX_DEV void route_token_lds_t(const float* lg, int E, int k, bool norm, bool wan
     sm.idx[t * k + lane] = e;
     sm.w[t * k + lane] = w;
   }
-  if (lane == 0) sm.sgw[t] = want_sgw ? sigmoidf_(sg) : 0.0f;
+  if (lane == 0) sm.sgw[t] = want_sgw ? sigmoidf_(sg_late(sg)) : 0.0f;
   // the token's expert mask: cleared, then one bit per selected expert (the
   // wave's LDS operations take effect in program order)
   if (lane < HX_SMALL_W) sm.emask[t][lane] = 0ull;
@@ -283,7 +292,7 @@ HX_DEV void route_token_lds_t(const float* lg, int E, int k, bool norm, bool wan
 // entry starts its own slot, and slot = position.
 template <int EPL>
 HX_DEV void route_one_token(const float* lg, int E, int k, bool norm, bool want_sgw, RouteSmem& sm) {
-  const float sg = want_sgw ? lg[E] : 0.0f;
+  const float sg = lg[want_sgw ? E : 0];   // as in route_token_lds_t
   int e;
   float w;
   route_token_core<EPL>(lg, E, k, norm, e, w);
@@ -301,7 +310,7 @@ HX_DEV void route_one_token(const float* lg, int E, int k, bool norm, bool want_
     sm.slots[3 * pos + 2] = 1;
   }
   if (lane == 0) {
-    sm.sgw[0] = want_sgw ? sigmoidf_(sg) : 0.0f;
+    sm.sgw[0] = want_sgw ? sigmoidf_(sg_late(sg)) : 0.0f;
     sm.nroute = k;
   }
 }
@@ -322,10 +331,16 @@ HX_DEV void route_one_token_lds(const float* lg, int E, int k, bool norm, bool w
   else route_one_token<16>(lg, E, k, norm, want_sgw, sm);
 }
 
+// threads of the k_route_small workgroup for T tokens (one wave a token, at
+// least four waves)
+__host__ __device__ inline int route_small_threads(int T) { return T > 4 ? 512 : 256; }
+
 // Full routing of T tokens from logits [T][E1] into RouteSmem; ends with a
 // barrier. The shared-expert gate sigmoid is computed only when want_sgw.
+// nt: the workgroup's threads (blockDim.x), passed in: read from the
+// kernel's hidden arguments it cost a scalar round trip ahead of the logits
 HX_DEV void route_small_lds(const float* logits, int E1, int E, int k, bool norm, bool want_sgw, int T,
-                            RouteSmem& sm) {
+                            RouteSmem& sm, int nt) {
   const int tid = threadIdx.x, wave = tid >> 6;
   const int F = T * k;
   if (T == 1) {
@@ -333,7 +348,7 @@ HX_DEV void route_small_lds(const float* logits, int E1, int E, int k, bool norm
     __syncthreads();
     return;
   }
-  const int nw = blockDim.x >> 6, nt = blockDim.x;
+  const int nw = nt >> 6;
   for (int t = wave; t < T; t += nw) route_token_lds(logits + (int64_t)t * E1, E, k, norm, want_sgw, t, sm);
   __syncthreads();
   // dispatch from the tokens' expert masks (a token's k experts are distinct):
