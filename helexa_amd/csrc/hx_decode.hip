@@ -170,6 +170,14 @@ HX_DEV void load_record(P src, u32x4v (&v)[HX_REC_VECS]) {
 #pragma unroll
   for (int g = 0; g < HX_REC_VECS; g++) v[g] = src[g];
 }
+// keeps every word of a loaded record live up to this point: a word the
+// format does not read is otherwise free at once, and the compiler reused its
+// register right after the load, which made the wave wait for that load (and
+// for every load issued before it) on the spot
+HX_DEV void hold_record(u32x4v (&v)[HX_REC_VECS]) {
+#pragma unroll
+  for (int g = 0; g < HX_REC_VECS; g++) asm volatile("" : "+v"(v[g]));
+}
 
 // the decode plan, pulled into LDS by the whole workgroup in one pass
 // the plan's first per-row word, 4 + 4 max_slots, taken from the kernel
@@ -428,7 +436,12 @@ __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a
   // the logits first: a wait for them then leaves the later loads in flight
   float lv[EPL];
   route_logits_load<EPL>(r.logits, r.E, lv);
-  const float sg = r.has_shared ? r.logits[r.E] : 0.f;
+  // the shared gate's logit: a vector load (its index held in a VGPR) issued
+  // with the logits and counted with them, not a scalar load that the next
+  // wait for kernel arguments would wait for too; used only at publication
+  int sgi = r.has_shared ? r.E : 0;
+  asm volatile("" : "+v"(sgi));
+  const float sg = r.logits[sgi];
   u32x4v xr[HX_REC_VECS];
   load_record((const u32x4v*)(a.xcv + (int64_t)lane * HX_XCV_WORDS), xr);
   const bool shrow = a.Is > 0 && row < a.Is, rrow = row < a.I;
@@ -466,10 +479,11 @@ __global__ __launch_bounds__(256) void k_gate_up_dec1(RouterArgs r, ExpertArgs a
 #pragma unroll
   for (int j = 0; j < KR; j++) pos += __builtin_amdgcn_readlane(my_e, j) < my_e;
   if (blockIdx.x == 0 && wave == 0)
-    publish_one_token(r.d, r.topk_w, r.sgw, my_e, my_w, pos, r.has_shared ? sigmoidf_(sg) : 0.0f);
+    publish_one_token(r.d, r.topk_w, r.sgw, my_e, my_w, pos, r.has_shared ? sigmoidf_(sg_late(sg)) : 0.0f);
   uint32_t xp[D::NX];
   int xs[D::NS];
   float dx;
+  hold_record(xr);
   unpack_record<D>(xr, xp, xs, dx);
   float v[16];
 #pragma unroll
