@@ -734,22 +734,24 @@ __global__ __launch_bounds__(64 * WPG * OG) void k_down_one(ExpertArgs a) {
   // threads use theirs)
   const int n_out = blockIdx.x * NO + (int)threadIdx.x;
   const uint16_t rx = a.resid ? a.resid[min(n_out, a.H - 1)] : 0;
+  // the plan's words first (thread 32 part + r < 96 stores row r's token
+  // (part 0), weight (1) or expert (2); every thread loads an in-bounds word,
+  // so no branch surrounds the load): loads complete in order, so the wait
+  // for the plan, which the weight loads need, leaves the rows of h in flight
+  const int pi = threadIdx.x, part = min(pi >> 5, 2), pr = pi & 31;
+  const int pv = a.plan[tok0 + part * NH + min(pr, nh - 1)];
+  __builtin_amdgcn_sched_barrier(0);
   float hx[QS][NG][8];
 #pragma unroll
   for (int s = 0; s < QS; s++)   // rows past the end read row 0 (not quantised)
     h_row_load<NG>(a.hbuf + (int64_t)(w + NW * s < nh ? w + NW * s : 0) * a.hstride, hx[s]);
-  {
-    // thread 32 part + r < 96 loads row r's token (part 0), weight (1) or
-    // expert (2); rows r in [nh, ROWS) get token -1 (no token's row)
-    const int i = threadIdx.x, part = i >> 5, r = i & 31;
-    if (i < 96) {
-      const int v = a.plan[tok0 + part * NH + min(r, nh - 1)];
-      int* dst = part == 0 ? stok : part == 1 ? (int*)swt : sexp;
-      if (r < nh) dst[r] = v;
-      else if (part == 0 && r < ROWS) dst[r] = -1;
-    }
+  __builtin_amdgcn_sched_barrier(0);
+  if (pi < 96) {   // rows r in [nh, ROWS) get token -1 (no token's row)
+    int* dst = part == 0 ? stok : part == 1 ? (int*)swt : sexp;
+    if (pr < nh) dst[pr] = pv;
+    else if (part == 0 && pr < ROWS) dst[pr] = -1;
   }
-  __syncthreads();
+  lds_barrier();   // LDS only: the rows of h stay in flight
   const int lane = lane_id(), og = w / WPG, wq = w % WPG, rg = lane / LPR, c = lane % LPR;
   const int row = (blockIdx.x * OG + og) * RG + rg;
   // every weight load of the wave, unconditional (rows past the end, and
@@ -767,7 +769,7 @@ __global__ __launch_bounds__(64 * WPG * OG) void k_down_one(ExpertArgs a) {
 #pragma unroll
   for (int s = 0; s < QS; s++)
     if (w + NW * s < nh) h_regs_records<FMT, NG>(hx[s], srec + (w + NW * s) * LPR * HX_XCV_WORDS);
-  __syncthreads();
+  lds_barrier();   // LDS only: the weight loads stay in flight for the dot products
 #pragma unroll
   for (int s = 0; s < SPW; s++) {
     const int hr = wq + WPG * s;
@@ -857,20 +859,24 @@ __global__ __launch_bounds__(64 * NW) void k_down_one_q6p(ExpertArgs a) {
   // thread: no lane-dependent branch around the load)
   const int n_out = blockIdx.x * RG + (int)threadIdx.x;
   const uint16_t rx = a.resid ? a.resid[min(n_out, a.H - 1)] : 0;
+  // the plan's words first (thread 32 part + r < 96 stores row r's token
+  // (part 0), weight (1) or expert (2); every thread loads an in-bounds word,
+  // so no branch surrounds the load): loads complete in order, so the wait
+  // for the plan, which the weight loads need, leaves the rows of h in flight
+  const int pi = threadIdx.x, part = min(pi >> 5, 2), pr = pi & 31;
+  const int pv = a.plan[tok0 + part * NH + min(pr, nh - 1)];
+  __builtin_amdgcn_sched_barrier(0);
   float hx[QS][NG][8];
 #pragma unroll
   for (int s = 0; s < QS; s++)
     h_row_load<NG>(a.hbuf + (int64_t)(w + NW * s < nh ? w + NW * s : 0) * a.hstride, hx[s]);
-  {
-    const int i = threadIdx.x, part = i >> 5, r = i & 31;
-    if (i < 96) {
-      const int v = a.plan[tok0 + part * NH + min(r, nh - 1)];
-      int* dst = part == 0 ? stok : part == 1 ? (int*)swt : sexp;
-      if (r < nh) dst[r] = v;
-      else if (part == 0 && r < ROWS) dst[r] = -1;
-    }
+  __builtin_amdgcn_sched_barrier(0);
+  if (pi < 96) {   // rows r in [nh, ROWS) get token -1 (no token's row)
+    int* dst = part == 0 ? stok : part == 1 ? (int*)swt : sexp;
+    if (pr < nh) dst[pr] = pv;
+    else if (part == 0 && pr < ROWS) dst[pr] = -1;
   }
-  __syncthreads();
+  lds_barrier();   // LDS only: the rows of h stay in flight
   const int lane = lane_id(), rg = lane / LPR, pc = lane % LPR;
   const int row = blockIdx.x * RG + rg;
   Q6Pair raw[SPW];
@@ -886,7 +892,7 @@ __global__ __launch_bounds__(64 * NW) void k_down_one_q6p(ExpertArgs a) {
 #pragma unroll
   for (int s = 0; s < QS; s++)
     if (w + NW * s < nh) h_regs_records<HX_Q6_K, NG>(hx[s], srec + (w + NW * s) * NC * HX_XCV_WORDS);
-  __syncthreads();
+  lds_barrier();   // LDS only: the weight loads stay in flight for the dot products
 #pragma unroll
   for (int s = 0; s < SPW; s++) {
     const int hr = w + NW * s;
