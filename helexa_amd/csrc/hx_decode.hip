@@ -578,11 +578,13 @@ HX_DEV void h_row_records(const float* hrow, uint32_t* rec) {
 template <int FMT, int NG>
 __global__ __launch_bounds__(256) void k_hrec(ExpertArgs a, int nrows) {
   // the kernel arguments all read in one round trip before the bound check
-  // (which otherwise split them in two, ahead of the row's loads)
+  // (which otherwise split them in two, ahead of the row's loads); the asm
+  // only uses them (one that rewrote the pointers would hide their address
+  // space and turn the row's loads and stores into flat ones)
   const float* hb = a.hbuf;
   uint32_t* hr = a.hrec;
-  int hs = a.hstride;
-  asm volatile("" : "+s"(hb), "+s"(hr), "+s"(hs));
+  const int hs = a.hstride;
+  asm volatile("" ::"s"(hb), "s"(hr), "s"(hs));
   const int row = (int)blockIdx.x * 4 + (int)(threadIdx.x >> 6);
   if (row >= nrows) return;
   h_row_records<FMT, NG>(hb + (int64_t)row * hs, hr + (int64_t)row * (16 * NG) * HX_XCV_WORDS);
